@@ -1,0 +1,799 @@
+// C ABI of libinferno_hip.so: argument validation, host-side planning (the
+// reference dispatcher's routing and split plan), and kernel launches.
+// Declarations and the reference interface each entry point replaces are in
+// include/inferno_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/inferno_hip.h"
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+thread_local int32_t g_status = IFR_OK;
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  g_status = code;
+  return code;
+}
+
+int32_t ok() {
+  g_status = IFR_OK;
+  return IFR_OK;
+}
+
+int32_t hip_fail(hipError_t err, const char* what) {
+  return fail(IFR_EHIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+#define IFR_HIP(call, what)                        \
+  do {                                             \
+    hipError_t e_ = (call);                        \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+inline hipStream_t as_stream(uint64_t s) {
+  return reinterpret_cast<hipStream_t>(static_cast<uintptr_t>(s));
+}
+
+bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int64_t pow2_shift(int64_t value) {  // kernels/attention_ops.mojo:32-37
+  int64_t shift = 0;
+  while ((int64_t{1} << shift) < value) ++shift;
+  return shift;
+}
+
+// ---- reference planning helpers -------------------------------------------
+
+// worker_range (kernels/helpers.mojo:182-191).
+void worker_range(int64_t total, int64_t nw, int64_t w, int64_t* s, int64_t* e) {
+  const int64_t per = (total + nw - 1) / nw;
+  int64_t start = w * per;
+  int64_t end = std::min(start + per, total);
+  if (start >= total) start = end = total;
+  *s = start;
+  *e = end;
+}
+
+// recommended_workers (kernels/helpers.mojo:206-219) with DISPATCH_BW_PRODUCT
+// 2280 and PARALLEL_AMORTIZED_BYTES 1 MiB (kernels/dispatch_heuristics.mojo).
+int64_t recommended_workers(int64_t data_bytes, int64_t capacity) {
+  if (capacity <= 1) return capacity;
+  if (data_bytes >= 1024 * 1024) return capacity;
+  const int64_t target = data_bytes / 2280;
+  int64_t n = 1;
+  while ((n + 1) * (n + 1) <= target && n < capacity) ++n;
+  return n;
+}
+
+int64_t sliding_valid_len(int64_t pos, int64_t window) {
+  return pos + 1 >= window ? window : pos + 1;
+}
+
+// plan_run_splits (kernels/attention_ops.mojo:99-137).  The greedy step
+// gives the next split to the run with the largest kv/n (first index wins
+// ties); a max-heap keyed by that ratio and the index does the same in
+// O(cap log runs).
+void plan_run_splits(const std::vector<int64_t>& kv, int64_t cap,
+                     int64_t min_split, std::vector<int64_t>& n_splits,
+                     std::vector<int64_t>& split_base) {
+  const size_t R = kv.size();
+  n_splits.assign(R, 0);
+  split_base.assign(R, 0);
+  std::vector<int64_t> ceil_splits(R);
+  int64_t remaining = cap;
+  for (size_t i = 0; i < R; ++i) {
+    ceil_splits[i] = kv[i] > 0 ? (kv[i] + min_split - 1) / min_split : 0;
+    const int64_t seeded = (ceil_splits[i] > 0 && remaining > 0) ? 1 : 0;
+    remaining -= seeded;
+    n_splits[i] = seeded;
+  }
+  // heap entries: run index; ordering: larger kv/n first, then smaller index.
+  auto better = [&](size_t a, size_t b) {  // true if a has lower priority
+    const __int128 lhs = static_cast<__int128>(kv[b]) * n_splits[a];
+    const __int128 rhs = static_cast<__int128>(kv[a]) * n_splits[b];
+    if (lhs != rhs) return lhs > rhs;  // kv[b]/n[b] > kv[a]/n[a]
+    return a > b;
+  };
+  std::vector<size_t> heap;
+  for (size_t i = 0; i < R; ++i)
+    if (n_splits[i] > 0 && n_splits[i] < ceil_splits[i]) heap.push_back(i);
+  std::make_heap(heap.begin(), heap.end(), better);
+  while (remaining > 0 && !heap.empty()) {
+    std::pop_heap(heap.begin(), heap.end(), better);
+    const size_t best = heap.back();
+    heap.pop_back();
+    n_splits[best] += 1;
+    remaining -= 1;
+    if (n_splits[best] < ceil_splits[best]) {
+      heap.push_back(best);
+      std::push_heap(heap.begin(), heap.end(), better);
+    }
+  }
+  int64_t running = 0;
+  for (size_t i = 0; i < R; ++i) {
+    split_base[i] = running;
+    running += n_splits[i];
+  }
+}
+
+struct Geometry {
+  int64_t shift, row_mask, page_mask;
+};
+
+int64_t plan_words(int64_t num_runs, int64_t num_rows, int64_t seq_len,
+                   int64_t cap) {
+  const int64_t items = std::max<int64_t>({cap, seq_len, 1});
+  const int64_t units = std::max<int64_t>({seq_len, num_runs, 1});
+  return ifr::kHdrWords + 4 * num_runs + num_rows + std::max<int64_t>(seq_len, 1) +
+         ifr::kItemWords * items + ifr::kUnitWords * units;
+}
+
+// Validates a host run table against the cache geometry and the positions
+// the append and attention kernels will touch.
+int32_t check_runs(const int32_t* runs, int64_t num_runs,
+                   const int32_t* base_rows, int64_t num_rows, int64_t seq_len,
+                   int64_t kind, int64_t window, const Geometry& g,
+                   int64_t page_len, int64_t cache_rows) {
+  if (num_runs <= 0) return fail(IFR_EINVAL, "num_runs must be positive");
+  if (!runs || !base_rows) return fail(IFR_EINVAL, "null run table");
+  if (runs[0] != 0) return fail(IFR_EINVAL, "runs[0].buf_start must be 0");
+  for (int64_t i = 0; i < num_runs; ++i) {
+    const int64_t buf_start = runs[4 * i], base_pos = runs[4 * i + 1];
+    const int64_t rows_off = runs[4 * i + 2], page_count = runs[4 * i + 3];
+    const int64_t next = i + 1 < num_runs ? runs[4 * (i + 1)] : seq_len;
+    if (buf_start < 0 || next < buf_start || buf_start >= seq_len)
+      return fail(IFR_EINVAL, "run %lld: buf_start %lld out of order or range",
+                  (long long)i, (long long)buf_start);
+    if (base_pos < 0) return fail(IFR_EINVAL, "run %lld: negative base_pos", (long long)i);
+    if (rows_off < 0 || page_count < 0 || rows_off + page_count > num_rows)
+      return fail(IFR_EINVAL, "run %lld: rows [%lld, +%lld) outside base_rows[%lld]",
+                  (long long)i, (long long)rows_off, (long long)page_count,
+                  (long long)num_rows);
+    const int64_t n_tok = next - buf_start;
+    if (n_tok <= 0) continue;
+    const int64_t hi_pos = base_pos + n_tok - 1;
+    if (hi_pos > INT32_MAX / 2) return fail(IFR_EINVAL, "run %lld: position overflow", (long long)i);
+    int64_t lo_pos = 0;
+    if (kind == 0) lo_pos = std::max<int64_t>(0, base_pos - window + 1);
+    // Page ordinals the kernels index: (p >> shift) & page_mask, p in [lo, hi].
+    int64_t need;
+    if (g.page_mask < 0) {
+      need = (hi_pos >> g.shift) + 1;
+    } else if ((hi_pos >> g.shift) - (lo_pos >> g.shift) >= g.page_mask) {
+      need = g.page_mask + 1;
+    } else {
+      need = 0;
+      for (int64_t p = lo_pos >> g.shift; p <= (hi_pos >> g.shift); ++p)
+        need = std::max(need, (p & g.page_mask) + 1);
+    }
+    if (need > page_count)
+      return fail(IFR_EINVAL, "run %lld needs %lld pages, has %lld", (long long)i,
+                  (long long)need, (long long)page_count);
+    for (int64_t j = 0; j < need; ++j) {
+      const int64_t row = base_rows[rows_off + j];
+      if (row < 0 || row + page_len > cache_rows)
+        return fail(IFR_EINVAL, "run %lld page %lld: base row %lld outside cache of %lld rows",
+                    (long long)i, (long long)j, (long long)row, (long long)cache_rows);
+    }
+  }
+  return IFR_OK;
+}
+
+int32_t geometry(int64_t kind, int64_t cache_size, int64_t page_len,
+                 Geometry* g) {
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len %lld is not a power of two", (long long)page_len);
+  g->shift = pow2_shift(page_len);
+  g->row_mask = page_len - 1;
+  if (kind == 0) {
+    const int64_t ring = cache_size / page_len;
+    if (cache_size % page_len != 0 || !is_pow2(ring))
+      return fail(IFR_EINVAL, "cache_size/page_len must be a power of two");
+    g->page_mask = ring - 1;
+  } else if (kind == 1) {
+    g->page_mask = -1;
+  } else {
+    return fail(IFR_EINVAL, "kind must be 0 (sliding) or 1 (full)");
+  }
+  return IFR_OK;
+}
+
+// The reference dispatcher's routing (kernels/attention_dispatch_kernels.mojo:
+// 36-160 sliding, 163-299 full, degree 1) written into a plan image.
+int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
+                  int64_t num_runs, const int32_t* base_rows, int64_t num_rows,
+                  int64_t seq_len, int64_t kind, int64_t window,
+                  int64_t cache_size, int64_t page_len, int64_t cache_rows,
+                  int64_t cap, int64_t kv_row_bytes, int64_t* info) {
+  using namespace ifr;
+  if (!img || !info) return fail(IFR_EINVAL, "null image or info");
+  if (seq_len <= 0) return fail(IFR_EINVAL, "seq_len must be positive");
+  if (cap < 1) return fail(IFR_EINVAL, "cap must be >= 1");
+  if (kind == 0 && window <= 0) return fail(IFR_EINVAL, "window must be positive");
+  if (kv_row_bytes <= 0) return fail(IFR_EINVAL, "kv_row_bytes must be positive");
+  if (cache_rows <= 0) return fail(IFR_EINVAL, "cache_rows must be positive");
+  Geometry g;
+  int32_t st = geometry(kind, cache_size, page_len, &g);
+  if (st) return st;
+  st = check_runs(runs, num_runs, base_rows, num_rows, seq_len, kind, window, g,
+                  page_len, cache_rows);
+  if (st) return st;
+  const int64_t need = plan_words(num_runs, num_rows, seq_len, cap);
+  if (need > img_words)
+    return fail(IFR_ESPACE, "plan image needs %lld bytes, have %lld",
+                (long long)(need * 4), (long long)(img_words * 4));
+  if (need > INT32_MAX) return fail(IFR_EINVAL, "plan too large");
+
+  const bool sliding = kind == 0;
+  int32_t* hdr = img;
+  memset(hdr, 0, sizeof(int32_t) * kHdrWords);
+  int64_t off = kHdrWords;
+  hdr[kHdrOffRuns] = static_cast<int32_t>(off);
+  memcpy(img + off, runs, sizeof(int32_t) * 4 * num_runs);
+  off += 4 * num_runs;
+  hdr[kHdrOffRows] = static_cast<int32_t>(off);
+  memcpy(img + off, base_rows, sizeof(int32_t) * num_rows);
+  off += num_rows;
+  hdr[kHdrOffTokRun] = static_cast<int32_t>(off);
+  {
+    int64_t r = 0;
+    for (int64_t t = 0; t < seq_len; ++t) {
+      while (r + 1 < num_runs && t >= runs[4 * (r + 1)]) ++r;
+      img[off + t] = static_cast<int32_t>(r);
+    }
+  }
+  off += seq_len;
+  int32_t* items = img + off;
+  hdr[kHdrOffItems] = static_cast<int32_t>(off);
+  int64_t n_items = 0, n_units = 0, n_stripes = 0;
+  int32_t mode = IFR_PLAN_SPLIT_MERGE;
+  auto put_item = [&](int64_t q_row, int64_t run, int64_t start_pos,
+                      int64_t start, int64_t end, int64_t stripe) {
+    int32_t* it = items + n_items * kItemWords;
+    it[0] = static_cast<int32_t>(q_row);
+    it[1] = static_cast<int32_t>(run);
+    it[2] = static_cast<int32_t>(start_pos);
+    it[3] = static_cast<int32_t>(start);
+    it[4] = static_cast<int32_t>(end);
+    it[5] = static_cast<int32_t>(stripe);
+    it[6] = 0;
+    it[7] = 0;
+    ++n_items;
+  };
+  std::vector<int64_t> unit_buf;  // out_row, stripe_base, n_stripes
+
+  if (seq_len == 1) {
+    const int64_t base_pos = runs[1];
+    const int64_t valid = sliding ? sliding_valid_len(base_pos, window) : base_pos + 1;
+    if (valid > 0) {
+      const int64_t start_pos = sliding ? base_pos - valid + 1 : 0;
+      int64_t nw = recommended_workers(valid * kv_row_bytes, cap);
+      if (nw <= 0) nw = cap;
+      nw = std::min(std::min(nw, cap), valid);
+      for (int64_t w = 0; w < nw; ++w) {
+        int64_t s, e;
+        worker_range(valid, nw, w, &s, &e);
+        put_item(0, 0, start_pos, s, e, w);
+      }
+      unit_buf.insert(unit_buf.end(), {0, 0, nw});
+      n_stripes = nw;
+    }
+  } else if (num_runs == seq_len && num_runs > 1 && num_runs < cap) {
+    std::vector<int64_t> kv(num_runs), ns, sb;
+    for (int64_t i = 0; i < num_runs; ++i) {
+      const int64_t p = runs[4 * i + 1];
+      kv[i] = sliding ? sliding_valid_len(p, window) : p + 1;
+    }
+    plan_run_splits(kv, cap, ifr::kTile, ns, sb);
+    for (int64_t i = 0; i < num_runs; ++i) {
+      const int64_t start_pos = sliding ? runs[4 * i + 1] - kv[i] + 1 : 0;
+      for (int64_t s = 0; s < ns[i]; ++s) {
+        int64_t a, b;
+        worker_range(kv[i], ns[i], s, &a, &b);
+        put_item(runs[4 * i], i, start_pos, a, b, sb[i] + s);
+      }
+      unit_buf.insert(unit_buf.end(), {runs[4 * i], sb[i], ns[i]});
+      n_stripes += ns[i];
+    }
+  } else {
+    // Token-partitioned prefill kernels (kernels/flash_attention_prefill.mojo).
+    mode = sliding ? IFR_PLAN_TOKEN_DIRECT : IFR_PLAN_TOKEN_MERGE;
+    int64_t r = 0;
+    for (int64_t t = 0; t < seq_len; ++t) {
+      while (r + 1 < num_runs && t >= runs[4 * (r + 1)]) ++r;
+      const int64_t abs_pos = runs[4 * r + 1] + (t - runs[4 * r]);
+      int64_t lo = 0, hi = abs_pos + 1;
+      if (sliding) lo = std::max<int64_t>(0, abs_pos - window + 1);
+      put_item(t, r, 0, lo, hi, t);
+      unit_buf.insert(unit_buf.end(), {t, t, 1});
+    }
+    n_stripes = seq_len;
+  }
+  off += n_items * kItemWords;
+  hdr[kHdrOffUnits] = static_cast<int32_t>(off);
+  n_units = static_cast<int64_t>(unit_buf.size() / 3);
+  for (int64_t u = 0; u < n_units; ++u) {
+    int32_t* un = img + off + u * kUnitWords;
+    un[0] = static_cast<int32_t>(unit_buf[3 * u]);
+    un[1] = static_cast<int32_t>(unit_buf[3 * u + 1]);
+    un[2] = static_cast<int32_t>(unit_buf[3 * u + 2]);
+    un[3] = 0;
+  }
+  off += n_units * kUnitWords;
+  hdr[kHdrMagic] = kPlanMagic;
+  hdr[kHdrNumRuns] = static_cast<int32_t>(num_runs);
+  hdr[kHdrNumRows] = static_cast<int32_t>(num_rows);
+  hdr[kHdrSeqLen] = static_cast<int32_t>(seq_len);
+  hdr[kHdrNumItems] = static_cast<int32_t>(n_items);
+  hdr[kHdrNumUnits] = static_cast<int32_t>(n_units);
+  hdr[kHdrMode] = mode;
+  hdr[kHdrNumStripes] = static_cast<int32_t>(n_stripes);
+  hdr[kHdrTotalWords] = static_cast<int32_t>(off);
+  info[0] = n_items;
+  info[1] = n_units;
+  info[2] = mode;
+  info[3] = n_stripes;
+  info[4] = off * 4;
+  info[5] = seq_len;
+  info[6] = num_runs;
+  info[7] = g.shift;
+  info[8] = g.row_mask;
+  info[9] = g.page_mask;
+  info[10] = cache_rows;
+  info[11] = kind;
+  info[12] = window;
+  info[13] = info[14] = info[15] = 0;
+  return ok();
+}
+
+int32_t check_info(const int64_t* info) {
+  if (!info) return fail(IFR_EINVAL, "null info");
+  if (info[0] < 0 || info[1] < 0 || info[0] > INT32_MAX || info[1] > INT32_MAX ||
+      info[2] < 0 || info[2] > 2 || info[5] <= 0 || info[7] < 0 || info[7] > 30)
+    return fail(IFR_EINVAL, "info does not describe a plan");
+  return IFR_OK;
+}
+
+// The kernels index the cache with the geometry the plan was validated for;
+// any other geometry could reach rows outside the cache.
+int32_t check_geometry(const int64_t* info, int64_t shift, int64_t row_mask,
+                       int64_t page_mask) {
+  if (shift != info[7] || row_mask != info[8] || page_mask != info[9])
+    return fail(IFR_EINVAL,
+                "page geometry (shift %lld, row_mask %lld, page_mask %lld) differs from the "
+                "plan's (%lld, %lld, %lld)",
+                (long long)shift, (long long)row_mask, (long long)page_mask,
+                (long long)info[7], (long long)info[8], (long long)info[9]);
+  return IFR_OK;
+}
+
+int32_t check_attention_shapes(int64_t num_q, int64_t num_kv, int64_t head_dim,
+                               int64_t partial_stride, int64_t kv_stride,
+                               int64_t elt_bytes) {
+  if (num_q <= 0 || num_kv <= 0 || num_q % num_kv != 0)
+    return fail(IFR_EINVAL, "num_q must be a positive multiple of num_kv");
+  if (num_q > 64) return fail(IFR_EUNSUPPORTED, "num_q > 64");
+  if (!ifr::attention_shape_supported(static_cast<int>(head_dim),
+                                      static_cast<int>(num_q / num_kv)))
+    return fail(IFR_EUNSUPPORTED, "head_dim %lld with gqa %lld is not compiled",
+                (long long)head_dim, (long long)(num_q / num_kv));
+  if (kv_stride < num_kv * head_dim || (kv_stride * elt_bytes) % 16 != 0)
+    return fail(IFR_EINVAL, "kv_stride must cover num_kv*head_dim and keep rows 16-byte aligned");
+  if (partial_stride < num_q * head_dim + 2 * num_q || partial_stride % 4 != 0)
+    return fail(IFR_EINVAL, "partial_stride too small or not a multiple of 4");
+  return IFR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t ifr_abi_version(void) { return IFR_ABI_VERSION; }
+
+int32_t ifr_last_error(char* buf, int64_t len) {
+  if (buf && len > 0) {
+    const size_t n = std::min<size_t>(static_cast<size_t>(len - 1), g_error.size());
+    memcpy(buf, g_error.data(), n);
+    buf[n] = '\0';
+  }
+  return g_status;
+}
+
+int32_t ifr_device_count(int64_t* out) {
+  if (!out) return fail(IFR_EINVAL, "null out");
+  int n = 0;
+  IFR_HIP(hipGetDeviceCount(&n), "hipGetDeviceCount");
+  *out = n;
+  return ok();
+}
+
+int32_t ifr_set_device(int64_t device) {
+  IFR_HIP(hipSetDevice(static_cast<int>(device)), "hipSetDevice");
+  return ok();
+}
+
+int32_t ifr_malloc(void** out, int64_t bytes) {
+  if (!out || bytes <= 0) return fail(IFR_EINVAL, "bad malloc arguments");
+  IFR_HIP(hipMalloc(out, static_cast<size_t>(bytes)), "hipMalloc");
+  return ok();
+}
+
+int32_t ifr_free(void* ptr) {
+  IFR_HIP(hipFree(ptr), "hipFree");
+  return ok();
+}
+
+int32_t ifr_host_alloc(void** out, int64_t bytes) {
+  if (!out || bytes <= 0) return fail(IFR_EINVAL, "bad host alloc arguments");
+  IFR_HIP(hipHostMalloc(out, static_cast<size_t>(bytes), hipHostMallocDefault),
+          "hipHostMalloc");
+  return ok();
+}
+
+int32_t ifr_host_free(void* ptr) {
+  IFR_HIP(hipHostFree(ptr), "hipHostFree");
+  return ok();
+}
+
+int32_t ifr_memcpy_h2d(void* dst, const void* src, int64_t bytes, uint64_t stream) {
+  if (bytes < 0) return fail(IFR_EINVAL, "negative size");
+  if (bytes == 0) return ok();
+  IFR_HIP(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyHostToDevice,
+                         as_stream(stream)), "hipMemcpyAsync H2D");
+  return ok();
+}
+
+int32_t ifr_memcpy_d2h(void* dst, const void* src, int64_t bytes, uint64_t stream) {
+  if (bytes < 0) return fail(IFR_EINVAL, "negative size");
+  if (bytes == 0) return ok();
+  IFR_HIP(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToHost,
+                         as_stream(stream)), "hipMemcpyAsync D2H");
+  return ok();
+}
+
+int32_t ifr_memcpy_d2d(void* dst, const void* src, int64_t bytes, uint64_t stream) {
+  if (bytes < 0) return fail(IFR_EINVAL, "negative size");
+  if (bytes == 0) return ok();
+  IFR_HIP(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToDevice,
+                         as_stream(stream)), "hipMemcpyAsync D2D");
+  return ok();
+}
+
+int32_t ifr_memset(void* dst, int32_t value, int64_t bytes, uint64_t stream) {
+  if (bytes < 0) return fail(IFR_EINVAL, "negative size");
+  if (bytes == 0) return ok();
+  IFR_HIP(hipMemsetAsync(dst, value, static_cast<size_t>(bytes), as_stream(stream)),
+          "hipMemsetAsync");
+  return ok();
+}
+
+int32_t ifr_stream_create(uint64_t* out) {
+  if (!out) return fail(IFR_EINVAL, "null out");
+  hipStream_t s;
+  IFR_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  *out = static_cast<uint64_t>(reinterpret_cast<uintptr_t>(s));
+  return ok();
+}
+
+int32_t ifr_stream_destroy(uint64_t stream) {
+  IFR_HIP(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+  return ok();
+}
+
+int32_t ifr_stream_sync(uint64_t stream) {
+  IFR_HIP(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+  return ok();
+}
+
+int32_t ifr_fill_normal_bf16(void* dst, int64_t n, uint64_t seed,
+                             int64_t outlier_every, float outlier_scale,
+                             uint64_t stream) {
+  if (n < 0 || (n > 0 && !dst)) return fail(IFR_EINVAL, "bad fill arguments");
+  IFR_HIP(ifr::launch_fill_normal_bf16(dst, n, seed, outlier_every, outlier_scale,
+                                       as_stream(stream)), "fill_normal_bf16");
+  return ok();
+}
+
+int64_t ifr_flash_partial_stride(int64_t num_q, int64_t head_dim) {
+  return ((num_q * head_dim + 2 * num_q) * 4 + 63) / 64 * 16;
+}
+
+int64_t ifr_plan_bytes(int64_t num_runs, int64_t num_rows, int64_t seq_len,
+                       int64_t cap) {
+  if (num_runs < 0 || num_rows < 0 || seq_len < 0 || cap < 0) return -1;
+  return 4 * plan_words(num_runs, num_rows, seq_len, cap);
+}
+
+int32_t ifr_plan_attention(void* image, int64_t image_bytes,
+                           const int32_t* runs, int64_t num_runs,
+                           const int32_t* base_rows, int64_t num_rows,
+                           int64_t seq_len, int64_t kind, int64_t window,
+                           int64_t cache_size, int64_t page_len,
+                           int64_t cache_rows, int64_t cap,
+                           int64_t kv_row_bytes, int64_t* info) {
+  return plan_impl(static_cast<int32_t*>(image), image_bytes / 4, runs,
+                   num_runs, base_rows, num_rows, seq_len, kind, window,
+                   cache_size, page_len, cache_rows, cap, kv_row_bytes, info);
+}
+
+int32_t ifr_rope_cache_write(const void* image_dev, const int64_t* info,
+                             void* q, const void* k_src, const void* v_src,
+                             void* k_cache, void* v_cache,
+                             const float* cos_table, const float* sin_table,
+                             int64_t num_q, int64_t num_kv,
+                             int64_t page_shift, int64_t row_mask,
+                             int64_t page_mask, int64_t seq_len, int64_t half,
+                             int64_t pair_stride, int64_t head_dim,
+                             uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (seq_len != info[5]) return fail(IFR_EINVAL, "seq_len differs from the plan");
+  if (!image_dev || !q || !k_src || !v_src || !k_cache || !v_cache || !cos_table || !sin_table)
+    return fail(IFR_EINVAL, "null pointer");
+  if (num_q <= 0 || num_kv <= 0 || head_dim <= 0 || half <= 0 || half > pair_stride ||
+      pair_stride + half > head_dim)
+    return fail(IFR_EINVAL, "bad rope geometry");
+  st = check_geometry(info, page_shift, row_mask, page_mask);
+  if (st) return st;
+  ifr::PagedGeom g{static_cast<int>(page_shift), static_cast<int>(row_mask),
+                   static_cast<int>(page_mask)};
+  IFR_HIP(ifr::launch_rope_cache_write(static_cast<const int32_t*>(image_dev),
+                                       static_cast<int>(seq_len), q, k_src, v_src,
+                                       k_cache, v_cache, cos_table, sin_table,
+                                       static_cast<int>(num_q), static_cast<int>(num_kv),
+                                       g, static_cast<int>(half),
+                                       static_cast<int>(pair_stride),
+                                       static_cast<int>(head_dim), as_stream(stream)),
+          "rope_cache_write");
+  return ok();
+}
+
+int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
+                           const void* q, const void* k_base,
+                           const void* v_base, void* output, void* partials,
+                           int64_t partials_bytes, int64_t num_q,
+                           int64_t num_kv, int64_t head_dim,
+                           int64_t partial_stride, int64_t kv_stride,
+                           int64_t page_len, int64_t page_mask,
+                           uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  st = check_attention_shapes(num_q, num_kv, head_dim, partial_stride, kv_stride, 2);
+  if (st) return st;
+  if (!image_dev || !q || !k_base || !v_base || !output || !partials)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q, 16) || !aligned(k_base, 16) || !aligned(v_base, 16) ||
+      !aligned(output, 16) || !aligned(partials, 16))
+    return fail(IFR_EINVAL, "q, k_base, v_base, output and partials must be 16-byte aligned");
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
+  st = check_geometry(info, pow2_shift(page_len), page_len - 1, page_mask);
+  if (st) return st;
+  if (partials_bytes < info[3] * partial_stride * 4)
+    return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
+  ifr::PagedGeom g{static_cast<int>(pow2_shift(page_len)), static_cast<int>(page_len - 1),
+                   static_cast<int>(page_mask)};
+  IFR_HIP(ifr::launch_attention_bf16(static_cast<const int32_t*>(image_dev),
+                                     static_cast<int>(info[0]), static_cast<int>(info[1]),
+                                     static_cast<int>(info[2]), q, k_base, v_base, output,
+                                     static_cast<float*>(partials), partial_stride,
+                                     static_cast<int>(num_q), static_cast<int>(num_kv),
+                                     static_cast<int>(head_dim), kv_stride, g,
+                                     as_stream(stream)),
+          "attention_bf16");
+  return ok();
+}
+
+static int32_t dispatch_attention(int64_t kind, const void* q, const void* k_base,
+                                  const void* v_base, void* output, void* partials,
+                                  int64_t partials_bytes, const int32_t* runs,
+                                  int64_t num_runs, const int32_t* base_rows,
+                                  int64_t num_rows, int64_t num_q,
+                                  int64_t partial_stride, int64_t kv_stride,
+                                  int64_t seq_len, int64_t head_dim, int64_t gqa_ratio,
+                                  int64_t window, int64_t cache_size, int64_t page_len,
+                                  int64_t cache_rows, int64_t cap, void* ws_host,
+                                  void* ws_dev, int64_t ws_bytes, uint64_t stream) {
+  if (seq_len <= 0) return ok();  // the reference returns without work
+  if (gqa_ratio <= 0 || num_q % gqa_ratio != 0)
+    return fail(IFR_EINVAL, "num_q must be a multiple of gqa_ratio");
+  if (!ws_host || !ws_dev) return fail(IFR_EINVAL, "null plan staging");
+  int64_t info[16];
+  int32_t st = plan_impl(static_cast<int32_t*>(ws_host), ws_bytes / 4, runs, num_runs,
+                         base_rows, num_rows, seq_len, kind, window, cache_size,
+                         page_len, cache_rows, cap, kv_stride * 2, info);
+  if (st) return st;
+  IFR_HIP(hipMemcpyAsync(ws_dev, ws_host, static_cast<size_t>(info[4]),
+                         hipMemcpyHostToDevice, as_stream(stream)),
+          "plan upload");
+  const int64_t page_mask = kind == 0 ? cache_size / page_len - 1 : -1;
+  return ifr_attention_bf16(ws_dev, info, q, k_base, v_base, output, partials,
+                            partials_bytes, num_q, num_q / gqa_ratio, head_dim,
+                            partial_stride, kv_stride, page_len, page_mask, stream);
+}
+
+int32_t ifr_dispatch_sliding_attention(
+    const void* q, const void* k_base, const void* v_base, void* output,
+    void* partials, int64_t partials_bytes, const int32_t* runs,
+    int64_t num_runs, const int32_t* base_rows, int64_t num_rows,
+    int64_t num_q, int64_t partial_stride, int64_t kv_stride, int64_t seq_len,
+    int64_t head_dim, int64_t gqa_ratio, int64_t window, int64_t cache_size,
+    int64_t page_len, int64_t cache_rows, int64_t cap, void* ws_host,
+    void* ws_dev, int64_t ws_bytes, uint64_t stream) {
+  return dispatch_attention(0, q, k_base, v_base, output, partials, partials_bytes,
+                            runs, num_runs, base_rows, num_rows, num_q, partial_stride,
+                            kv_stride, seq_len, head_dim, gqa_ratio, window, cache_size,
+                            page_len, cache_rows, cap, ws_host, ws_dev, ws_bytes, stream);
+}
+
+int32_t ifr_dispatch_full_attention(
+    const void* q, const void* k_base, const void* v_base, void* output,
+    void* partials, int64_t partials_bytes, const int32_t* runs,
+    int64_t num_runs, const int32_t* base_rows, int64_t num_rows,
+    int64_t num_q, int64_t partial_stride, int64_t kv_stride, int64_t seq_len,
+    int64_t head_dim, int64_t gqa_ratio, int64_t page_len, int64_t cache_rows,
+    int64_t cap, void* ws_host, void* ws_dev, int64_t ws_bytes,
+    uint64_t stream) {
+  return dispatch_attention(1, q, k_base, v_base, output, partials, partials_bytes,
+                            runs, num_runs, base_rows, num_rows, num_q, partial_stride,
+                            kv_stride, seq_len, head_dim, gqa_ratio, 1, page_len,
+                            page_len, cache_rows, cap, ws_host, ws_dev, ws_bytes, stream);
+}
+
+// ---- page copy and gather ---------------------------------------------------
+
+static constexpr int64_t kCopyChunk = 64 * 1024;
+
+int64_t ifr_copy_jobs_bytes(int64_t num_jobs, int64_t total_bytes) {
+  if (num_jobs < 0 || total_bytes < 0) return -1;
+  return 32 * (num_jobs + total_bytes / kCopyChunk + 1);
+}
+
+int32_t ifr_dispatch_copy_jobs(void* arena, const int64_t* jobs, int64_t num_jobs,
+                               void* ws_host, void* ws_dev, int64_t ws_bytes,
+                               uint64_t stream) {
+  if (num_jobs <= 0) return ok();  // page_copy.mojo:72-74
+  if (!arena || !jobs || !ws_host || !ws_dev) return fail(IFR_EINVAL, "null pointer");
+  int64_t total = 0;
+  bool aligned16 = aligned(arena, 16);
+  for (int64_t i = 0; i < num_jobs; ++i) {
+    const int64_t s = jobs[3 * i], d = jobs[3 * i + 1], n = jobs[3 * i + 2];
+    if (s < 0 || d < 0 || n < 0) return fail(IFR_EINVAL, "job %lld has a negative field", (long long)i);
+    if (n > 0 && ((s < d) ? (s + n > d) : (d + n > s)))
+      return fail(IFR_EINVAL, "job %lld copies between overlapping ranges", (long long)i);
+    total += n;
+    if ((s | d | n) & 15) aligned16 = false;
+  }
+  if (total == 0) return ok();
+  int64_t* chunks = static_cast<int64_t*>(ws_host);
+  int64_t nc = 0;
+  const int64_t cap_chunks = ws_bytes / 32;
+  for (int64_t i = 0; i < num_jobs; ++i) {
+    for (int64_t o = 0; o < jobs[3 * i + 2]; o += kCopyChunk) {
+      if (nc >= cap_chunks) return fail(IFR_ESPACE, "copy staging too small");
+      chunks[4 * nc] = jobs[3 * i] + o;
+      chunks[4 * nc + 1] = jobs[3 * i + 1] + o;
+      chunks[4 * nc + 2] = std::min(kCopyChunk, jobs[3 * i + 2] - o);
+      chunks[4 * nc + 3] = 0;
+      ++nc;
+    }
+  }
+  if (nc > INT32_MAX) return fail(IFR_EINVAL, "too many chunks");
+  IFR_HIP(hipMemcpyAsync(ws_dev, ws_host, static_cast<size_t>(nc * 32),
+                         hipMemcpyHostToDevice, as_stream(stream)),
+          "copy job upload");
+  IFR_HIP(ifr::launch_copy_chunks(arena, static_cast<const int64_t*>(ws_dev),
+                                  static_cast<int>(nc), aligned16 ? 1 : 0,
+                                  as_stream(stream)),
+          "copy_chunks");
+  return ok();
+}
+
+int32_t ifr_dispatch_gather_rows(const void* src, void* dst, const int32_t* rows,
+                                 int64_t num_rows, int64_t cols, uint64_t stream) {
+  if (num_rows <= 0) return ok();  // gather.mojo:42-43
+  if (!src || !dst || !rows) return fail(IFR_EINVAL, "null pointer");
+  if (cols <= 0 || cols > INT32_MAX) return fail(IFR_EINVAL, "bad cols");
+  if ((cols & 7) == 0 && (!aligned(src, 16) || !aligned(dst, 16)))
+    return fail(IFR_EINVAL, "src and dst must be 16-byte aligned");
+  IFR_HIP(ifr::launch_gather_rows(src, dst, rows, static_cast<int>(num_rows),
+                                  static_cast<int>(cols), as_stream(stream)),
+          "gather_rows");
+  return ok();
+}
+
+// ---- butterquant --------------------------------------------------------------
+
+int32_t ifr_bq_attn_prep(const void* image_dev, const int64_t* info,
+                         const void* q_src, const void* k_src, const void* v_src,
+                         const void* q_norm, const void* k_norm, void* q_i8,
+                         float* qi_bias, float* f_q, void* k_cache, float* k_scale,
+                         void* v_cache, float* v_scale, const float* cos_table,
+                         const float* sin_table, int64_t num_q, int64_t num_kv,
+                         int64_t page_shift, int64_t row_mask, int64_t page_mask,
+                         int64_t seq_len, int64_t head_dim, int64_t rope_half,
+                         int64_t pair_stride, float sqrt_n, float n_eps,
+                         uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (seq_len != info[5]) return fail(IFR_EINVAL, "seq_len differs from the plan");
+  if (!image_dev || !q_src || !k_src || !v_src || !q_norm || !k_norm || !q_i8 || !qi_bias ||
+      !f_q || !k_cache || !k_scale || !v_cache || !v_scale || !cos_table || !sin_table)
+    return fail(IFR_EINVAL, "null pointer");
+  if (head_dim != 256) return fail(IFR_EUNSUPPORTED, "bq prep is compiled for head_dim 256");
+  if (rope_half <= 0 || rope_half % 4 != 0 || rope_half > pair_stride ||
+      pair_stride + rope_half > head_dim || pair_stride % 4 != 0)
+    return fail(IFR_EINVAL, "bad rope geometry");
+  if (num_q <= 0 || num_kv <= 0) return fail(IFR_EINVAL, "bad head counts");
+  st = check_geometry(info, page_shift, row_mask, page_mask);
+  if (st) return st;
+  ifr::PagedGeom g{static_cast<int>(page_shift), static_cast<int>(row_mask),
+                   static_cast<int>(page_mask)};
+  IFR_HIP(ifr::launch_bq_attn_prep(static_cast<const int32_t*>(image_dev),
+                                   static_cast<int>(seq_len), q_src, k_src, v_src, q_norm,
+                                   k_norm, q_i8, qi_bias, f_q, k_cache, k_scale, v_cache,
+                                   v_scale, cos_table, sin_table, static_cast<int>(num_q),
+                                   static_cast<int>(num_kv), g, static_cast<int>(head_dim),
+                                   static_cast<int>(rope_half),
+                                   static_cast<int>(pair_stride), sqrt_n, n_eps,
+                                   as_stream(stream)),
+          "bq_attn_prep");
+  return ok();
+}
+
+int32_t ifr_bq_attention(const void* image_dev, const int64_t* info,
+                         const void* q_i8, const float* qi_bias, const float* f_q,
+                         const void* k_base, const float* k_scale, const void* v_base,
+                         const float* v_scale, void* output, void* partials,
+                         int64_t partials_bytes, int64_t num_q, int64_t num_kv,
+                         int64_t head_dim, int64_t partial_stride, int64_t kv_stride,
+                         int64_t page_len, int64_t page_mask, uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  st = check_attention_shapes(num_q, num_kv, head_dim, partial_stride, kv_stride, 1);
+  if (st) return st;
+  if (head_dim != 256 || num_q / num_kv != 2)
+    return fail(IFR_EUNSUPPORTED, "bq attention is compiled for head_dim 256, gqa 2");
+  if (!image_dev || !q_i8 || !qi_bias || !f_q || !k_base || !k_scale || !v_base ||
+      !v_scale || !output || !partials)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q_i8, 16) || !aligned(k_base, 16) || !aligned(v_base, 16) ||
+      !aligned(output, 16) || !aligned(partials, 16))
+    return fail(IFR_EINVAL, "code, output and partial buffers must be 16-byte aligned");
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
+  st = check_geometry(info, pow2_shift(page_len), page_len - 1, page_mask);
+  if (st) return st;
+  if (partials_bytes < info[3] * partial_stride * 4)
+    return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
+  ifr::PagedGeom g{static_cast<int>(pow2_shift(page_len)), static_cast<int>(page_len - 1),
+                   static_cast<int>(page_mask)};
+  IFR_HIP(ifr::launch_bq_attention(static_cast<const int32_t*>(image_dev),
+                                   static_cast<int>(info[0]), static_cast<int>(info[1]),
+                                   static_cast<int>(info[2]), q_i8, qi_bias, f_q, k_base,
+                                   k_scale, v_base, v_scale, output,
+                                   static_cast<float*>(partials), partial_stride,
+                                   static_cast<int>(num_q), static_cast<int>(num_kv),
+                                   static_cast<int>(head_dim), kv_stride, g,
+                                   as_stream(stream)),
+          "bq_attention");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,395 @@
+// Paged split-KV flash attention (bf16 KV) and the log-sum-exp merge for
+// gfx950.
+//
+// One wave64 owns one (work item, kv head): it walks the item's positions in
+// tiles of 16 consecutive positions starting at the item's first position,
+// exactly as FlashAttentionKernel walks its worker range
+// (kernels/flash_attention.mojo:44-54), and applies the online softmax of
+// process_kv_tile (kernels/attention_ops.mojo:193-253) once per tile per q
+// head.  Matching the tile boundaries matters: the reference's biased exp
+// returns fexp(0) = 0.99963, so every tile rescales all earlier tiles and the
+// output depends on where tiles start.
+//
+// Lane layouts (D = head_dim):
+//   QK:  8 lanes per position, 8 positions per pass, two passes per tile.
+//        Lane (tk, c) holds bf16 elements {8c + 64i .. 8c + 64i + 7} of K and
+//        of each GQA query head, so one pass loads 8 rows x 128 contiguous
+//        bytes per 16-byte load.  Scores use v_dot2_f32_bf16 and a 3-step DPP
+//        reduction inside each 8-lane group.
+//   PV:  lane L owns output dims {DPL*L .. DPL*L + DPL-1}, DPL = D/64, and
+//        accumulates positions in order with fma(v, w, acc), the reference's
+//        per-element order.  Weights are broadcast with v_readlane.
+// The tile max is a wave-wide max (exact in any order); the tile weight sum
+// follows the halving tree of SIMD.reduce_add over the 16 positions.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ifr {
+namespace {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
+}
+
+template <int DPL>
+struct VecOf;
+template <>
+struct VecOf<4> {
+  using T = uint2;
+  __device__ static void unpack(const uint2& v, float* f) {
+    f[0] = bf16_lo(v.x);
+    f[1] = bf16_hi(v.x);
+    f[2] = bf16_lo(v.y);
+    f[3] = bf16_hi(v.y);
+  }
+};
+template <>
+struct VecOf<8> {
+  using T = uint4;
+  __device__ static void unpack(const uint4& v, float* f) {
+    f[0] = bf16_lo(v.x);
+    f[1] = bf16_hi(v.x);
+    f[2] = bf16_lo(v.y);
+    f[3] = bf16_hi(v.y);
+    f[4] = bf16_lo(v.z);
+    f[5] = bf16_hi(v.z);
+    f[6] = bf16_lo(v.w);
+    f[7] = bf16_hi(v.w);
+  }
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void flash_partial_bf16_kernel(
+    const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    float* __restrict__ partials, int64_t partial_stride, int num_q,
+    int num_kv, int64_t kv_stride, int shift, int row_mask, int page_mask) {
+  constexpr int NCH = D / 64;  // 16-byte K chunks per lane per position
+  constexpr int DPL = D / 64;  // PV output dims per lane
+  using V = VecOf<DPL>;
+  using VT = typename V::T;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = blockIdx.y * 4 + wave;
+  if (g >= num_kv) return;
+
+  const int32_t* item = image + image[kHdrOffItems] + blockIdx.x * kItemWords;
+  const int q_row = item[0];
+  const int run = item[1];
+  const int start_pos = item[2];
+  const int start = item[3];
+  const int end = item[4];
+  const int stripe = item[5];
+  const int32_t* rows =
+      image + image[kHdrOffRows] + image[image[kHdrOffRuns] + run * 4 + 2];
+
+  const int tk = lane >> 3;
+  const int c = lane & 7;
+
+  uint4 qv[G][NCH];
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    const uint16_t* qr =
+        q + (static_cast<int64_t>(q_row) * num_q + g * G + r) * D + 8 * c;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i)
+      qv[r][i] = *reinterpret_cast<const uint4*>(qr + 64 * i);
+  }
+
+  const uint16_t* kh = kc + static_cast<int64_t>(g) * D + 8 * c;
+  const uint16_t* vh = vc + static_cast<int64_t>(g) * D + DPL * lane;
+
+  float m[G], l[G], acc[G][DPL];
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    m[r] = kNegBig;
+    l[r] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[r][e] = 0.0f;
+  }
+
+  for (int pos0 = start; pos0 < end; pos0 += kTile) {
+    const int tile_len = min(kTile, end - pos0);
+
+    // ---- scores for the tile's 16 positions (two passes of 8) ----
+    float s[2][G];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int t = 8 * b + tk;
+      const bool valid = t < tile_len;
+      uint4 kv4[NCH];
+      if (valid) {
+        const int p = start_pos + pos0 + t;
+        const int64_t slot =
+            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+        const uint16_t* kr = kh + slot * kv_stride;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+          kv4[i] = *reinterpret_cast<const uint4*>(kr + 64 * i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) kv4[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < G; ++r) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+          a = dot2_bf16(kv4[i].x, qv[r][i].x, a);
+          a = dot2_bf16(kv4[i].y, qv[r][i].y, a);
+          a = dot2_bf16(kv4[i].z, qv[r][i].z, a);
+          a = dot2_bf16(kv4[i].w, qv[r][i].w, a);
+        }
+        a = a + dpp_f32<kDppXor1>(a);
+        a = a + dpp_f32<kDppXor2>(a);
+        a = a + dpp_f32<kDppHalfMirror>(a);
+        s[b][r] = valid ? a : kNegBig;
+      }
+    }
+
+    // ---- V rows of the tile (positions are wave-uniform) ----
+    VT vv[kTile];
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      if (t < tile_len) {
+        const int p = start_pos + pos0 + t;
+        const int64_t slot =
+            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+        vv[t] = *reinterpret_cast<const VT*>(vh + slot * kv_stride);
+      }
+    }
+
+    // ---- online softmax, once per tile per q head ----
+    float w[2][G];
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      float mx = max_ref(s[0][r], s[1][r]);
+      mx = max_ref(mx, dpp_f32<kDppRowRor8>(mx));
+      mx = max_ref(mx, shfl_xor_f32(mx, 16));
+      mx = max_ref(mx, shfl_xor_f32(mx, 32));
+      const float m_new = mx > m[r] ? mx : m[r];
+      const float corr = fexp(max_ref(-87.0f, m[r] - m_new));
+      w[0][r] = fexp(max_ref(-87.0f, s[0][r] - m_new));
+      w[1][r] = fexp(max_ref(-87.0f, s[1][r] - m_new));
+      // Halving tree over positions t = 8b + tk: (t, t+8) in-lane, then
+      // tk ^ 4, tk ^ 2, tk ^ 1 = lane ^ 32, ^ 16, ^ 8.
+      float ts = w[0][r] + w[1][r];
+      ts = ts + shfl_xor_f32(ts, 32);
+      ts = ts + shfl_xor_f32(ts, 16);
+      ts = ts + dpp_f32<kDppRowRor8>(ts);
+      const float lc = l[r] * corr;
+      l[r] = lc + ts;
+      m[r] = m_new;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[r][e] = acc[r][e] * corr;
+    }
+
+    // ---- PV in position order ----
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      if (t < tile_len) {
+        float wr[G];
+#pragma unroll
+        for (int r = 0; r < G; ++r) wr[r] = readlane_f32(w[t >> 3][r], 8 * (t & 7));
+        float vf[DPL];
+        V::unpack(vv[t], vf);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+#pragma unroll
+          for (int r = 0; r < G; ++r) acc[r][e] = fmaf(vf[e], wr[r], acc[r][e]);
+      }
+    }
+  }
+
+  float* part = partials + static_cast<int64_t>(stripe) * partial_stride;
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    float* dst = part + static_cast<int64_t>(g * G + r) * D + DPL * lane;
+#pragma unroll
+    for (int e = 0; e < DPL; e += 4)
+      *reinterpret_cast<float4*>(dst + e) =
+          make_float4(acc[r][e], acc[r][e + 1], acc[r][e + 2], acc[r][e + 3]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      part[num_q * D + g * G + r] = m[r];
+      part[num_q * D + num_q + g * G + r] = l[r];
+    }
+  }
+}
+
+// merge_segments + write_finalized_head (kernels/logsum_merge.mojo:28-122)
+// for one merge unit and one q head per wave; mode IFR_PLAN_TOKEN_DIRECT
+// finalises as acc * (1/l) like the sliding prefill kernels
+// (kernels/flash_attention_prefill.mojo:95-106).  Every lane evaluates the
+// scalar part of the merge identically, so the order of operations is the
+// reference's: sequential max, 16-wide batches of corrections summed by the
+// halving tree, acc initialised by the first live segment, then fma.
+template <int D>
+__global__ __launch_bounds__(256) void merge_kernel(
+    const int32_t* __restrict__ image, const float* __restrict__ partials,
+    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode) {
+  constexpr int DPL = D / 64;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * 4 + wave;
+  if (h >= num_q) return;
+  const int32_t* unit = image + image[kHdrOffUnits] + blockIdx.x * kUnitWords;
+  const int out_row = unit[0];
+  const int stripe_base = unit[1];
+  const int n = unit[2];
+  const float* base = partials + static_cast<int64_t>(stripe_base) * partial_stride;
+  const int m_off = num_q * D;
+  const int l_off = m_off + num_q;
+  float acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = 0.0f;
+  float inv_l = 0.0f;
+  bool live = false;
+
+  if (mode == 1) {
+    const float lv = base[l_off + h];
+    if (lv > 0.0f) {
+      live = true;
+      inv_l = 1.0f / lv;
+      const float* src = base + static_cast<int64_t>(h) * D + DPL * lane;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[e] = src[e];
+    }
+  } else {
+    float gm = kNegBig;
+    for (int s = 0; s < n; ++s) {
+      const float sm = base[static_cast<int64_t>(s) * partial_stride + m_off + h];
+      if (sm > gm) gm = sm;
+    }
+    float gl = 0.0f;
+    bool first = true;
+    for (int bs = 0; bs < n; bs += 16) {
+      float corr[16], prod[16];
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        float delta = kNegBig, ls = 0.0f;
+        if (bs + b < n) {
+          const float* sp = base + static_cast<int64_t>(bs + b) * partial_stride;
+          delta = sp[m_off + h] - gm;
+          ls = sp[l_off + h];
+        }
+        float cv = fexp(max_ref(-87.0f, delta));
+        cv = ls > 0.0f ? cv : 0.0f;
+        corr[b] = cv;
+        prod[b] = ls * cv;
+      }
+#pragma unroll
+      for (int wdt = 8; wdt >= 1; wdt >>= 1)
+#pragma unroll
+        for (int j = 0; j < wdt; ++j) prod[j] = prod[j] + prod[j + wdt];
+      gl = gl + prod[0];
+      const int bn = min(16, n - bs);
+      for (int b = 0; b < bn; ++b) {
+        const float cv = corr[b];
+        if (cv <= 0.0f) continue;
+        const float* src = base + static_cast<int64_t>(bs + b) * partial_stride +
+                           static_cast<int64_t>(h) * D + DPL * lane;
+        if (first) {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[e] = src[e] * cv;
+          first = false;
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[e] = fmaf(src[e], cv, acc[e]);
+        }
+      }
+    }
+    if (gl > 0.0f) {
+      live = true;
+      inv_l = 1.0f / gl;
+    }
+  }
+
+  uint16_t* dst = out + (static_cast<int64_t>(out_row) * num_q + h) * D + DPL * lane;
+  uint32_t packed[DPL / 2];
+#pragma unroll
+  for (int e = 0; e < DPL; e += 2) {
+    uint32_t lo = live ? f32_to_bf16_bits(acc[e] * inv_l) : 0u;
+    uint32_t hi = live ? f32_to_bf16_bits(acc[e + 1] * inv_l) : 0u;
+    packed[e / 2] = lo | (hi << 16);
+  }
+  if constexpr (DPL == 4) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+  } else {
+    *reinterpret_cast<uint4*>(dst) =
+        make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  }
+}
+
+template <int D, int G>
+hipError_t launch_partials(const int32_t* image, int num_items, const void* q,
+                           const void* k, const void* v, float* partials,
+                           int64_t ps, int num_q, int num_kv, int64_t kv_stride,
+                           PagedGeom geom, hipStream_t stream) {
+  dim3 grid(num_items, (num_kv + 3) / 4);
+  hipLaunchKernelGGL((flash_partial_bf16_kernel<D, G>), grid, dim3(256), 0,
+                     stream, image, static_cast<const uint16_t*>(q),
+                     static_cast<const uint16_t*>(k),
+                     static_cast<const uint16_t*>(v), partials, ps, num_q,
+                     num_kv, kv_stride, geom.shift, geom.row_mask,
+                     geom.page_mask);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool attention_shape_supported(int head_dim, int gqa) {
+  return (head_dim == 256 || head_dim == 512) && (gqa == 1 || gqa == 2);
+}
+
+hipError_t launch_merge(const int32_t* image, int num_units, int mode,
+                        const float* partials, void* output, int64_t ps,
+                        int num_q, int head_dim, hipStream_t stream) {
+  if (num_units <= 0) return hipSuccess;
+  dim3 grid(num_units, (num_q + 3) / 4);
+  if (head_dim == 256)
+    hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image,
+                       partials, static_cast<uint16_t*>(output), ps, num_q,
+                       mode);
+  else
+    hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image,
+                       partials, static_cast<uint16_t*>(output), ps, num_q,
+                       mode);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_bf16(const int32_t* image, int num_items,
+                                 int num_units, int mode, const void* q,
+                                 const void* k, const void* v, void* output,
+                                 float* partials, int64_t ps, int num_q,
+                                 int num_kv, int head_dim, int64_t kv_stride,
+                                 PagedGeom geom, hipStream_t stream) {
+  hipError_t err = hipSuccess;
+  if (num_items > 0) {
+    const int gqa = num_q / num_kv;
+    if (head_dim == 256 && gqa == 2)
+      err = launch_partials<256, 2>(image, num_items, q, k, v, partials, ps,
+                                    num_q, num_kv, kv_stride, geom, stream);
+    else if (head_dim == 256 && gqa == 1)
+      err = launch_partials<256, 1>(image, num_items, q, k, v, partials, ps,
+                                    num_q, num_kv, kv_stride, geom, stream);
+    else if (head_dim == 512 && gqa == 2)
+      err = launch_partials<512, 2>(image, num_items, q, k, v, partials, ps,
+                                    num_q, num_kv, kv_stride, geom, stream);
+    else
+      err = launch_partials<512, 1>(image, num_items, q, k, v, partials, ps,
+                                    num_q, num_kv, kv_stride, geom, stream);
+    if (err != hipSuccess) return err;
+  }
+  return launch_merge(image, num_units, mode, partials, output, ps, num_q,
+                      head_dim, stream);
+}
+
+}  // namespace ifr

@@ -1,0 +1,432 @@
+// Butterquant int8 KV for gfx950: the quantizing KV append (BqAttnPrepKernel,
+// butterquant_kernels/attention.mojo:494-582) and the int8 paged split-KV
+// attention (bq_process_kv_tile / BqFlashAttentionKernel, :27-167), whose
+// partials feed the shared log-sum-exp merge.
+//
+// Prep, one wave per head (D = 256, lane L owns elements 4L..4L+3):
+//   RMS     the reference's lane-wise chain over 16 AVX-512 lanes
+//           (butterquant/head_prep.mojo:9-16) is replayed exactly: lane
+//           j < 16 runs ssq_j = x_j^2, then fma(x_{16ri+j}, x_{16ri+j}, ssq_j)
+//           for ri = 1..15, and the 16 partial sums are tree-reduced.
+//   RoPE    partner elements arrive with ds_bpermute; no FMA contraction.
+//   FWHT    strides 1 and 2 inside the lane, 4..128 across lanes (xor 1..32);
+//           the lower element of each pair becomes a+b, the upper a-b, in the
+//           reference's stage order (butterquant/fwht.mojo:20-57), so the
+//           rotated values -- and with them the int8 codes -- are the
+//           reference's bit for bit.
+//   absmax  wave max, 127/amax, round-to-nearest-even, clamp [-128, 127].
+// Attention, one wave per (work item, kv head): 4 lanes per position, 16
+// positions per pass (one tile); integer scores with v_dot4_i32_i8 (exact),
+// scaled as (((float)dot * f_q) * k_scale) / 127^2 like the reference; PV with
+// lane L owning output dims 4L..4L+3 and fma in position order.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ifr {
+namespace {
+
+constexpr int kBqD = 256;
+
+__device__ __forceinline__ float bpermute_f32(float v, int src_lane) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
+}
+
+// Absmax int8 quantisation of the wave's 256 values (4 per lane); returns
+// amax and writes the lane's 4 codes packed little-endian into *codes.
+__device__ __forceinline__ float absmax_quantize(const float* r, uint32_t* codes,
+                                                 int* qsum) {
+  float vmax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = fabsf(r[e]);
+    vmax = a > vmax ? a : vmax;
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float o = shfl_xor_f32(vmax, m);
+    vmax = o > vmax ? o : vmax;
+  }
+  float amax = vmax;
+  if (amax < 1e-10f) amax = 1e-10f;
+  const float inv = 127.0f / amax;
+  uint32_t packed = 0;
+  int s = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = rintf(r[e] * inv);
+    v = v < -128.0f ? -128.0f : v;
+    v = v > 127.0f ? 127.0f : v;
+    const int qi = static_cast<int>(v);
+    s += qi;
+    packed |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * e);
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) s += shfl_xor_i32(s, m);
+  *codes = packed;
+  *qsum = s;
+  return amax;
+}
+
+// fwht_apply over 256 values held 4 per lane.
+__device__ __forceinline__ void fwht256(float* r, int lane) {
+  {  // stride 1
+    const float a0 = r[0], b0 = r[1], a1 = r[2], b1 = r[3];
+    r[0] = a0 + b0;
+    r[1] = a0 - b0;
+    r[2] = a1 + b1;
+    r[3] = a1 - b1;
+  }
+  {  // stride 2
+    const float a0 = r[0], b0 = r[2], a1 = r[1], b1 = r[3];
+    r[0] = a0 + b0;
+    r[2] = a0 - b0;
+    r[1] = a1 + b1;
+    r[3] = a1 - b1;
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {  // strides 4 .. 128
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = shfl_xor_f32(r[e], m);
+      r[e] = upper ? (p - r[e]) : (r[e] + p);
+    }
+  }
+  const float sc = static_cast<float>(1.0 / static_cast<double>(sqrtf(256.0f)));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = r[e] * sc;
+}
+
+__global__ __launch_bounds__(256) void bq_prep_kernel(
+    const int32_t* __restrict__ image, const uint16_t* __restrict__ q_src,
+    const uint16_t* __restrict__ k_src, const uint16_t* __restrict__ v_src,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
+    int8_t* __restrict__ q_i8, float* __restrict__ qi_bias,
+    float* __restrict__ f_q, int8_t* __restrict__ k_cache,
+    float* __restrict__ k_scale, int8_t* __restrict__ v_cache,
+    float* __restrict__ v_scale, const float* __restrict__ cos_table,
+    const float* __restrict__ sin_table, int num_q, int num_kv, int shift,
+    int row_mask, int page_mask, int rope_half, int pair_stride, float sqrt_n,
+    float n_eps) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x;
+  const int run = image[image[kHdrOffTokRun] + tok];
+  const int32_t* rp = image + image[kHdrOffRuns] + run * 4;
+  const int pos = rp[1] + (tok - rp[0]);
+  const int32_t* rows = image + image[kHdrOffRows] + rp[2];
+  const float* cos_row = cos_table + static_cast<int64_t>(pos) * rope_half;
+  const float* sin_row = sin_table + static_cast<int64_t>(pos) * rope_half;
+  const int64_t slot =
+      static_cast<int64_t>(rows[(pos >> shift) & page_mask]) + (pos & row_mask);
+  const int64_t kv_stride = static_cast<int64_t>(num_kv) * kBqD;
+  const float inv_sqrt_n = 1.0f / sqrt_n;
+  const int n_heads = num_q + 2 * num_kv;
+
+  for (int hh = wave; hh < n_heads; hh += 4) {
+    const bool is_q = hh < num_q;
+    const bool is_k = !is_q && hh < num_q + num_kv;
+    const int h = is_q ? hh : (is_k ? hh - num_q : hh - num_q - num_kv);
+    const uint16_t* src =
+        is_q ? q_src + (static_cast<int64_t>(tok) * num_q + h) * kBqD
+             : (is_k ? k_src : v_src) + (static_cast<int64_t>(tok) * num_kv + h) * kBqD;
+    const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * lane);
+    float r[4] = {bf16_lo(raw.x), bf16_hi(raw.x), bf16_lo(raw.y), bf16_hi(raw.y)};
+
+    if (is_q || is_k) {
+      // head_inv_rms: lane j < 16 replays the reference's 16-lane register
+      // chain over elements 16*ri + j, reading the bf16 row again (cached).
+      float ssq = 0.0f;
+      if (lane < 16) {
+        const float x0 = bf16_to_f32(src[lane]);
+        ssq = x0 * x0;
+#pragma unroll
+        for (int ri = 1; ri < 16; ++ri) {
+          const float x = bf16_to_f32(src[16 * ri + lane]);
+          ssq = fmaf(x, x, ssq);
+        }
+      }
+      ssq = ssq + shfl_xor_f32(ssq, 8);
+      ssq = ssq + shfl_xor_f32(ssq, 4);
+      ssq = ssq + shfl_xor_f32(ssq, 2);
+      ssq = ssq + shfl_xor_f32(ssq, 1);
+      const float total = readlane_f32(ssq, 0);
+      const float inv_rms = sqrt_n / sqrtf(total + n_eps);
+      const uint16_t* gamma = is_q ? q_norm : k_norm;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float g = bf16_to_f32(gamma[4 * lane + e]);
+        const float t = r[e] * inv_rms;
+        r[e] = t * g;
+      }
+      // RoPE pairs (j, pair_stride + j), j < rope_half.
+      const int e0 = 4 * lane;
+      int partner = lane;
+      if (e0 < rope_half) partner = (e0 + pair_stride) >> 2;
+      else if (e0 >= pair_stride && e0 < pair_stride + rope_half) partner = (e0 - pair_stride) >> 2;
+      float pv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = bpermute_f32(r[e], partner);
+      if (e0 < rope_half) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float cv = cos_row[e0 + e], sv = sin_row[e0 + e];
+          const float a = r[e] * cv, b = pv[e] * sv;
+          r[e] = a - b;
+        }
+      } else if (e0 >= pair_stride && e0 < pair_stride + rope_half) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = e0 - pair_stride + e;
+          const float cv = cos_row[j], sv = sin_row[j];
+          const float c = r[e] * cv, d = pv[e] * sv;
+          r[e] = c + d;
+        }
+      }
+    }
+
+    fwht256(r, lane);
+    uint32_t codes;
+    int qsum;
+    const float amax = absmax_quantize(r, &codes, &qsum);
+    if (is_q) {
+      *reinterpret_cast<uint32_t*>(q_i8 + (static_cast<int64_t>(tok) * num_q + h) * kBqD +
+                                   4 * lane) = codes;
+      if (lane == 0) {
+        qi_bias[static_cast<int64_t>(tok) * num_q + h] = static_cast<float>(qsum) * 128.0f;
+        f_q[static_cast<int64_t>(tok) * num_q + h] = amax * inv_sqrt_n;
+      }
+    } else if (is_k) {
+      *reinterpret_cast<uint32_t*>(k_cache + slot * kv_stride + h * kBqD + 4 * lane) = codes;
+      if (lane == 0) k_scale[slot * num_kv + h] = amax;
+    } else {
+      *reinterpret_cast<uint32_t*>(v_cache + slot * kv_stride + h * kBqD + 4 * lane) = codes;
+      if (lane == 0) v_scale[slot * num_kv + h] = amax;
+    }
+  }
+}
+
+__device__ __forceinline__ void unpack_i8x4(uint32_t w, float* f) {
+  f[0] = static_cast<float>(static_cast<int8_t>(w & 0xFFu));
+  f[1] = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xFFu));
+  f[2] = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xFFu));
+  f[3] = static_cast<float>(static_cast<int8_t>(w >> 24));
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void bq_partial_kernel(
+    const int32_t* __restrict__ image, const int8_t* __restrict__ q_i8,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const int8_t* __restrict__ kc,
+    const float* __restrict__ k_scale, const int8_t* __restrict__ vc,
+    const float* __restrict__ v_scale, float* __restrict__ partials,
+    int64_t partial_stride, int num_q, int num_kv, int64_t kv_stride,
+    int shift, int row_mask, int page_mask) {
+  constexpr int D = kBqD;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = blockIdx.y * 4 + wave;
+  if (g >= num_kv) return;
+  const int32_t* item = image + image[kHdrOffItems] + blockIdx.x * kItemWords;
+  const int q_row = item[0];
+  const int run = item[1];
+  const int start_pos = item[2];
+  const int start = item[3];
+  const int end = item[4];
+  const int stripe = item[5];
+  const int32_t* rows =
+      image + image[kHdrOffRows] + image[image[kHdrOffRuns] + run * 4 + 2];
+  const float inv127 = 1.0f / 127.0f;
+  const float inv127sq = inv127 * inv127;
+
+  const int tk = lane >> 2;  // position within the tile
+  const int c = lane & 3;
+  uint4 qv[G][4];
+  float fq[G], qb[G];
+  int qsum128[G];
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    const int8_t* qr = q_i8 + (static_cast<int64_t>(q_row) * num_q + g * G + r) * D + 16 * c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[r][i] = *reinterpret_cast<const uint4*>(qr + 64 * i);
+    fq[r] = f_q[static_cast<int64_t>(q_row) * num_q + g * G + r];
+    qb[r] = qi_bias[static_cast<int64_t>(q_row) * num_q + g * G + r];
+    // The reference's VNNI dot reads (k ^ 0x80) as unsigned: raw = dot +
+    // 128 * sum(q).  Sum the lane's 64 codes, then the 4 lanes of a group.
+    int qs = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(qv[r][i].x), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(qv[r][i].y), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(qv[r][i].z), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(qv[r][i].w), 0x01010101, qs, false);
+    }
+    qs = qs + dpp_i32<kDppXor1>(qs);
+    qs = qs + dpp_i32<kDppXor2>(qs);
+    qsum128[r] = 128 * qs;
+  }
+  const int8_t* kh = kc + static_cast<int64_t>(g) * D + 16 * c;
+  const int8_t* vh = vc + static_cast<int64_t>(g) * D + 4 * lane;
+
+  float m[G], l[G], acc[G][4];
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    m[r] = kNegBig;
+    l[r] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
+  }
+
+  for (int pos0 = start; pos0 < end; pos0 += kTile) {
+    const int tile_len = min(kTile, end - pos0);
+    const bool valid = tk < tile_len;
+    float s[G];
+    {
+      uint4 kv4[4];
+      float ks = 0.0f;
+      if (valid) {
+        const int p = start_pos + pos0 + tk;
+        const int64_t slot =
+            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+        const int8_t* kr = kh + slot * kv_stride;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kv4[i] = *reinterpret_cast<const uint4*>(kr + 64 * i);
+        ks = k_scale[slot * num_kv + g];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kv4[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < G; ++r) {
+        int a = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].x), static_cast<int>(qv[r][i].x), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].y), static_cast<int>(qv[r][i].y), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].z), static_cast<int>(qv[r][i].z), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].w), static_cast<int>(qv[r][i].w), a, false);
+        }
+        a = a + dpp_i32<kDppXor1>(a);
+        a = a + dpp_i32<kDppXor2>(a);
+        float sc = static_cast<float>(a + qsum128[r]) - qb[r];
+        sc = sc * fq[r];
+        sc = sc * ks;
+        sc = sc * inv127sq;
+        s[r] = valid ? sc : kNegBig;
+      }
+    }
+
+    uint32_t vv[kTile];
+    float vs[kTile];
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      if (t < tile_len) {
+        const int p = start_pos + pos0 + t;
+        const int64_t slot =
+            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+        vv[t] = *reinterpret_cast<const uint32_t*>(vh + slot * kv_stride);
+        vs[t] = v_scale[slot * num_kv + g];
+      }
+    }
+
+    float w[G];
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      float mx = s[r];
+      mx = max_ref(mx, dpp_f32<kDppHalfMirror>(mx));  // position ^ 1
+      mx = max_ref(mx, dpp_f32<kDppRowRor8>(mx));     // position ^ 2
+      mx = max_ref(mx, shfl_xor_f32(mx, 16));         // position ^ 4
+      mx = max_ref(mx, shfl_xor_f32(mx, 32));         // position ^ 8
+      const float m_new = mx > m[r] ? mx : m[r];
+      const float corr = fexp(max_ref(-87.0f, m[r] - m_new));
+      w[r] = fexp(max_ref(-87.0f, s[r] - m_new));
+      // Halving tree over positions: ^8, ^4, ^2, ^1 = lane ^32, ^16, ^8, ^4.
+      float ts = w[r];
+      ts = ts + shfl_xor_f32(ts, 32);
+      ts = ts + shfl_xor_f32(ts, 16);
+      ts = ts + dpp_f32<kDppRowRor8>(ts);
+      ts = ts + dpp_f32<kDppHalfMirror>(ts);
+      const float lc = l[r] * corr;
+      l[r] = lc + ts;
+      m[r] = m_new;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][e] = acc[r][e] * corr;
+    }
+
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      if (t < tile_len) {
+        float vf[4];
+        unpack_i8x4(vv[t], vf);
+#pragma unroll
+        for (int r = 0; r < G; ++r) {
+          const float wt = readlane_f32(w[r], 4 * t);
+          const float a = wt * vs[t];
+          const float wts = a * inv127;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r][e] = fmaf(vf[e], wts, acc[r][e]);
+        }
+      }
+    }
+  }
+
+  float* part = partials + static_cast<int64_t>(stripe) * partial_stride;
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    float* dst = part + static_cast<int64_t>(g * G + r) * D + 4 * lane;
+    *reinterpret_cast<float4*>(dst) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      part[num_q * D + g * G + r] = m[r];
+      part[num_q * D + num_q + g * G + r] = l[r];
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_bq_attn_prep(const int32_t* image, int seq_len, const void* q_src,
+                               const void* k_src, const void* v_src, const void* q_norm,
+                               const void* k_norm, void* q_i8, float* qi_bias, float* f_q,
+                               void* k_cache, float* k_scale, void* v_cache,
+                               float* v_scale, const float* cos_table,
+                               const float* sin_table, int num_q, int num_kv,
+                               PagedGeom geom, int head_dim, int rope_half,
+                               int pair_stride, float sqrt_n, float n_eps,
+                               hipStream_t stream) {
+  (void)head_dim;
+  if (seq_len <= 0) return hipSuccess;
+  hipLaunchKernelGGL(bq_prep_kernel, dim3(seq_len), dim3(256), 0, stream, image,
+                     static_cast<const uint16_t*>(q_src), static_cast<const uint16_t*>(k_src),
+                     static_cast<const uint16_t*>(v_src), static_cast<const uint16_t*>(q_norm),
+                     static_cast<const uint16_t*>(k_norm), static_cast<int8_t*>(q_i8),
+                     qi_bias, f_q, static_cast<int8_t*>(k_cache), k_scale,
+                     static_cast<int8_t*>(v_cache), v_scale, cos_table, sin_table, num_q,
+                     num_kv, geom.shift, geom.row_mask, geom.page_mask, rope_half,
+                     pair_stride, sqrt_n, n_eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_units,
+                               int mode, const void* q_i8, const float* qi_bias,
+                               const float* f_q, const void* k_base, const float* k_scale,
+                               const void* v_base, const float* v_scale, void* output,
+                               float* partials, int64_t ps, int num_q, int num_kv,
+                               int head_dim, int64_t kv_stride, PagedGeom geom,
+                               hipStream_t stream) {
+  if (num_items > 0) {
+    dim3 grid(num_items, (num_kv + 3) / 4);
+    hipLaunchKernelGGL(bq_partial_kernel<2>, grid, dim3(256), 0, stream, image,
+                       static_cast<const int8_t*>(q_i8), qi_bias, f_q,
+                       static_cast<const int8_t*>(k_base), k_scale,
+                       static_cast<const int8_t*>(v_base), v_scale, partials, ps, num_q,
+                       num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return launch_merge(image, num_units, mode, partials, output, ps, num_q, head_dim, stream);
+}
+
+}  // namespace ifr

@@ -1,0 +1,119 @@
+// Shared device helpers and the plan-image layout for libinferno_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifr {
+
+// ---------------------------------------------------------------------------
+// Plan image layout (int32 words).  Built on the host by ifr_plan_attention,
+// uploaded once per step, read by the append, attention and merge kernels.
+// ---------------------------------------------------------------------------
+constexpr int32_t kPlanMagic = 0x49465231;  // "IFR1"
+enum PlanHeader : int {
+  kHdrMagic = 0,
+  kHdrNumRuns,
+  kHdrNumRows,
+  kHdrSeqLen,
+  kHdrNumItems,
+  kHdrNumUnits,
+  kHdrMode,
+  kHdrNumStripes,
+  kHdrOffRuns,
+  kHdrOffRows,
+  kHdrOffTokRun,
+  kHdrOffItems,
+  kHdrOffUnits,
+  kHdrTotalWords,
+  kHdrWords = 16
+};
+// A work item: one contiguous position range of one run, for every kv head.
+// {q_row, run, start_pos, start, end, stripe, 0, 0}
+constexpr int kItemWords = 8;
+// A merge unit: one output token row, for every q head.
+// {out_row, stripe_base, n_stripes, 0}
+constexpr int kUnitWords = 4;
+
+constexpr int kTile = 16;  // reference TILE = f32 SIMD width on AVX-512
+constexpr float kNegBig = -1e30f;
+
+// ---------------------------------------------------------------------------
+// Scalar numerics shared by every kernel.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t packed) {
+  return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t packed) {
+  return __uint_as_float(packed & 0xFFFF0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// Round-to-nearest-even f32 -> bf16 bits (butterquant/convert.mojo:14-17).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u + ((u >> 16) & 1u) + 0x7FFFu) >> 16;
+}
+
+// fast_exp_softmax_biased (simd_math/exponential.mojo:177-194), evaluated
+// with the same float operations in the same order (no contraction: the
+// library is compiled with -ffp-contract=off).
+__device__ __forceinline__ float fexp(float x) {
+  const float a_magic = 12102203.16156148f;
+  const float bias_f = 1059208216.0f;
+  const float inv_two23 = 1.0f / 8388608.0f;
+  const float qc_a = 1.6501418352127075f;
+  const float qc_b = -0.37554836273193359f;
+  const float qc_c = 0.38696467876434326f;
+  float t = a_magic * x;
+  t = t + bias_f;
+  int32_t i = static_cast<int32_t>(t);
+  uint32_t u = static_cast<uint32_t>(i);
+  float k = __uint_as_float(u);
+  float f = static_cast<float>(u & 0x7FFFFFu) * inv_two23;
+  float p = f * qc_c;
+  p = qc_b + p;
+  p = f * p;
+  p = qc_a + p;
+  return k * p;
+}
+
+__device__ __forceinline__ float max_ref(float a, float b) {
+  return a > b ? a : b;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers (wave64).
+// ---------------------------------------------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(
+      0, __float_as_int(v), kCtrl, 0xF, 0xF, true));
+}
+template <int kCtrl>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xF, 0xF, true);
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8 lanes
+constexpr int kDppRowRor8 = 0x128;     // lane i <- (i+8)%16 within 16 lanes
+
+__device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
+  int lane = __lane_id();
+  return __int_as_float(
+      __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ int shfl_xor_i32(int v, int mask) {
+  int lane = __lane_id();
+  return __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, v);
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int uniform_i32(int v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+}  // namespace ifr

@@ -1,0 +1,75 @@
+// Internal launch interface between the C ABI layer (api.hip) and the kernel
+// translation units.  Nothing here is exported.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifr {
+
+struct PagedGeom {
+  int shift;      // log2(page_len)
+  int row_mask;   // page_len - 1
+  int page_mask;  // ring pages - 1, or -1 for an unbounded page table
+};
+
+// Split-KV partials for every work item of the plan, then the merge units.
+hipError_t launch_attention_bf16(const int32_t* image_dev, int num_items,
+                                 int num_units, int mode, const void* q,
+                                 const void* k_base, const void* v_base,
+                                 void* output, float* partials,
+                                 int64_t partial_stride, int num_q, int num_kv,
+                                 int head_dim, int64_t kv_stride,
+                                 PagedGeom geom, hipStream_t stream);
+
+hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
+                               int num_units, int mode, const void* q_i8,
+                               const float* qi_bias, const float* f_q,
+                               const void* k_base, const float* k_scale,
+                               const void* v_base, const float* v_scale,
+                               void* output, float* partials,
+                               int64_t partial_stride, int num_q, int num_kv,
+                               int head_dim, int64_t kv_stride, PagedGeom geom,
+                               hipStream_t stream);
+
+hipError_t launch_merge(const int32_t* image_dev, int num_units, int mode,
+                        const float* partials, void* output,
+                        int64_t partial_stride, int num_q, int head_dim,
+                        hipStream_t stream);
+
+hipError_t launch_rope_cache_write(const int32_t* image_dev, int seq_len,
+                                   void* q, const void* k_src,
+                                   const void* v_src, void* k_cache,
+                                   void* v_cache, const float* cos_table,
+                                   const float* sin_table, int num_q,
+                                   int num_kv, PagedGeom geom, int half,
+                                   int pair_stride, int head_dim,
+                                   hipStream_t stream);
+
+hipError_t launch_bq_attn_prep(const int32_t* image_dev, int seq_len,
+                               const void* q_src, const void* k_src,
+                               const void* v_src, const void* q_norm,
+                               const void* k_norm, void* q_i8, float* qi_bias,
+                               float* f_q, void* k_cache, float* k_scale,
+                               void* v_cache, float* v_scale,
+                               const float* cos_table, const float* sin_table,
+                               int num_q, int num_kv, PagedGeom geom,
+                               int head_dim, int rope_half, int pair_stride,
+                               float sqrt_n, float n_eps, hipStream_t stream);
+
+// Copy chunks: int64 [n][4] = {src_off, dst_off, bytes, 0}.
+hipError_t launch_copy_chunks(void* arena, const int64_t* chunks_dev,
+                              int num_chunks, int aligned16,
+                              hipStream_t stream);
+
+hipError_t launch_gather_rows(const void* src, void* dst, const int32_t* rows,
+                              int num_rows, int cols, hipStream_t stream);
+
+hipError_t launch_fill_normal_bf16(void* dst, int64_t n, uint64_t seed,
+                                   int64_t outlier_every, float outlier_scale,
+                                   hipStream_t stream);
+
+// Head-dim / GQA pairs the attention kernels are compiled for.
+bool attention_shape_supported(int head_dim, int gqa);
+
+}  // namespace ifr
