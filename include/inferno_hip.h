@@ -158,6 +158,27 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
                            int64_t page_len, int64_t page_mask,
                            uint64_t stream);
 
+/* The two phases of ifr_attention_bf16 as separate launches: the split-KV
+ * partials (the FlashAttentionKernel fan-out of dispatch_flash_sliding /
+ * dispatch_flash_full, kernels/attention_dispatch_kernels.mojo:116-134) and
+ * the merge (dispatch_merge_flash_partials / dispatch_merge_batched_flash_
+ * partials, kernels/logsum_merge.mojo:205-248,331-365; with a token plan,
+ * the finalisation of kernels/flash_attention_prefill.mojo:95-106,251-286).
+ * The merge reads only the partials, so it serves the bf16 and the
+ * butterquant partials alike. */
+int32_t ifr_flash_partials_bf16(const void* image_dev, const int64_t* info,
+                                const void* q, const void* k_base,
+                                const void* v_base, void* partials,
+                                int64_t partials_bytes, int64_t num_q,
+                                int64_t num_kv, int64_t head_dim,
+                                int64_t partial_stride, int64_t kv_stride,
+                                int64_t page_len, int64_t page_mask,
+                                uint64_t stream);
+int32_t ifr_merge_flash_partials(const void* image_dev, const int64_t* info,
+                                 const void* partials, int64_t partials_bytes,
+                                 void* output, int64_t num_q, int64_t head_dim,
+                                 int64_t partial_stride, uint64_t stream);
+
 /* dispatch_sliding_attention (kernels/attention_dispatch_kernels.mojo:302-363)
  * with its argument list, plus the plan staging the GPU needs: the run table
  * is read from host memory, planned for `cap`, written to ws_host (pinned,

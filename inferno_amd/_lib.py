@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                    I64, I64, I64, I64, I64, I64, I64, U64]),
     "ifr_attention_bf16": (I32, [VP, P_I64, VP, VP, VP, VP, VP, I64, I64, I64, I64,
                                  I64, I64, I64, I64, U64]),
+    "ifr_flash_partials_bf16": (I32, [VP, P_I64, VP, VP, VP, VP, I64, I64, I64, I64, I64,
+                                      I64, I64, I64, U64]),
+    "ifr_merge_flash_partials": (I32, [VP, P_I64, VP, I64, VP, I64, I64, I64, U64]),
     "ifr_dispatch_sliding_attention": (I32, [VP, VP, VP, VP, VP, I64, P_I32, I64, P_I32,
                                              I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                              I64, I64, I64, VP, VP, I64, U64]),
@@ -77,6 +80,15 @@ def lib() -> C.CDLL:
         if not LIB_PATH.exists():
             raise FileNotFoundError(
                 f"{LIB_PATH} is missing: build it with `python -m inferno_amd.build`")
+        # The library and torch must share one HIP runtime: device pointers and
+        # stream handles cross between them.  torch ships its own libamdhip64
+        # (same soname, loaded under another name), so it has to be loaded
+        # first; the library's dependency then resolves to it.  Without torch
+        # (e.g. under the Mojo host) the system runtime is used.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         handle = C.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)

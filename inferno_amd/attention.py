@@ -56,6 +56,25 @@ def attention_bf16(plan: AttentionPlan, q, k_base, v_base, output, partials,
         partial_stride, kv_stride, plan.page_len, plan.page_mask, _stream()))
 
 
+def flash_partials_bf16(plan: AttentionPlan, q, k_base, v_base, partials,
+                        partial_stride: int, *, num_q: int, num_kv: int, head_dim: int,
+                        kv_stride: int) -> None:
+    """The split-KV partial phase alone (FlashAttentionKernel fan-out)."""
+    check(lib().ifr_flash_partials_bf16(
+        _ptr(plan.image), plan.info_ptr, _ptr(q), _ptr(k_base), _ptr(v_base),
+        _ptr(partials), partials.numel() * 4, num_q, num_kv, head_dim, partial_stride,
+        kv_stride, plan.page_len, plan.page_mask, _stream()))
+
+
+def merge_flash_partials(plan: AttentionPlan, partials, output, partial_stride: int, *,
+                         num_q: int, head_dim: int) -> None:
+    """dispatch_merge_batched_flash_partials (kernels/logsum_merge.mojo:331-365)
+    and the other merge/finalise routes, on the plan's merge units."""
+    check(lib().ifr_merge_flash_partials(
+        _ptr(plan.image), plan.info_ptr, _ptr(partials), partials.numel() * 4,
+        _ptr(output), num_q, head_dim, partial_stride, _stream()))
+
+
 def dispatch_sliding_attention(q, k_base, v_base, output, table: KVRunTable, *,
                                num_q: int, kv_stride: int, seq_len: int,
                                head_dim: int, gqa_ratio: int, window: int,
@@ -177,7 +196,8 @@ def bq_attention(plan: AttentionPlan, q_i8, qi_bias, f_q, k_base, k_scale, v_bas
 
 __all__ = [
     "SLIDING", "FULL", "KVRunTable", "AttentionPlan", "partials_buffer",
-    "dispatch_rope_cache_write", "attention_bf16", "dispatch_sliding_attention",
+    "dispatch_rope_cache_write", "attention_bf16", "flash_partials_bf16",
+    "merge_flash_partials", "dispatch_sliding_attention",
     "dispatch_full_attention", "dispatch_copy_jobs", "dispatch_gather_rows",
     "dispatch_bq_attn_prep", "bq_attention",
 ]

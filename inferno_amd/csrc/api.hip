@@ -601,6 +601,61 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
   return ok();
 }
 
+int32_t ifr_flash_partials_bf16(const void* image_dev, const int64_t* info,
+                                const void* q, const void* k_base, const void* v_base,
+                                void* partials, int64_t partials_bytes, int64_t num_q,
+                                int64_t num_kv, int64_t head_dim, int64_t partial_stride,
+                                int64_t kv_stride, int64_t page_len, int64_t page_mask,
+                                uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  st = check_attention_shapes(num_q, num_kv, head_dim, partial_stride, kv_stride, 2);
+  if (st) return st;
+  if (!image_dev || !q || !k_base || !v_base || !partials)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q, 16) || !aligned(k_base, 16) || !aligned(v_base, 16) || !aligned(partials, 16))
+    return fail(IFR_EINVAL, "q, k_base, v_base and partials must be 16-byte aligned");
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
+  st = check_geometry(info, pow2_shift(page_len), page_len - 1, page_mask);
+  if (st) return st;
+  if (partials_bytes < info[3] * partial_stride * 4)
+    return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
+  ifr::PagedGeom g{static_cast<int>(pow2_shift(page_len)), static_cast<int>(page_len - 1),
+                   static_cast<int>(page_mask)};
+  IFR_HIP(ifr::launch_partials_bf16(static_cast<const int32_t*>(image_dev),
+                                    static_cast<int>(info[0]), q, k_base, v_base,
+                                    static_cast<float*>(partials), partial_stride,
+                                    static_cast<int>(num_q), static_cast<int>(num_kv),
+                                    static_cast<int>(head_dim), kv_stride, g,
+                                    as_stream(stream)),
+          "flash_partials_bf16");
+  return ok();
+}
+
+int32_t ifr_merge_flash_partials(const void* image_dev, const int64_t* info,
+                                 const void* partials, int64_t partials_bytes,
+                                 void* output, int64_t num_q, int64_t head_dim,
+                                 int64_t partial_stride, uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (!image_dev || !partials || !output) return fail(IFR_EINVAL, "null pointer");
+  if (head_dim != 256 && head_dim != 512)
+    return fail(IFR_EUNSUPPORTED, "merge is compiled for head_dim 256 and 512");
+  if (num_q <= 0 || num_q > 64) return fail(IFR_EINVAL, "bad num_q");
+  if (partial_stride < num_q * head_dim + 2 * num_q)
+    return fail(IFR_EINVAL, "partial_stride too small");
+  if (!aligned(output, 16) || !aligned(partials, 16))
+    return fail(IFR_EINVAL, "output and partials must be 16-byte aligned");
+  if (partials_bytes < info[3] * partial_stride * 4)
+    return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
+  IFR_HIP(ifr::launch_merge(static_cast<const int32_t*>(image_dev), static_cast<int>(info[1]),
+                            static_cast<int>(info[2]), static_cast<const float*>(partials),
+                            output, partial_stride, static_cast<int>(num_q),
+                            static_cast<int>(head_dim), as_stream(stream)),
+          "merge_flash_partials");
+  return ok();
+}
+
 static int32_t dispatch_attention(int64_t kind, const void* q, const void* k_base,
                                   const void* v_base, void* output, void* partials,
                                   int64_t partials_bytes, const int32_t* runs,

@@ -365,29 +365,36 @@ hipError_t launch_merge(const int32_t* image, int num_units, int mode,
   return hipGetLastError();
 }
 
+hipError_t launch_partials_bf16(const int32_t* image, int num_items,
+                                const void* q, const void* k, const void* v,
+                                float* partials, int64_t ps, int num_q,
+                                int num_kv, int head_dim, int64_t kv_stride,
+                                PagedGeom geom, hipStream_t stream) {
+  if (num_items <= 0) return hipSuccess;
+  const int gqa = num_q / num_kv;
+  if (head_dim == 256 && gqa == 2)
+    return launch_partials<256, 2>(image, num_items, q, k, v, partials, ps,
+                                   num_q, num_kv, kv_stride, geom, stream);
+  if (head_dim == 256 && gqa == 1)
+    return launch_partials<256, 1>(image, num_items, q, k, v, partials, ps,
+                                   num_q, num_kv, kv_stride, geom, stream);
+  if (head_dim == 512 && gqa == 2)
+    return launch_partials<512, 2>(image, num_items, q, k, v, partials, ps,
+                                   num_q, num_kv, kv_stride, geom, stream);
+  return launch_partials<512, 1>(image, num_items, q, k, v, partials, ps,
+                                 num_q, num_kv, kv_stride, geom, stream);
+}
+
 hipError_t launch_attention_bf16(const int32_t* image, int num_items,
                                  int num_units, int mode, const void* q,
                                  const void* k, const void* v, void* output,
                                  float* partials, int64_t ps, int num_q,
                                  int num_kv, int head_dim, int64_t kv_stride,
                                  PagedGeom geom, hipStream_t stream) {
-  hipError_t err = hipSuccess;
-  if (num_items > 0) {
-    const int gqa = num_q / num_kv;
-    if (head_dim == 256 && gqa == 2)
-      err = launch_partials<256, 2>(image, num_items, q, k, v, partials, ps,
-                                    num_q, num_kv, kv_stride, geom, stream);
-    else if (head_dim == 256 && gqa == 1)
-      err = launch_partials<256, 1>(image, num_items, q, k, v, partials, ps,
-                                    num_q, num_kv, kv_stride, geom, stream);
-    else if (head_dim == 512 && gqa == 2)
-      err = launch_partials<512, 2>(image, num_items, q, k, v, partials, ps,
-                                    num_q, num_kv, kv_stride, geom, stream);
-    else
-      err = launch_partials<512, 1>(image, num_items, q, k, v, partials, ps,
-                                    num_q, num_kv, kv_stride, geom, stream);
-    if (err != hipSuccess) return err;
-  }
+  hipError_t err = launch_partials_bf16(image, num_items, q, k, v, partials, ps,
+                                        num_q, num_kv, head_dim, kv_stride,
+                                        geom, stream);
+  if (err != hipSuccess) return err;
   return launch_merge(image, num_units, mode, partials, output, ps, num_q,
                       head_dim, stream);
 }

@@ -22,6 +22,14 @@ hipError_t launch_attention_bf16(const int32_t* image_dev, int num_items,
                                  int head_dim, int64_t kv_stride,
                                  PagedGeom geom, hipStream_t stream);
 
+// The partial phase alone (no merge).
+hipError_t launch_partials_bf16(const int32_t* image_dev, int num_items,
+                                const void* q, const void* k_base,
+                                const void* v_base, float* partials,
+                                int64_t partial_stride, int num_q, int num_kv,
+                                int head_dim, int64_t kv_stride, PagedGeom geom,
+                                hipStream_t stream);
+
 hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
                                int num_units, int mode, const void* q_i8,
                                const float* qi_bias, const float* f_q,
