@@ -139,11 +139,14 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cap", type=int, default=2048)
+    ap.add_argument("--cap", type=int, default=512)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="one 1 GiB device-to-device copy (torch's copy kernel): the "
+                         "known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: every GPU box in this build has one MI355X, "
@@ -159,6 +162,16 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if a.copy_calibration:
+        n = 1 << 30
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "read_kib": n // 1024,
+                          "write_kib": n // 1024}))
+        return
     ctx, workload = config_contexts(a.config, a.seed)
     extra = 128 - 65 if a.config == 1 else 0
     table, pool, pages = build_case(ctx, a.seed, extra)
@@ -256,6 +269,15 @@ def main() -> None:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": nb["partials_kernel"]},
     }
+    traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                "traffic.json")
+    key = f"config{a.config}_cap{a.cap}"
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            measured = json.load(f).get(key)
+        if measured:
+            res["roofline"]["traffic"] = measured["traffic"]
+            res["roofline"]["traffic_source"] = measured["source"]
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, pages, k_cache, v_cache, q_host, a.cap,
                                            a.cpu_budget)
