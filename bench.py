@@ -1,17 +1,18 @@
-"""Benchmark of the MI355X paged-KV decode path (headline: config 2).
+"""Benchmark of the MI355X paged-KV attention path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cap C] [--config 2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--cap C]
 
-One step = one layer of batched paged decode: append one token per sequence
-(RoPE + paged cache write), split-KV flash-decode partials over every page of
-every sequence, and the log-sum-exp merge.  Inputs (KV cache pages, queries,
-RoPE tables, plan image) are resident in HBM before the timed region; the
-plan is built once, as the reference binds its run tables once per step for
-all layers.
+Headline (default): config 2 of BASELINE.json -- one layer of batched paged
+decode for 64 sequences with contexts ~ U[512, 32768]: append one token per
+sequence (RoPE + paged cache write), split-KV flash-decode partials over every
+page, log-sum-exp merge.  --config 1, 3 and 5 run the other decode configs
+(single sequence, sliding ring, butterquant int8) the same way.
 
-Prints ONE JSON line.  `value` is the whole step's algorithmic bytes divided
-by its wall time (GB/s); `roofline` covers the dominant kernel (the split-KV
-partial kernel) timed with HIP events on the launch stream; `cpu_baseline`
+Inputs (KV pages, queries, RoPE tables, the plan image) are resident in HBM
+before the timed region; the plan is built once, as the reference binds its
+run tables once per step for all layers.  Prints ONE JSON line: `value` is the
+step's algorithmic bytes over its wall time (GB/s); `roofline` covers the
+dominant kernel timed with HIP events on the launch stream; `cpu_baseline`
 times the CPU oracle (a C restatement of the reference's algorithm) on a
 bounded sample of the same batch on this host's cores.
 """
@@ -31,6 +32,7 @@ HBM_PEAK_GBS = 8000.0
 NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
+DEFAULT_CAP = {1: 128, 2: 512, 3: 512, 5: 512}
 
 
 def splitmix64(x: int) -> int:
@@ -40,37 +42,9 @@ def splitmix64(x: int) -> int:
     return z ^ (z >> 31)
 
 
-def config_contexts(config: int, seed: int) -> tuple[list[int], str]:
-    """Context lengths of the configured batch (SplitMix64 counter stream)."""
-    if config == 1:
-        return [4096], "config1: B=1, ctx 4096, 128-page pool, append 1 + decode"
-    if config == 2:
-        ctx = [512 + splitmix64(seed ^ splitmix64(i)) % 32257 for i in range(64)]
-        return ctx, ("config2: B=64 batched paged decode, ctx ~ U[512,32768], "
-                     "16q/8kv hd256 bf16, 64-token pages, append 1 + split-KV decode + merge")
-    raise SystemExit(f"unknown --config {config}")
-
-
-def build_case(ctx: list[int], seed: int, extra_pages: int = 0):
-    """Pages per sequence after the append, drawn from a seeded permutation of
-    one shared pool; the run table of the step (one token per sequence)."""
-    from inferno_amd.kv import KVRunTable
-
-    need = [(c + 1 + PAGE_LEN - 1) // PAGE_LEN for c in ctx]
-    pool = sum(need) + extra_pages
-    rng = np.random.default_rng(seed)
-    perm = rng.permutation(pool)
-    table = KVRunTable()
-    off = 0
-    pages = []
-    for i, c in enumerate(ctx):
-        table.begin_run(i, c)
-        pg = perm[off:off + need[i]]
-        off += need[i]
-        pages.append(pg)
-        for p in pg:
-            table.add_base_row(int(p) * PAGE_LEN)
-    return table, pool, pages
+def uniform_ints(seed: int, n: int, lo: int, hi: int) -> list[int]:
+    """n integers in [lo, hi] from the SplitMix64 counter stream."""
+    return [lo + splitmix64(seed ^ splitmix64(i)) % (hi - lo + 1) for i in range(n)]
 
 
 def rope_tables(max_pos: int, half: int = 128, theta: float = 10000.0):
@@ -79,59 +53,318 @@ def rope_tables(max_pos: int, half: int = 128, theta: float = 10000.0):
     return np.cos(ang).astype(np.float32).reshape(-1), np.sin(ang).astype(np.float32).reshape(-1)
 
 
-def step_bytes(ctx: list[int], pages: int) -> dict:
-    B = len(ctx)
-    kv = sum(c + 1 for c in ctx) * KV_STRIDE * 2 * 2
-    q = B * NUM_Q * HEAD_DIM * 2
-    out = q
-    table = 4 * pages
-    append = B * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 2)
-    return {"kv": kv, "q": q, "out": out, "table": table, "append": append,
-            "decode": kv + q + out + table, "step": kv + q + out + table + append,
-            "partials_kernel": kv + q + table}
+def _fill(t, seed, sid, outlier_every=0, scale=1.0):
+    from inferno_amd._lib import check, lib
+
+    check(lib().ifr_fill_normal_bf16(t.data_ptr(), t.numel() * t.element_size() // 2, seed,
+                                     outlier_every, scale, sid))
 
 
-def cpu_baseline(ctx, pages_list, k_dev, v_dev, q_host, cap_unused, budget_s: float):
-    """Times the CPU oracle on a bounded sample of the batch (the first
-    sequences, their pages copied from HBM into a compact host cache)."""
+class DecodeBf16:
+    """Configs 1-3: bf16 append + split-KV decode + merge."""
+
+    dtype = "bf16"
+    phases = ("append", "partials", "merge")
+    dominant = "flash_partial_bf16_kernel<256,2>"
+
+    def __init__(self, config: int, seed: int):
+        self.cfg, self.seed = config, seed
+        if config == 1:
+            self.pos = [4096]
+            self.kind, self.window, self.ring = 1, 0, 0
+            self.extra_pages = 128 - 65
+            self.name = ("config1: B=1 paged decode, ctx 4096 in a shuffled 128-page pool, "
+                         "16q/8kv hd256 bf16, append 1 + split-KV decode + merge")
+        elif config == 2:
+            self.pos = uniform_ints(seed, 64, 512, 32768)
+            self.kind, self.window, self.ring = 1, 0, 0
+            self.extra_pages = 0
+            self.name = ("config2: B=64 batched paged decode, ctx ~ U[512,32768], "
+                         "16q/8kv hd256 bf16, 64-token pages, append 1 + split-KV decode + merge")
+        else:
+            self.pos = uniform_ints(seed, 64, 1023, 32767)
+            self.kind, self.window, self.ring = 0, 1024, 32
+            self.extra_pages = 0
+            self.name = ("config3: B=64 sliding-window decode, window 1024 over 32-page rings, "
+                         "positions ~ U[1023,32767], 16q/8kv hd256 bf16, append 1 + decode + merge")
+
+    def setup(self, dev, a):
+        import torch
+
+        from inferno_amd import attention as A
+        from inferno_amd.kv import AttentionPlan, KVRunTable
+
+        self.A = A
+        B = len(self.pos)
+        table = KVRunTable()
+        self.pages = []
+        if self.ring:
+            # KVPageAccountant.admit hands each sequence its fixed ring pages in
+            # acquire order (continuous_batching/paging.mojo:156-170): the LIFO
+            # stack starts n-1..0, so sequence s holds pages ring*s .. ring*s+ring-1.
+            pool = B * self.ring
+            for i, p in enumerate(self.pos):
+                table.begin_run(i, p)
+                pg = list(range(self.ring * i, self.ring * (i + 1)))
+                self.pages.append(pg)
+                for x in pg:
+                    table.add_base_row(x * PAGE_LEN)
+            cache_size = self.ring * PAGE_LEN
+        else:
+            need = [(p + 1 + PAGE_LEN - 1) // PAGE_LEN for p in self.pos]
+            pool = sum(need) + self.extra_pages
+            perm = np.random.default_rng(self.seed).permutation(pool)
+            off = 0
+            for i, p in enumerate(self.pos):
+                table.begin_run(i, p)
+                pg = perm[off:off + need[i]]
+                off += need[i]
+                self.pages.append(list(pg))
+                for x in pg:
+                    table.add_base_row(int(x) * PAGE_LEN)
+            cache_size = PAGE_LEN
+        self.pool, self.table = pool, table
+        self.cache_size = cache_size
+        rows = pool * PAGE_LEN
+        self.stream = torch.cuda.current_stream()
+        sid = int(self.stream.cuda_stream)
+        self.k = torch.empty(rows * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.v = torch.empty_like(self.k)
+        self.q = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.ks = torch.empty(B * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.vs = torch.empty_like(self.ks)
+        for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
+            _fill(t, self.seed * 16 + i, sid)
+        cos, sin = rope_tables(max(self.pos) + 2)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        self.plan = AttentionPlan(table, B, kind=self.kind, window=self.window,
+                                  cache_size=cache_size, page_len=PAGE_LEN, cache_rows=rows,
+                                  cap=a.cap, kv_row_bytes=KV_STRIDE * 2, device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
+        self.out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.q_host = self.q.cpu().numpy().view(np.uint16).copy()
+        self.cap = a.cap
+
+    def launch(self, phase):
+        A, p = self.A, self.plan
+        if phase == "append":
+            A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
+                                        self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
+                                        pair_stride=128, head_dim=HEAD_DIM)
+        elif phase == "partials":
+            A.flash_partials_bf16(p, self.q, self.k, self.v, self.partials, self.ps,
+                                  num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
+                                  kv_stride=KV_STRIDE)
+        else:
+            A.merge_flash_partials(p, self.partials, self.out, self.ps, num_q=NUM_Q,
+                                   head_dim=HEAD_DIM)
+
+    def kv_positions(self, pos=None) -> int:
+        pos = self.pos if pos is None else pos
+        if self.kind == 0:
+            return sum(min(p + 1, self.window) for p in pos)
+        return sum(p + 1 for p in pos)
+
+    def dominant_bytes(self) -> int:
+        """Partial kernel: K+V of every attended position, q and the page table."""
+        B = len(self.pos)
+        return (self.kv_positions() * KV_STRIDE * 4 + B * NUM_Q * HEAD_DIM * 2
+                + 4 * len(self.table.base_rows))
+
+    def step_bytes(self) -> int:
+        """Whole step: the partial kernel's bytes, the output and the append."""
+        B = len(self.pos)
+        append = B * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 2)
+        return self.dominant_bytes() + B * NUM_Q * HEAD_DIM * 2 + append
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": len(self.pos),
+                "attended_positions": self.kv_positions(), "pool_pages": self.pool,
+                "page_len": PAGE_LEN, "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM,
+                "window": self.window or None, "cap": self.cap, "seed": self.seed,
+                "plan_items": self.plan.summary.num_items}
+
+    def cpu_baseline(self, budget_s):
+        import torch
+
+        import oracle
+
+        threads = min(16, os.cpu_count() or 1)
+        n_seq = min(len(self.pos), max(threads, 8))
+        pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
+        idx = torch.from_numpy(pages.astype(np.int64)).to(self.k.device)
+        kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
+        vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
+        runs, rows, off = [], [], 0
+        for i in range(n_seq):
+            n = len(self.pages[i])
+            runs.append([i, self.pos[i], off, n])
+            rows.extend((off + j) * PAGE_LEN for j in range(n))
+            off += n
+        runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
+        q = np.ascontiguousarray(self.q_host[:n_seq * NUM_Q * HEAD_DIM])
+        sample_pos = self.kv_positions(self.pos[:n_seq])
+        nbytes = sample_pos * KV_STRIDE * 4
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.attention(self.kind, runs, rows, q, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
+                             head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=self.window,
+                             cache_size=self.cache_size, page_len=PAGE_LEN, seq_len=n_seq,
+                             cap=threads, threads=threads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "port",
+                "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
+                           f"({nbytes / 1e9:.3f} GB of K+V), the reference's routing at "
+                           f"cap={threads} workers, median of {len(times)}"),
+                "us_per_layer_equiv": round(med * 1e6 * self.kv_positions() / sample_pos, 1)}
+
+
+class DecodeBq:
+    """Config 5: butterquant int8 KV -- quantizing append + int8 decode + merge."""
+
+    dtype = "int8 KV (f32 scales), f32 accumulate"
+    phases = ("append", "attention")
+    dominant = "bq_partial_kernel<2> + merge_kernel<256>"
+
+    def __init__(self, seed: int):
+        self.seed = seed
+        self.pos = uniform_ints(seed, 128, 1024, 65536)
+        self.name = ("config5: B=128 butterquant decode, ctx ~ U[1024,65536], 16q/8kv hd256, "
+                     "int8 FWHT-256 codes + f32 per-(position, kv head) scales (the reference's "
+                     "bq format), quantizing append 1 + int8 split-KV decode + merge")
+
+    def setup(self, dev, a):
+        import torch
+
+        from inferno_amd import attention as A
+        from inferno_amd.kv import AttentionPlan, KVRunTable
+
+        self.A = A
+        B = len(self.pos)
+        need = [(p + 1 + PAGE_LEN - 1) // PAGE_LEN for p in self.pos]
+        pool = sum(need)
+        perm = np.random.default_rng(self.seed).permutation(pool)
+        table = KVRunTable()
+        off = 0
+        for i, p in enumerate(self.pos):
+            table.begin_run(i, p)
+            for x in perm[off:off + need[i]]:
+                table.add_base_row(int(x) * PAGE_LEN)
+            off += need[i]
+        rows = pool * PAGE_LEN
+        self.pool, self.table = pool, table
+        self.stream = torch.cuda.current_stream()
+        sid = int(self.stream.cuda_stream)
+        self.kc = torch.empty(rows * KV_STRIDE, dtype=torch.int8, device=dev)
+        self.vc = torch.empty_like(self.kc)
+        _fill(self.kc, self.seed * 16 + 1, sid)
+        _fill(self.vc, self.seed * 16 + 2, sid)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(self.seed)
+        self.ksc = torch.rand(rows * NUM_KV, device=dev, generator=gen) * 4 + 0.5
+        self.vsc = torch.rand(rows * NUM_KV, device=dev, generator=gen) * 4 + 0.5
+        self.qs = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.kss = torch.empty(B * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.vss = torch.empty_like(self.kss)
+        for i, t in enumerate((self.qs, self.kss, self.vss)):
+            _fill(t, self.seed * 16 + 3 + i, sid, outlier_every=100, scale=20.0)
+        self.qn = torch.full((HEAD_DIM,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
+        self.kn = self.qn
+        cos, sin = rope_tables(max(self.pos) + 2)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        self.q_i8 = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int8, device=dev)
+        self.qb = torch.empty(B * NUM_Q, dtype=torch.float32, device=dev)
+        self.fq = torch.empty_like(self.qb)
+        self.plan = AttentionPlan(table, B, kind=1, window=0, cache_size=PAGE_LEN,
+                                  page_len=PAGE_LEN, cache_rows=rows, cap=a.cap,
+                                  kv_row_bytes=KV_STRIDE, device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
+        self.out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.cap = a.cap
+
+    def launch(self, phase):
+        A, p = self.A, self.plan
+        if phase == "append":
+            A.dispatch_bq_attn_prep(p, self.qs, self.kss, self.vss, self.qn, self.kn,
+                                    self.q_i8, self.qb, self.fq, self.kc, self.ksc, self.vc,
+                                    self.vsc, self.cos, self.sin, num_q=NUM_Q, num_kv=NUM_KV,
+                                    head_dim=HEAD_DIM, rope_half=128, pair_stride=128,
+                                    sqrt_n=16.0,
+                                    n_eps=float(np.float32(256) * np.float32(1e-6)))
+        else:
+            A.bq_attention(p, self.q_i8, self.qb, self.fq, self.kc, self.ksc, self.vc,
+                           self.vsc, self.out, self.partials, self.ps, num_q=NUM_Q,
+                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE)
+
+    def dominant_bytes(self) -> int:
+        B = len(self.pos)
+        kv = sum(p + 1 for p in self.pos) * (KV_STRIDE * 2 + NUM_KV * 4 * 2)
+        return (kv + B * NUM_Q * (HEAD_DIM + 8) + 4 * len(self.table.base_rows)
+                + B * NUM_Q * HEAD_DIM * 2)
+
+    def step_bytes(self) -> int:
+        B = len(self.pos)
+        append = B * ((NUM_Q + 2 * NUM_KV) * HEAD_DIM * 2 + (NUM_Q + 2 * NUM_KV) * HEAD_DIM)
+        return self.dominant_bytes() + append
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": len(self.pos),
+                "attended_positions": sum(p + 1 for p in self.pos), "pool_pages": self.pool,
+                "page_len": PAGE_LEN, "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM,
+                "cap": self.cap, "seed": self.seed, "plan_items": self.plan.summary.num_items}
+
+    def cpu_baseline(self, budget_s):
+        return None
+
+
+def measure(w, steps: int, warmup: int):
     import torch
 
-    import oracle
+    stream = w.stream
+    for _ in range(warmup):
+        for ph in w.phases:
+            w.launch(ph)
+    torch.cuda.synchronize()
+    # Timed region 1: wall clock over K steps, nothing but the step's launches.
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for ph in w.phases:
+            w.launch(ph)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # Timed region 2: the same K steps with HIP events between the kernels.
+    n = len(w.phases)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        evs[i][0].record(stream)
+        for j, ph in enumerate(w.phases):
+            w.launch(ph)
+            evs[i][j + 1].record(stream)
+    torch.cuda.synchronize()
+    per = {ph: statistics.mean(e[j].elapsed_time(e[j + 1]) * 1e3 for e in evs)
+           for j, ph in enumerate(w.phases)}
+    per["step"] = statistics.mean(e[0].elapsed_time(e[n]) * 1e3 for e in evs)
+    return wall, per
 
-    threads = min(16, os.cpu_count() or 1)
-    n_seq = min(len(ctx), max(threads, 8))
-    sample_ctx = ctx[:n_seq]
-    pages = np.concatenate([np.asarray(p) for p in pages_list[:n_seq]])
-    idx = torch.from_numpy(pages.astype(np.int64)).to(k_dev.device)
-    kp = k_dev.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy().view(np.uint16)
-    vp = v_dev.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy().view(np.uint16)
-    runs, rows, off = [], [], 0
-    for i, c in enumerate(sample_ctx):
-        n = len(pages_list[i])
-        runs.append([i, c, off, n])
-        rows.extend((off + j) * PAGE_LEN for j in range(n))
-        off += n
-    runs = np.asarray(runs, dtype=np.int32)
-    rows = np.asarray(rows, dtype=np.int32)
-    q = np.ascontiguousarray(q_host[:n_seq * NUM_Q * HEAD_DIM])
-    kp, vp = np.ascontiguousarray(kp.reshape(-1)), np.ascontiguousarray(vp.reshape(-1))
-    nbytes = sum(c + 1 for c in sample_ctx) * KV_STRIDE * 2 * 2
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 and (not times or time.perf_counter() < t_end):
-        t0 = time.perf_counter()
-        oracle.attention(1, runs, rows, q, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
-                         head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
-                         cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n_seq,
-                         cap=threads, threads=threads)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"first {n_seq} of the {len(ctx)} sequences ({nbytes / 1e9:.2f} GB of K+V), "
-                       f"reference routing at cap={threads} workers, median of {len(times)}"),
-            "us_per_layer_equiv": round(med * 1e6 * sum(c + 1 for c in ctx)
-                                        / sum(c + 1 for c in sample_ctx), 1)}
+
+def copy_calibration(dev) -> None:
+    import torch
+
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "read_kib": n // 1024,
+                      "write_kib": n // 1024}))
 
 
 def main() -> None:
@@ -139,8 +372,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cap", type=int, default=512)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 5))
+    ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -153,93 +386,23 @@ def main() -> None:
               f"so --gpus {a.gpus} is not run (the path shards by sequence; see DESIGN.md).",
               file=sys.stderr)
         sys.exit(2)
-
     import torch
-
-    from inferno_amd import attention as A
-    from inferno_amd._lib import check, lib
-    from inferno_amd.kv import FULL, AttentionPlan
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if a.copy_calibration:
-        n = 1 << 30
-        src = torch.ones(n, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes": n, "read_kib": n // 1024,
-                          "write_kib": n // 1024}))
+        copy_calibration(dev)
         return
-    ctx, workload = config_contexts(a.config, a.seed)
-    extra = 128 - 65 if a.config == 1 else 0
-    table, pool, pages = build_case(ctx, a.seed, extra)
-    B = len(ctx)
-    rows_cache = pool * PAGE_LEN
-    stream = torch.cuda.current_stream()
-    sid = int(stream.cuda_stream)
-
-    k_cache = torch.empty(rows_cache * KV_STRIDE, dtype=torch.int16, device=dev)
-    v_cache = torch.empty_like(k_cache)
-    q = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
-    k_src = torch.empty(B * KV_STRIDE, dtype=torch.int16, device=dev)
-    v_src = torch.empty_like(k_src)
-    for i, t in enumerate((k_cache, v_cache, q, k_src, v_src)):
-        check(lib().ifr_fill_normal_bf16(t.data_ptr(), t.numel(), a.seed * 16 + i, 0, 1.0, sid))
-    cos, sin = rope_tables(max(ctx) + 2)
-    cos_d, sin_d = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
-    plan = AttentionPlan(table, B, kind=FULL, window=0, cache_size=PAGE_LEN,
-                         page_len=PAGE_LEN, cache_rows=rows_cache, cap=a.cap,
-                         kv_row_bytes=KV_STRIDE * 2, device=dev)
-    partials, ps = A.partials_buffer(plan, NUM_Q, HEAD_DIM)
-    out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
-    q_host = q.cpu().numpy().view(np.uint16).copy()
+    if a.cap <= 0:
+        a.cap = DEFAULT_CAP[a.config]
+    w = DecodeBq(a.seed) if a.config == 5 else DecodeBf16(a.config, a.seed)
+    w.setup(dev, a)
     torch.cuda.synchronize()
-
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
-        A.dispatch_rope_cache_write(plan, q, k_src, v_src, k_cache, v_cache, cos_d, sin_d,
-                                    num_q=NUM_Q, num_kv=NUM_KV, half=128, pair_stride=128,
-                                    head_dim=HEAD_DIM)
-        if ev is not None:
-            ev[1].record(stream)
-        A.flash_partials_bf16(plan, q, k_cache, v_cache, partials, ps, num_q=NUM_Q,
-                              num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE)
-        if ev is not None:
-            ev[2].record(stream)
-        A.merge_flash_partials(plan, partials, out, ps, num_q=NUM_Q, head_dim=HEAD_DIM)
-        if ev is not None:
-            ev[3].record(stream)
-
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # Timed region 1: wall clock over K steps, nothing but the step's launches.
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
-    # Timed region 2: the same K steps with HIP events between the kernels.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
-    torch.cuda.synchronize()
-    for i in range(a.steps):
-        step(evs[i])
-    torch.cuda.synchronize()
-    t_app = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
-    t_par = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
-    t_mrg = [e[2].elapsed_time(e[3]) * 1e3 for e in evs]
-    t_all = [e[0].elapsed_time(e[3]) * 1e3 for e in evs]
-
-    nb = step_bytes(ctx, len(table.base_rows))
+    wall, per = measure(w, a.steps, a.warmup)
     ms_per_step = wall / a.steps * 1e3
-    value = nb["step"] / (wall / a.steps) / 1e9
-    par_us = statistics.mean(t_par)
-    achieved = nb["partials_kernel"] / (par_us * 1e-6) / 1e9
+    value = w.step_bytes() / (wall / a.steps) / 1e9
+    dom_us = per["partials"] if "partials" in per else per["attention"]
+    achieved = w.dominant_bytes() / (dom_us * 1e-6) / 1e9
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -251,23 +414,17 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded SplitMix64/Box-Muller N(0,1) bf16 on device)",
-        "config": {"workload": workload, "batch": B, "context_tokens": int(sum(ctx)),
-                   "pool_pages": pool, "page_len": PAGE_LEN, "num_q": NUM_Q,
-                   "num_kv": NUM_KV, "head_dim": HEAD_DIM, "cap": a.cap,
-                   "seed": a.seed, "plan_items": plan.summary.num_items},
+        "dtype": w.dtype,
+        "data": "synthetic (seeded SplitMix64/Box-Muller N(0,1) on device)",
+        "config": w.config(),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "us_per_layer": round(ms_per_step * 1e3, 2),
-        "us_breakdown_events": {"append": round(statistics.mean(t_app), 2),
-                                "partials": round(par_us, 2),
-                                "merge": round(statistics.mean(t_mrg), 2),
-                                "step": round(statistics.mean(t_all), 2)},
-        "step_bytes": nb["step"],
-        "roofline": {"bound": "hbm", "kernel": "flash_partial_bf16_kernel<256,2>",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "us_breakdown_events": {k: round(v, 2) for k, v in per.items()},
+        "step_bytes": w.step_bytes(),
+        "roofline": {"bound": "hbm", "kernel": w.dominant, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": nb["partials_kernel"]},
+                     "bytes_per_launch": w.dominant_bytes()},
     }
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 "traffic.json")
@@ -279,8 +436,9 @@ def main() -> None:
             res["roofline"]["traffic"] = measured["traffic"]
             res["roofline"]["traffic_source"] = measured["source"]
     if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(ctx, pages, k_cache, v_cache, q_host, a.cap,
-                                           a.cpu_budget)
+        cb = w.cpu_baseline(a.cpu_budget)
+        if cb is not None:
+            res["cpu_baseline"] = cb
     print(json.dumps(res), flush=True)
 
 
