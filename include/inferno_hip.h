@@ -115,7 +115,9 @@ int64_t ifr_plan_bytes(int64_t num_runs, int64_t num_rows, int64_t seq_len,
  *   info[6] = num_runs                    info[7] = page shift
  *   info[8] = row mask                    info[9] = page mask (-1 = full)
  *   info[10] = cache_rows                 info[11] = kind
- *   info[12] = window                     info[13..15] = 0
+ *   info[12] = window                     info[13] = 0
+ *   info[14] = MFMA prefill query blocks (token plans of full attention)
+ *   info[15] = 0
  * Every launch entry point below takes the same info and refuses a page
  * geometry other than the one the plan was validated for. */
 #define IFR_INFO_LEN 16

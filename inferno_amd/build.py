@@ -29,7 +29,7 @@ LIB = PKG / "libinferno_hip.so"
 OBJ_DIR = PKG.parent / "_build" / "obj"
 ARCH = "gfx950"
 
-SOURCES = ["api.hip", "attention.hip", "append.hip", "copy.hip", "bq.hip"]
+SOURCES = ["api.hip", "attention.hip", "append.hip", "copy.hip", "bq.hip", "prefill.hip"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <string>
 #include <vector>
 
@@ -143,8 +144,9 @@ int64_t plan_words(int64_t num_runs, int64_t num_rows, int64_t seq_len,
                    int64_t cap) {
   const int64_t items = std::max<int64_t>({cap, seq_len, 1});
   const int64_t units = std::max<int64_t>({seq_len, num_runs, 1});
+  const int64_t qblocks = seq_len / ifr::kPrefillTokens + num_runs + 1;
   return ifr::kHdrWords + 4 * num_runs + num_rows + std::max<int64_t>(seq_len, 1) +
-         ifr::kItemWords * items + ifr::kUnitWords * units;
+         ifr::kItemWords * items + ifr::kUnitWords * units + ifr::kQBlockWords * qblocks;
 }
 
 // Validates a host run table against the cache geometry and the positions
@@ -338,6 +340,30 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
     un[3] = 0;
   }
   off += n_units * kUnitWords;
+  // Query blocks for the MFMA prefill (token plans of full attention).
+  hdr[kHdrOffQBlocks] = static_cast<int32_t>(off);
+  int64_t n_qblocks = 0;
+  if (mode == IFR_PLAN_TOKEN_MERGE) {
+    std::vector<std::array<int64_t, 4>> qbs;
+    for (int64_t r = 0; r < num_runs; ++r) {
+      const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
+      for (int64_t t = b; t < e; t += kPrefillTokens) {
+        const int64_t n = std::min<int64_t>(kPrefillTokens, e - t);
+        qbs.push_back({r, t, n, runs[4 * r + 1] + (t + n - 1 - b) + 1});
+      }
+    }
+    std::stable_sort(qbs.begin(), qbs.end(),
+                     [](const std::array<int64_t, 4>& a, const std::array<int64_t, 4>& b) {
+                       return a[3] > b[3];
+                     });
+    for (const auto& qb : qbs) {
+      int32_t* w = img + off + n_qblocks * kQBlockWords;
+      for (int i = 0; i < 4; ++i) w[i] = static_cast<int32_t>(qb[i]);
+      ++n_qblocks;
+    }
+  }
+  off += n_qblocks * kQBlockWords;
+  hdr[kHdrNumQBlocks] = static_cast<int32_t>(n_qblocks);
   hdr[kHdrMagic] = kPlanMagic;
   hdr[kHdrNumRuns] = static_cast<int32_t>(num_runs);
   hdr[kHdrNumRows] = static_cast<int32_t>(num_rows);
@@ -360,7 +386,9 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   info[10] = cache_rows;
   info[11] = kind;
   info[12] = window;
-  info[13] = info[14] = info[15] = 0;
+  info[13] = 0;
+  info[14] = n_qblocks;
+  info[15] = 0;
   return ok();
 }
 
@@ -590,6 +618,17 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
     return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
   ifr::PagedGeom g{static_cast<int>(pow2_shift(page_len)), static_cast<int>(page_len - 1),
                    static_cast<int>(page_mask)};
+  if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 256 &&
+      num_q == 2 * num_kv && page_mask < 0) {
+    // Prefill chunk of full attention: MFMA query blocks, finalised in-kernel.
+    IFR_HIP(ifr::launch_prefill_full_mfma(static_cast<const int32_t*>(image_dev),
+                                          static_cast<int>(info[14]), q, k_base, v_base,
+                                          output, static_cast<int>(num_q),
+                                          static_cast<int>(num_kv), kv_stride, g,
+                                          as_stream(stream)),
+            "prefill_full_mfma");
+    return ok();
+  }
   IFR_HIP(ifr::launch_attention_bf16(static_cast<const int32_t*>(image_dev),
                                      static_cast<int>(info[0]), static_cast<int>(info[1]),
                                      static_cast<int>(info[2]), q, k_base, v_base, output,

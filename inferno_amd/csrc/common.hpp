@@ -26,6 +26,8 @@ enum PlanHeader : int {
   kHdrOffItems,
   kHdrOffUnits,
   kHdrTotalWords,
+  kHdrOffQBlocks,
+  kHdrNumQBlocks,
   kHdrWords = 16
 };
 // A work item: one contiguous position range of one run, for every kv head.
@@ -34,6 +36,12 @@ constexpr int kItemWords = 8;
 // A merge unit: one output token row, for every q head.
 // {out_row, stripe_base, n_stripes, 0}
 constexpr int kUnitWords = 4;
+
+// Query blocks of a token (prefill) plan for the MFMA prefill kernel:
+// {run, first token, token count, last token's position + 1}, at most
+// kPrefillTokens consecutive tokens of one run, longest key range first.
+constexpr int kQBlockWords = 4;
+constexpr int kPrefillTokens = 32;
 
 constexpr int kTile = 16;  // reference TILE = f32 SIMD width on AVX-512
 constexpr float kNegBig = -1e30f;

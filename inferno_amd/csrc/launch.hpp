@@ -30,6 +30,14 @@ hipError_t launch_partials_bf16(const int32_t* image_dev, int num_items,
                                 int head_dim, int64_t kv_stride, PagedGeom geom,
                                 hipStream_t stream);
 
+// MFMA chunked prefill, full attention, head_dim 256, gqa 2: writes the
+// finalised output of every query block of a token plan.
+hipError_t launch_prefill_full_mfma(const int32_t* image_dev, int num_qblocks,
+                                    const void* q, const void* k_base,
+                                    const void* v_base, void* output, int num_q,
+                                    int num_kv, int64_t kv_stride, PagedGeom geom,
+                                    hipStream_t stream);
+
 hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
                                int num_units, int mode, const void* q_i8,
                                const float* qi_bias, const float* f_q,

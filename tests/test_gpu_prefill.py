@@ -1,0 +1,114 @@
+"""GPU parity of chunked prefill over the paged cache (full attention):
+append of the chunk (RoPE + cache write, bit-exact), then the MFMA prefill
+kernel against the oracle's token-partitioned route
+(FlashPrefillFullKernel + PrefillMergeKernel) within 1e-2 / one bf16 spacing."""
+import numpy as np
+import pytest
+
+import oracle
+from inferno_amd import attention as A
+from inferno_amd.kv import FULL, AttentionPlan, KVRunTable
+from tests.gpu_util import announce, empty_dev, from_dev, to_dev
+from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, compare_bf16,
+                           make_prefill_case, seeded_bf16)
+
+pytestmark = pytest.mark.gpu
+
+
+def _table(runs, rows) -> KVRunTable:
+    t = KVRunTable()
+    for r in runs:
+        t.begin_run(int(r[0]), int(r[1]))
+        for j in range(int(r[3])):
+            t.add_base_row(int(rows[int(r[2]) + j]))
+    return t
+
+
+def _prefill(case, n, q, k, v, cap=16):
+    plan = AttentionPlan(_table(case.runs, case.base_rows), n, kind=FULL, window=0,
+                         cache_size=PAGE_LEN, page_len=PAGE_LEN, cache_rows=case.cache_rows,
+                         cap=cap, kv_row_bytes=KV_STRIDE * 2)
+    assert plan.summary.mode == 2 and int(plan.info[14]) > 0
+    out = empty_dev(n * NUM_Q * HEAD_DIM, np.uint16)
+    partials, ps = A.partials_buffer(plan, NUM_Q, HEAD_DIM)
+    A.attention_bf16(plan, q, k, v, out, partials, ps, num_q=NUM_Q, num_kv=NUM_KV,
+                     head_dim=HEAD_DIM, kv_stride=KV_STRIDE)
+    return from_dev(out, np.uint16)
+
+
+def test_prefill_small_all_tokens():
+    announce("prefill small")
+    prefix, new = [0, 100, 1000, 3000, 63], [40, 33, 100, 64, 1]
+    case = make_prefill_case(3, prefix, new)
+    n = sum(new)
+    q = seeded_bf16(n * NUM_Q * HEAD_DIM, 1)
+    k = seeded_bf16(case.cache_rows * KV_STRIDE, 2)
+    v = seeded_bf16(case.cache_rows * KV_STRIDE, 3)
+    got = _prefill(case, n, to_dev(q), to_dev(k), to_dev(v))
+    ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=NUM_Q,
+                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
+                           cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n, cap=16,
+                           threads=8)
+    r = compare_bf16(got, ref)
+    print(f"  prefill small: {r}", flush=True)
+    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+
+
+def test_prefill_config4_shape_append_then_attend():
+    """Config 4: 8 sequences append 2048 tokens each onto prefixes ~ U[0,16384]
+    (RoPE + cache write for the whole chunk, then causal prefill).  The cache
+    writes are compared whole (bit-exact); attention outputs are checked for
+    sampled query tokens against the oracle's token route."""
+    announce("prefill config4 shape")
+    rng = np.random.default_rng(44)
+    prefix = [int(x) for x in rng.integers(0, 16385, 8)]
+    new = [2048] * 8
+    case = make_prefill_case(45, prefix, new)
+    n = sum(new)
+    k = seeded_bf16(case.cache_rows * KV_STRIDE, 4)
+    v = seeded_bf16(case.cache_rows * KV_STRIDE, 5)
+    q = seeded_bf16(n * NUM_Q * HEAD_DIM, 6)
+    ks, vs = seeded_bf16(n * KV_STRIDE, 7), seeded_bf16(n * KV_STRIDE, 8)
+    maxpos = max(p + m for p, m in zip(prefix, new)) + 1
+    ang = rng.uniform(-3, 3, maxpos * 128)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    plan = AttentionPlan(_table(case.runs, case.base_rows), n, kind=FULL, window=0,
+                         cache_size=PAGE_LEN, page_len=PAGE_LEN, cache_rows=case.cache_rows,
+                         cap=16, kv_row_bytes=KV_STRIDE * 2)
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    A.dispatch_rope_cache_write(plan, qd, to_dev(ks), to_dev(vs), kd, vd, to_dev(cos),
+                                to_dev(sin), num_q=NUM_Q, num_kv=NUM_KV, half=128,
+                                pair_stride=128, head_dim=HEAD_DIM)
+    out = empty_dev(n * NUM_Q * HEAD_DIM, np.uint16)
+    partials, ps = A.partials_buffer(plan, NUM_Q, HEAD_DIM)
+    A.attention_bf16(plan, qd, kd, vd, out, partials, ps, num_q=NUM_Q, num_kv=NUM_KV,
+                     head_dim=HEAD_DIM, kv_stride=KV_STRIDE)
+    got = from_dev(out, np.uint16).reshape(n, NUM_Q * HEAD_DIM)
+    q_ref, k_ref, v_ref = q.copy(), k.copy(), v.copy()
+    oracle.rope_cache_write(case.runs, case.base_rows, q_ref, ks, vs, k_ref, v_ref, cos, sin,
+                            num_q=NUM_Q, num_kv=NUM_KV, page_shift=6, row_mask=63,
+                            page_mask=-1, seq_len=n, half=128, pair_stride=128,
+                            head_dim=HEAD_DIM)
+    assert np.array_equal(from_dev(kd, np.uint16), k_ref), "k cache after append"
+    assert np.array_equal(from_dev(vd, np.uint16), v_ref), "v cache after append"
+    assert np.array_equal(from_dev(qd, np.uint16), q_ref), "rotated q"
+    # Sampled tokens, each as its own one-token run of a token plan (cap below
+    # the run count): the same tiles-from-0 walk and one-segment merge.
+    picks = []
+    for r in range(8):
+        for t in (0, 1, 15, 16, 777, 2046, 2047):
+            picks.append((r, t))
+    runs, q_s = [], []
+    for i, (r, t) in enumerate(picks):
+        runs.append([i, prefix[r] + t, case.runs[r, 2], case.runs[r, 3]])
+        tok = r * 2048 + t
+        q_s.append(q_ref[tok * NUM_Q * HEAD_DIM:(tok + 1) * NUM_Q * HEAD_DIM])
+    runs = np.asarray(runs, dtype=np.int32)
+    ref = oracle.attention(FULL, runs, case.base_rows, np.concatenate(q_s), k_ref, v_ref,
+                           num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE,
+                           window=0, cache_size=PAGE_LEN, page_len=PAGE_LEN,
+                           seq_len=len(picks), cap=2, threads=16)
+    sel = np.concatenate([got[r * 2048 + t] for r, t in picks])
+    res = compare_bf16(sel, ref)
+    print(f"  config4 sampled tokens: {res}", flush=True)
+    assert res["n_fail"] == 0 and res["n_nan"] == 0, res
