@@ -32,7 +32,8 @@ HBM_PEAK_GBS = 8000.0
 NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
-DEFAULT_CAP = {1: 128, 2: 512, 3: 512, 5: 512}
+DEFAULT_CAP = {1: 128, 2: 512, 3: 512, 4: 16, 5: 512}
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def splitmix64(x: int) -> int:
@@ -323,6 +324,134 @@ class DecodeBq:
         return None
 
 
+class PrefillBf16:
+    """Config 4: chunked prefill -- 8 sequences append 2048 tokens each onto
+    prefixes ~ U[0, 16384] (RoPE + cache write), then causal full-attention
+    prefill over the paged prefix + chunk (MFMA)."""
+
+    dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
+    phases = ("append", "attention")
+    dominant = "prefill_full_mfma_kernel"
+    bound = "mfma"
+
+    def __init__(self, seed: int):
+        self.seed = seed
+        self.prefix = uniform_ints(seed, 8, 0, 16384)
+        self.new = 2048
+        self.name = ("config4: chunked prefill, 8 sequences x 2048 new tokens on prefixes "
+                     "~ U[0,16384], 16q/8kv hd256 bf16, 64-token pages, append + causal MFMA "
+                     "prefill over the paged prefix and chunk")
+
+    def setup(self, dev, a):
+        import torch
+
+        from inferno_amd import attention as A
+        from inferno_amd.kv import AttentionPlan, KVRunTable
+
+        self.A = A
+        n_seq = len(self.prefix)
+        need = [(p + self.new + PAGE_LEN - 1) // PAGE_LEN for p in self.prefix]
+        pool = sum(need)
+        perm = np.random.default_rng(self.seed).permutation(pool)
+        table = KVRunTable()
+        off = 0
+        for i, p in enumerate(self.prefix):
+            table.begin_run(i * self.new, p)
+            for x in perm[off:off + need[i]]:
+                table.add_base_row(int(x) * PAGE_LEN)
+            off += need[i]
+        n = n_seq * self.new
+        rows = pool * PAGE_LEN
+        self.pool, self.table, self.n = pool, table, n
+        self.stream = torch.cuda.current_stream()
+        sid = int(self.stream.cuda_stream)
+        self.k = torch.empty(rows * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.v = torch.empty_like(self.k)
+        self.q = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.ks = torch.empty(n * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.vs = torch.empty_like(self.ks)
+        for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
+            _fill(t, self.seed * 16 + i, sid)
+        cos, sin = rope_tables(max(self.prefix) + self.new + 1)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        self.plan = AttentionPlan(table, n, kind=1, window=0, cache_size=PAGE_LEN,
+                                  page_len=PAGE_LEN, cache_rows=rows, cap=a.cap,
+                                  kv_row_bytes=KV_STRIDE * 2, device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
+        self.out = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.cap = a.cap
+
+    def launch(self, phase):
+        A, p = self.A, self.plan
+        if phase == "append":
+            A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
+                                        self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
+                                        pair_stride=128, head_dim=HEAD_DIM)
+        else:
+            A.attention_bf16(p, self.q, self.k, self.v, self.out, self.partials, self.ps,
+                             num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
+                             kv_stride=KV_STRIDE)
+
+    def flops(self) -> int:
+        """4 * D * Hq * sum over query tokens of attended keys (QK^T + PV)."""
+        keys = sum(sum(p + t + 1 for t in range(self.new)) for p in self.prefix)
+        return 4 * HEAD_DIM * NUM_Q * keys
+
+    def step_bytes(self) -> int:
+        return self.n * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 3)
+
+    def dominant_bytes(self) -> int:
+        return 0
+
+    def config(self) -> dict:
+        return {"workload": self.name, "sequences": len(self.prefix), "new_tokens": self.new,
+                "prefixes": self.prefix, "pool_pages": self.pool, "page_len": PAGE_LEN,
+                "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM, "cap": self.cap,
+                "seed": self.seed, "query_blocks": int(self.plan.info[14]),
+                "algorithmic_tflop": round(self.flops() / 1e12, 3)}
+
+    def cpu_baseline(self, budget_s):
+        """The oracle's token route (FlashPrefillFullKernel) on a bounded sample:
+        the last 16 query tokens of the longest sequence."""
+        import torch
+
+        import oracle
+
+        threads = min(16, os.cpu_count() or 1)
+        i = int(np.argmax(self.prefix))
+        p0 = self.prefix[i]
+        npage = (p0 + self.new + PAGE_LEN - 1) // PAGE_LEN
+        rows = np.asarray(self.table.base_rows[self.table.runs[i][2]:][:npage], dtype=np.int64)
+        idx = torch.from_numpy(rows // PAGE_LEN).to(self.k.device)
+        kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
+        vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
+        n_s = 16
+        first = self.new - n_s
+        runs = np.asarray([[0, p0 + first, 0, npage]], dtype=np.int32)
+        base = np.arange(npage, dtype=np.int32) * PAGE_LEN
+        qh = self.q.view(-1, NUM_Q * HEAD_DIM)[i * self.new + first:(i + 1) * self.new]
+        qh = np.ascontiguousarray(qh.cpu().numpy().view(np.uint16).reshape(-1))
+        keys = sum(p0 + first + t + 1 for t in range(n_s))
+        fl = 4 * HEAD_DIM * NUM_Q * keys
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.attention(1, runs, base, qh, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
+                             head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
+                             cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
+                             cap=threads, threads=threads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port",
+                "sample": (f"last {n_s} query tokens of the longest sequence "
+                           f"({keys} query-key pairs), the reference's token route at "
+                           f"cap={threads} workers, median of {len(times)}")}
+
+
 def measure(w, steps: int, warmup: int):
     import torch
 
@@ -372,7 +501,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 5))
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5))
     ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -395,14 +524,32 @@ def main() -> None:
         return
     if a.cap <= 0:
         a.cap = DEFAULT_CAP[a.config]
-    w = DecodeBq(a.seed) if a.config == 5 else DecodeBf16(a.config, a.seed)
+    if a.config == 5:
+        w = DecodeBq(a.seed)
+    elif a.config == 4:
+        w = PrefillBf16(a.seed)
+    else:
+        w = DecodeBf16(a.config, a.seed)
     w.setup(dev, a)
     torch.cuda.synchronize()
     wall, per = measure(w, a.steps, a.warmup)
     ms_per_step = wall / a.steps * 1e3
     value = w.step_bytes() / (wall / a.steps) / 1e9
     dom_us = per["partials"] if "partials" in per else per["attention"]
-    achieved = w.dominant_bytes() / (dom_us * 1e-6) / 1e9
+    if getattr(w, "bound", "hbm") == "mfma":
+        tflops = w.flops() / (dom_us * 1e-6) / 1e12
+        roof = {"bound": "mfma", "kernel": w.dominant, "achieved": round(tflops, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "flops_per_launch": w.flops()}
+        value_override = round(w.flops() / (wall / a.steps) / 1e12, 2)
+    else:
+        achieved = w.dominant_bytes() / (dom_us * 1e-6) / 1e9
+        roof = {"bound": "hbm", "kernel": w.dominant, "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": w.dominant_bytes()}
+        value_override = None
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -421,11 +568,14 @@ def main() -> None:
         "us_per_layer": round(ms_per_step * 1e3, 2),
         "us_breakdown_events": {k: round(v, 2) for k, v in per.items()},
         "step_bytes": w.step_bytes(),
-        "roofline": {"bound": "hbm", "kernel": w.dominant, "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": w.dominant_bytes()},
+        "roofline": roof,
     }
+    if value_override is not None:
+        # Prefill is MFMA-bound: report TFLOP/s of the step (append + prefill).
+        res["value"] = value_override
+        res["unit"] = "TFLOP/s"
+        res["pct_hbm_peak"] = None
+        res["pct_mfma_peak"] = round(100 * value_override / MFMA_BF16_PEAK_TFLOPS, 2)
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 "traffic.json")
     key = f"config{a.config}_cap{a.cap}"

@@ -41,7 +41,7 @@ constexpr int kUnitWords = 4;
 // {run, first token, token count, last token's position + 1}, at most
 // kPrefillTokens consecutive tokens of one run, longest key range first.
 constexpr int kQBlockWords = 4;
-constexpr int kPrefillTokens = 32;
+constexpr int kPrefillTokens = 64;
 
 constexpr int kTile = 16;  // reference TILE = f32 SIMD width on AVX-512
 constexpr float kNegBig = -1e30f;

@@ -38,7 +38,7 @@ typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kPD = 256;             // head_dim
-constexpr int kPWaves = 4;           // waves per block
+constexpr int kPWaves = 8;           // waves per block
 constexpr int kPTokensPerWave = 8;   // x 2 q heads = 16 rows
 constexpr int kPTokens = kPWaves * kPTokensPerWave;  // tokens per block
 static_assert(kPTokens == kPrefillTokens, "plan query blocks must match the kernel");
@@ -50,7 +50,9 @@ constexpr int kBufBytes = kKBytes + kVBytes;
 
 __device__ __forceinline__ uint32_t bf16_rne_bits(float f) { return f32_to_bf16_bits(f); }
 
-__global__ __launch_bounds__(256) void prefill_full_mfma_kernel(
+// Two waves per SIMD (<= 256 VGPR + AGPR per lane).
+__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_full_mfma_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride,
@@ -104,55 +106,52 @@ __global__ __launch_bounds__(256) void prefill_full_mfma_kernel(
   float m = kNegBig, l = 0.0f;
 
   // Global -> register staging of one tile: 16 keys x 512 B of K and of V =
-  // 1024 chunks of 16 B; thread tid takes chunks tid, tid+256 (K) and the
-  // same for V.  Chunk c -> key c/32, dims 8*(c%32) .. +7.
+  // 512 chunks of 16 B each; thread tid takes chunk tid of K and of V.  Chunk
+  // c -> key c/32, dims 8*(c%32) .. +7.  Two register sets keep the loads of
+  // tiles j+1 and j+2 in flight while tile j is computed from LDS.
+  static_assert(kPWaves * 64 == 512, "one 16-byte chunk of K and V per thread");
   const uint16_t* kbase = kc + static_cast<int64_t>(g) * kPD;
   const uint16_t* vbase = vc + static_cast<int64_t>(g) * kPD;
+  const int ckey = tid >> 5, cd0 = 8 * (tid & 31);
   uint4 kreg[2], vreg[2];
-  auto gload = [&](int tile) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;
-      const int key = tile * 16 + (c >> 5);
-      if (key < count_max) {
-        const int64_t slot = static_cast<int64_t>(rows[key >> shift]) + (key & row_mask);
-        const int64_t off = slot * kv_stride + 8 * (c & 31);
-        kreg[i] = *reinterpret_cast<const uint4*>(kbase + off);
-        vreg[i] = *reinterpret_cast<const uint4*>(vbase + off);
-      } else {
-        kreg[i] = make_uint4(0, 0, 0, 0);
-        vreg[i] = make_uint4(0, 0, 0, 0);
-      }
+  auto gload = [&](int tile, int set) {
+    const int key = tile * 16 + ckey;
+    if (key < count_max) {
+      const int64_t slot = static_cast<int64_t>(rows[key >> shift]) + (key & row_mask);
+      const int64_t off = slot * kv_stride + cd0;
+      kreg[set] = *reinterpret_cast<const uint4*>(kbase + off);
+      vreg[set] = *reinterpret_cast<const uint4*>(vbase + off);
+    } else {
+      kreg[set] = make_uint4(0, 0, 0, 0);
+      vreg[set] = make_uint4(0, 0, 0, 0);
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, int set) {
     uint8_t* kl = lds + buf * kBufBytes;
     uint8_t* vl = kl + kKBytes;
+    *reinterpret_cast<uint4*>(kl + ckey * kKPitch + 2 * cd0) = kreg[set];
+    const uint32_t w[4] = {vreg[set].x, vreg[set].y, vreg[set].z, vreg[set].w};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;
-      const int kk = c >> 5, d0 = 8 * (c & 31);
-      *reinterpret_cast<uint4*>(kl + kk * kKPitch + 2 * d0) = kreg[i];
-      const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        *reinterpret_cast<uint16_t*>(vl + (d0 + 2 * e) * kVPitch + 2 * kk) =
-            static_cast<uint16_t>(w[e] & 0xFFFFu);
-        *reinterpret_cast<uint16_t*>(vl + (d0 + 2 * e + 1) * kVPitch + 2 * kk) =
-            static_cast<uint16_t>(w[e] >> 16);
-      }
+    for (int e = 0; e < 4; ++e) {
+      *reinterpret_cast<uint16_t*>(vl + (cd0 + 2 * e) * kVPitch + 2 * ckey) =
+          static_cast<uint16_t>(w[e] & 0xFFFFu);
+      *reinterpret_cast<uint16_t*>(vl + (cd0 + 2 * e + 1) * kVPitch + 2 * ckey) =
+          static_cast<uint16_t>(w[e] >> 16);
     }
   };
 
   if (n_tiles > 0) {
-    gload(0);
-    lstore(0);
+    gload(0, 0);
+    lstore(0, 0);
   }
+  if (n_tiles > 1) gload(1, 1);
   __syncthreads();
 
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int buf = tile & 1;
-    if (tile + 1 < n_tiles) gload(tile + 1);
+    // set (tile+1)&1 holds tile+1 (issued last iteration); reuse set tile&1
+    // for tile+2.
+    if (tile + 2 < n_tiles) gload(tile + 2, tile & 1);
     const uint8_t* kl = lds + buf * kBufBytes;
     const uint8_t* vl = kl + kKBytes;
 
@@ -196,8 +195,6 @@ __global__ __launch_bounds__(256) void prefill_full_mfma_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (key0 + j >= valid) w[j] = 0.0f;  // pads enter l only
-      } else {
-        // keep the lanes of the shuffles above converged; nothing to update
       }
       // ---- P^T as bf16 hi + lo ----
       uint32_t hi[4], lo[4];
@@ -221,7 +218,7 @@ __global__ __launch_bounds__(256) void prefill_full_mfma_kernel(
         acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
       }
     }
-    if (tile + 1 < n_tiles) lstore(buf ^ 1);
+    if (tile + 1 < n_tiles) lstore(buf ^ 1, (tile + 1) & 1);
     __syncthreads();
   }
 
@@ -252,7 +249,7 @@ hipError_t launch_prefill_full_mfma(const int32_t* image, int num_qblocks, const
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(prefill_full_mfma_kernel, dim3(num_qblocks * num_kv), dim3(256),
+  hipLaunchKernelGGL(prefill_full_mfma_kernel, dim3(num_qblocks * num_kv), dim3(64 * kPWaves),
                      2 * kBufBytes, stream, image, static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
