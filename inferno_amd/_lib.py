@@ -61,7 +61,60 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                F32, U64]),
     "ifr_bq_attention": (I32, [VP, P_I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, I64, I64,
                                I64, I64, I64, I64, I64, I64, U64]),
+    # ---- host-side page state (include/inferno_host.h) ----
+    "ifr_splitmix64": (U64, [U64]),
+    "ifr_hash_token_block": (U64, [VP, I64, I64]),
+    "ifr_chain_link": (U64, [U64, U64]),
+    "ifr_refresh_chain": (I64, [VP, I64, I64, VP, I64, I64]),
+    "ifr_hashed_prefix_len": (I64, [I64, VP, I64, VP, I64, VP, I64, VP, I64]),
+    "ifr_pages_create": (I32, [I64, VP, I64, C.POINTER(VP)]),
+    "ifr_pages_destroy": (None, [VP]),
+    "ifr_pages_admit": (I32, [VP, P_I64]),
+    "ifr_pages_release": (I32, [VP, I64]),
+    "ifr_pages_share": (I32, [VP, I64, I64, I64, I64]),
+    "ifr_pages_truncate": (I32, [VP, I64, I64]),
+    "ifr_pages_replace_with_private": (I32, [VP, I64, I64, I64, P_I64]),
+    "ifr_pages_pages_needed": (I32, [VP, I64, I64, VP]),
+    "ifr_pages_fits": (I32, [VP, VP, P_I64]),
+    "ifr_pages_reserve": (I32, [VP, I64, I64, P_I64]),
+    "ifr_pages_retain_page": (I32, [VP, I64, I64]),
+    "ifr_pages_release_page": (I32, [VP, I64, I64]),
+    "ifr_pages_query": (I64, [VP, I64, I64, I64, I64]),
+    "ifr_pages_export": (I32, [VP, I64, VP, VP, VP, P_I64]),
+    "ifr_registry_create": (I32, [I64, I64, C.POINTER(VP)]),
+    "ifr_registry_destroy": (None, [VP]),
+    "ifr_registry_open": (I32, [VP, I64, I64, U64]),
+    "ifr_registry_adopt": (I32, [VP, I64, I64, U64]),
+    "ifr_registry_extend": (I32, [VP, I64, VP, I64, I64, I64, I64, U64]),
+    "ifr_registry_seed": (I32, [VP, I64, VP, I64, I64, U64]),
+    "ifr_registry_set_warm": (I32, [VP, I64]),
+    "ifr_registry_close": (I32, [VP, I64]),
+    "ifr_registry_prefix_len": (I64, [VP, I64, VP, I64, VP, I64]),
+    "ifr_registry_exact_prefix_len": (I64, [VP, I64, VP, I64]),
+    "ifr_registry_lru_victim": (I64, [VP]),
+    "ifr_registry_query": (I64, [VP, I64, I64]),
+    "ifr_registry_export": (I32, [VP, I64, VP, I64, VP, I64]),
+    "ifr_scheduler_create": (I32, [I64, I64, I64, I64, VP, I64, I64, VP, I64, I64,
+                                   C.POINTER(VP)]),
+    "ifr_scheduler_destroy": (None, [VP]),
+    "ifr_scheduler_pages": (VP, [VP]),
+    "ifr_scheduler_registry": (VP, [VP]),
+    "ifr_scheduler_submit": (I32, [VP, VP, I64, I64, I64, P_I64]),
+    "ifr_scheduler_cancel": (I32, [VP, I64]),
+    "ifr_scheduler_retire": (I32, [VP, I64, P_I64]),
+    "ifr_scheduler_evict_warm": (I32, [VP, P_I64]),
+    "ifr_scheduler_build_schedule": (I32, [VP, U64, P_I64]),
+    "ifr_scheduler_absorb": (I32, [VP, VP, I64, U64]),
+    "ifr_scheduler_discard_step": (I32, [VP]),
+    "ifr_scheduler_query": (I64, [VP, I64, I64]),
+    "ifr_scheduler_export_schedule": (I32, [VP, VP, VP, VP]),
+    "ifr_scheduler_export_request": (I32, [VP, I64, VP, I64, VP, I64]),
+    "ifr_scheduler_export_pending": (I32, [VP, VP, I64, P_I64]),
+    "ifr_bind_pool_run_table": (I32, [VP, I64, I64, I64, VP, I64, VP, I64, P_I64, P_I64]),
+    "ifr_prefix_copy_jobs": (I32, [VP, I64, VP, VP, I64, VP, I64, P_I64]),
 }
+
+QUERY_ERROR = -(1 << 63)
 
 
 class InfernoHipError(RuntimeError):

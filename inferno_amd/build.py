@@ -30,6 +30,9 @@ OBJ_DIR = PKG.parent / "_build" / "obj"
 ARCH = "gfx950"
 
 SOURCES = ["api.hip", "attention.hip", "append.hip", "copy.hip", "bq.hip", "prefill.hip"]
+# Host-only C++ (page state, scheduler): built with the host compiler.
+HOST_SOURCES = ["host_state.cpp", "host_api.cpp"]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -51,8 +54,15 @@ def hipcc() -> str:
     return cand
 
 
+def host_cxx() -> str:
+    return os.environ.get("CXX") or shutil.which("g++") or "c++"
+
+
 def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cmd = [host_cxx(), *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -65,7 +75,8 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     objs = []
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        futs = [ex.submit(_compile, CSRC / s, OBJ_DIR / (s + ".o")) for s in SOURCES]
+        futs = [ex.submit(_compile, CSRC / s, OBJ_DIR / (s + ".o"))
+                for s in SOURCES + HOST_SOURCES]
         for f in futs:
             obj, warn = f.result()
             if warn.strip() and verbose:

@@ -432,6 +432,13 @@ int32_t check_attention_shapes(int64_t num_q, int64_t num_kv, int64_t head_dim,
 
 }  // namespace
 
+namespace ifr {
+// Status plumbing shared with the host-state entry points (host_api.cpp), so
+// that ifr_last_error() reports every entry point's failure.
+int32_t abi_fail(int32_t code, const char* msg) { return fail(code, "%s", msg); }
+int32_t abi_ok() { return ok(); }
+}  // namespace ifr
+
 extern "C" {
 
 int32_t ifr_abi_version(void) { return IFR_ABI_VERSION; }

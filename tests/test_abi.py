@@ -13,18 +13,23 @@ from inferno_amd import _lib
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.helpers import KV_STRIDE, PAGE_LEN, make_decode_case, make_prefill_case
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "inferno_hip.h"
+INCLUDE = Path(__file__).resolve().parent.parent / "include"
+HEADERS = [INCLUDE / "inferno_hip.h", INCLUDE / "inferno_host.h"]
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int32_t|int64_t)\s+(ifr_\w+)\s*\(", text, re.M)))
+    names = set()
+    for h in HEADERS:
+        names.update(re.findall(
+            r"^(?:int32_t|int64_t|uint64_t|void|ifr_\w+\s*\*)\s*(ifr_\w+)\s*\(",
+            h.read_text(), re.M))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     names = declared_functions()
-    assert len(names) >= 25
+    assert len(names) >= 75
     for n in names:
         assert hasattr(lib, n), n
     assert sorted(_lib.SIGNATURES) == names
