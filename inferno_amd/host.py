@@ -591,3 +591,17 @@ def dispatch_prefix_copies(mirrors: Sequence[KVPoolMirror], schedule_copies, are
     if jobs.shape[0]:
         dispatch_copy_jobs(arena, jobs)
     return int(jobs.shape[0])
+
+
+def bind_step_runs(scheduler: ContinuousBatchScheduler,
+                   mirrors: Sequence[KVPoolMirror]) -> List[KVRunTable]:
+    """bind_step_runs (modeling/gemma_4_moe.mojo:767-777): one run table per
+    pool for the scheduler's current step, pool order as in `mirrors`."""
+    return [bind_pool_run_table(scheduler, p, m) for p, m in enumerate(mirrors)]
+
+
+def run_prefix_copies(scheduler: ContinuousBatchScheduler, mirrors: Sequence[KVPoolMirror],
+                      arena) -> int:
+    """run_prefix_copies (modeling/gemma_4_moe.mojo:763-766): the current
+    step's page copies, issued before the step's appends on the same stream."""
+    return dispatch_prefix_copies(mirrors, scheduler.copies_array(), arena)

@@ -366,3 +366,42 @@ def test_bind_pool_run_table_matches_pages_and_oracle():
         outs = pm.execute(ps, sched, ps.pages)
         ps.absorb(outs, pc())
         os_.absorb(om.execute(os_, os_.schedule, os_.pages), oc())
+
+
+def test_config3_ring_256_decode_steps_lockstep():
+    """Config 3's page-state check: 64 sequences on 32-page rings (window
+    1024 at 64-token pages) plus a growing pool, prefilled past the ring
+    wrap, then 256 decode steps of the whole batch; page tables, holds, free
+    stacks and ring floors of the C++ scheduler equal the oracle's after
+    every step."""
+    rng = np.random.default_rng(33)
+    B, ring_pages, ppp = 64, 32, 64
+    ctx = [int(x) for x in rng.integers(1023, 4096, B)]
+    new_tokens = 700
+    grow_pages = sum((c + new_tokens) // ppp + 1 for c in ctx)
+    specs = [(B * ring_pages, ring_pages, ring_pages), (grow_pages, 0, 5120 // ppp)]
+    pg = P.BatchGeometry(B, B, 1024, [P.PagePoolSpec(*s) for s in specs])
+    og = O.BatchGeometry(B, B, 1024, [O.PagePoolSpec(*s) for s in specs])
+    ps = P.ContinuousBatchScheduler(ppp, pg, 1024, [-1])
+    os_ = O.ContinuousBatchScheduler(ppp, og, 1024, [-1])
+    for i in range(B):
+        toks = [int(x) for x in rng.integers(0, 30000, ctx[i])]
+        toks[0] = 40000 + i  # no shared prefixes
+        assert ps.submit(toks, new_tokens) == os_.submit(toks, new_tokens)
+    pc, oc = Clock(), Clock()
+    pm, om = EchoModel(997), EchoModel(997)
+    decode_steps = steps = 0
+    while decode_steps < 256:
+        n = ps.step(pm, pc)
+        assert n == os_.step(om, oc) and n > 0
+        assert pm.log[-1] == om.log[-1]
+        slots = pm.log[-1][0]
+        if len(slots) == B and all(s[3] == 1 for s in slots):
+            decode_steps += 1
+        assert _snapshot(ps, False, 2) == _snapshot(os_, True, 2)
+        _check_conservation(ps.pages, 2, B)
+        steps += 1
+        assert steps < 2000
+    wrapped = sum(ps.registry.length(sid) > ring_pages * ppp for sid in range(B))
+    assert wrapped > B // 2, "most rings wrapped"
+    assert ps.invariant_failures == (0, 0)
