@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0
 NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
-DEFAULT_CAP = {1: 128, 2: 512, 3: 512, 4: 16, 5: 512}
+DEFAULT_CAP = {1: 64, 2: 512, 3: 512, 4: 16, 5: 2048}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 

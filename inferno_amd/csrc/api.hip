@@ -343,7 +343,14 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   // Query blocks for the MFMA prefill (token plans of full attention).
   hdr[kHdrOffQBlocks] = static_cast<int32_t>(off);
   int64_t n_qblocks = 0;
-  if (mode == IFR_PLAN_TOKEN_MERGE) {
+  // Only when every run's page table fits the kernel's LDS copy.
+  bool mfma_tables_fit = true;
+  for (int64_t r = 0; r < num_runs; ++r) {
+    const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
+    if (e > b && ((runs[4 * r + 1] + (e - 1 - b)) >> g.shift) + 1 > kPrefillLdsPages)
+      mfma_tables_fit = false;
+  }
+  if (mode == IFR_PLAN_TOKEN_MERGE && mfma_tables_fit) {
     std::vector<std::array<int64_t, 4>> qbs;
     for (int64_t r = 0; r < num_runs; ++r) {
       const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
@@ -352,8 +359,16 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
         qbs.push_back({r, t, n, runs[4 * r + 1] + (t + n - 1 - b) + 1});
       }
     }
+    // Run-major order: the blocks of one run start together and walk its
+    // keys in step, so each XCD's L2 serves a key tile to all of them.
+    // Runs with the longest key range first, and inside a run the longest
+    // query block first, to even out the tail.
+    std::vector<int64_t> run_top(num_runs, 0);
+    for (const auto& qb : qbs) run_top[qb[0]] = std::max(run_top[qb[0]], qb[3]);
     std::stable_sort(qbs.begin(), qbs.end(),
-                     [](const std::array<int64_t, 4>& a, const std::array<int64_t, 4>& b) {
+                     [&](const std::array<int64_t, 4>& a, const std::array<int64_t, 4>& b) {
+                       if (run_top[a[0]] != run_top[b[0]]) return run_top[a[0]] > run_top[b[0]];
+                       if (a[0] != b[0]) return a[0] < b[0];
                        return a[3] > b[3];
                      });
     for (const auto& qb : qbs) {

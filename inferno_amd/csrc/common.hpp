@@ -42,6 +42,9 @@ constexpr int kUnitWords = 4;
 // kPrefillTokens consecutive tokens of one run, longest key range first.
 constexpr int kQBlockWords = 4;
 constexpr int kPrefillTokens = 64;
+// The MFMA prefill stages a run's page table in LDS: runs with more pages
+// than this take the token kernels.
+constexpr int kPrefillLdsPages = 4096;
 
 constexpr int kTile = 16;  // reference TILE = f32 SIMD width on AVX-512
 constexpr float kNegBig = -1e30f;

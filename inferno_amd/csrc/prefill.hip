@@ -5,28 +5,34 @@
 // with the online softmax of process_kv_tile (kernels/attention_ops.mojo:
 // 165-253), then its one-segment merge (kernels/logsum_merge.mojo:28-122).
 // Because all queries start at key 0 the tiles line up across queries, so a
-// block of queries can share each K/V tile:
-//
-//   S^T (16 keys x 16 rows) = K_tile (16 x 256) . Q^T      v_mfma_f32_16x16x32_bf16
-//   O^T (16 dims x 16 rows) += V^T (16 x 16 keys) . P^T    v_mfma_f32_16x16x16_bf16
+// block of query tokens shares every K/V tile of its kv head.
 //
 // A row is one (query token, q head); a wave owns 16 rows = 8 tokens x the
-// 2 q heads of one kv head.  In the MFMA C layout lane l holds keys
-// 4*(l/16)..+3 of row l%16, which is also the B layout P^T needs, and the
-// O^T accumulator keeps row l%16 in lane l, so the per-row softmax state and
-// the per-tile rescale stay lane-local.  Per row and tile the reference's
-// steps are kept: a row skips tiles past its position (the reference never
-// visits them), pads of its last tile score -1e30 (their fexp(-87) enters l,
-// not PV), m/corr/w use the biased exp, and the 16 weights are summed by the
-// halving tree (key ^8 = lane ^32, ^4 = lane ^16, ^2 and ^1 inside the lane).
-// P is fed to the bf16 MFMA as hi + lo bf16 parts, so the products carry ~16
-// significant bits of each weight; QK^T products are exact in f32.
+// 2 q heads of one kv head; a block of 8 waves owns 64 tokens.  Each
+// iteration stages 64 keys (4 tiles) in LDS and computes, per wave:
 //
-// K/V tiles are gathered through the page table into LDS (K row-major, V
-// transposed) with one barrier per tile; the next tile's global loads are in
-// flight while the current tile is computed.  Blocks are numbered
-// kv-head-fastest so every block of a kv head lands on one XCD (block id mod
-// 8) and shares that XCD's L2.
+//   S^T (16 keys x 16 rows) = K_tile . Q^T, per tile     v_mfma_f32_16x16x32_bf16
+//   O^T (16 dims x 16 rows) += V^T . P'^T, 32 keys/MFMA  v_mfma_f32_16x16x32_bf16
+//
+// In the MFMA C layout lane l holds keys 4*(l/16)..+3 of row l%16, and O^T
+// keeps row l%16 in lane l, so the per-row softmax state stays lane-local.
+// The reference's per-tile steps are kept in tile order: a row skips tiles
+// past its position (the reference never visits them), pads of its last
+// tile score -1e30 (their fexp(-87) enters l, not PV), and m, corr, w use
+// the biased exp; l is updated tile by tile.  The accumulator rescales of
+// an iteration's tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 (two
+// tiles shown) equals the reference's nested (acc*c0 + w0 V0)*c1 + w1 V1
+// up to f32 rounding, and the product of the rescales is carried as a
+// per-row scale S (acc = acc_stored * S) that divides the weights instead
+// of multiplying the 64 accumulators.  P' enters the bf16 MFMA as hi + lo bf16 parts (~16
+// significant bits per weight); QK^T products are exact in f32.
+//
+// K and V tiles are staged row-major in LDS; V^T operands come from
+// ds_read_b64_tr_b16 (a 16-lane transposing read).  The next iteration's
+// keys are loaded into registers while the current one is computed; the
+// run's page table is staged in LDS first.
+// Blocks are numbered kv-head-fastest so every block of a kv head lands on
+// one XCD (block id mod 8) and shares that XCD's L2.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -35,32 +41,109 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPD = 256;             // head_dim
-constexpr int kPWaves = 8;           // waves per block
+constexpr int kPWaves = 8;           // waves per block (one block per CU)
 constexpr int kPTokensPerWave = 8;   // x 2 q heads = 16 rows
 constexpr int kPTokens = kPWaves * kPTokensPerWave;  // tokens per block
 static_assert(kPTokens == kPrefillTokens, "plan query blocks must match the kernel");
-constexpr int kKPitch = kPD * 2 + 16;   // bytes per K row in LDS (padded)
-constexpr int kVPitch = 16 * 2 + 8;     // bytes per V^T dim row in LDS (padded)
-constexpr int kKBytes = 16 * kKPitch;
-constexpr int kVBytes = kPD * kVPitch;
+constexpr int kKeys = 64;                // keys per iteration
+constexpr int kTiles = kKeys / 16;       // 16-key tiles per iteration
+constexpr int kHalves = kTiles / 2;      // 32-key MFMA operands per iteration
+static_assert(kTiles % 2 == 0, "tiles pair up into 32-key MFMA operands");
+constexpr int kKPitch = kPD * 2 + 16;    // bytes per K row in LDS: 132 dwords
+constexpr int kVPitch = kPD * 2 + 32;    // bytes per V row in LDS: 136 dwords
+constexpr int kKBytes = kKeys * kKPitch;
+constexpr int kVBytes = kKeys * kVPitch;
 constexpr int kBufBytes = kKBytes + kVBytes;
+constexpr int kChunksPerThread = kKeys * kPD * 2 / 16 / (64 * kPWaves);  // of K and of V
+static_assert(kChunksPerThread == 4, "staging layout");
+constexpr int kKeyStep = kKeys / kChunksPerThread;  // keys between a thread's chunks
 
-__device__ __forceinline__ uint32_t bf16_rne_bits(float f) { return f32_to_bf16_bits(f); }
+static_assert(kKeyStep * 32 == 64 * kPWaves, "32 lanes per key row");
 
-// Two waves per SIMD (<= 256 VGPR + AGPR per lane).
+// x + x[lane ^ 16] and x + x[lane ^ 32] through the gfx950 lane swaps: with
+// both operands x, the two results hold the low and high member of each
+// pair, so their sum (low + high) is the same in both lanes.
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return max_ref(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return max_ref(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// One tile's online-softmax step for this lane's row (process_kv_tile's
+// m / corr / w / l updates, attention_ops.mojo:165-180).  Masked: the tile
+// reaches past some row's last key (or the row is empty); a row with no key
+// in the tile is left untouched (corr 1, weights 0), pads score -1e30 and
+// enter l only.  The in-lane sum of the 4 weights comes first, then the
+// lanes ^16 and ^32 (the same 16 weights as the reference's halving tree,
+// added in another order).
+template <bool kMasked>
+__device__ __forceinline__ void softmax_tile(const f32x4_t s, int valid, int key0, float& m,
+                                             float& l, float& corr, float (&w)[4]) {
+  float sc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sc[j] = (!kMasked || key0 + j < valid) ? s[j] : kNegBig;
+  float mx = max_ref(max_ref(sc[0], sc[1]), max_ref(sc[2], sc[3]));
+  mx = max_xor16(mx);
+  mx = max_xor32(mx);
+  const float m_new = mx > m ? mx : m;
+  const float c = fexp(max_ref(-87.0f, m - m_new));
+  float e[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) e[j] = fexp(max_ref(-87.0f, sc[j] - m_new));
+  float ts = (e[0] + e[1]) + (e[2] + e[3]);
+  ts = sum_xor16(ts);
+  ts = sum_xor32(ts);
+  if (kMasked) {
+    const bool any = valid > 0;
+    l = any ? l * c + ts : l;
+    m = any ? m_new : m;
+    corr = any ? c : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = key0 + j < valid ? e[j] : 0.0f;
+  } else {
+    l = l * c + ts;
+    m = m_new;
+    corr = c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = e[j];
+  }
+}
+
+// Two waves per SIMD (<= 256 VGPR + AGPR per lane); one block per CU.
 __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_full_mfma_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride,
     int shift, int row_mask) {
-  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ __align__(16) uint8_t lds[2 * kBufBytes];
+  __shared__ int32_t page_rows[kPrefillLdsPages];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
+  const int grp = lane >> 4;   // key group within a tile / k group of the MFMA
   const int g = blockIdx.x % num_kv;
   const int qb = blockIdx.x / num_kv;
 
@@ -75,7 +158,7 @@ void prefill_full_mfma_kernel(
 
   // Keys the block needs: [0, count_max), count_max = last token's position + 1.
   const int count_max = base_pos + (t0 + ntok - 1 - buf_start) + 1;
-  const int n_tiles = (count_max + 15) >> 4;
+  const int n_iters = (count_max + kKeys - 1) / kKeys;
 
   // This lane's row: token wave*8 + (l%16)/2, q head 2g + (l%16)%2.
   const int row = lane & 15;
@@ -84,15 +167,20 @@ void prefill_full_mfma_kernel(
   const bool row_live = tok_local < ntok;
   const int tok = t0 + tok_local;
   const int count = row_live ? base_pos + (tok - buf_start) + 1 : 0;
-  const int wave_last = min(ntok, (wave + 1) * kPTokensPerWave) - 1;
-  const int wave_count =
-      wave * kPTokensPerWave < ntok ? base_pos + (t0 + wave_last - buf_start) + 1 : 0;
+  const int wave_first = wave * kPTokensPerWave;
+  const int wave_last = min(ntok, wave_first + kPTokensPerWave) - 1;
+  const int wave_count = wave_first < ntok ? base_pos + (t0 + wave_last - buf_start) + 1 : 0;
+  // Keys below wave_min are valid for every row of the wave (0 if the wave
+  // has rows past the block's last token).
+  const int wave_min = wave_first + kPTokensPerWave <= ntok
+                           ? base_pos + (t0 + wave_first - buf_start) + 1
+                           : 0;
 
   // Q^T fragments: lane holds Q[row][32c + 8*(l/16) .. +7] for chunks c.
   bf16x8_t qf[8];
   {
     const uint16_t* qr =
-        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * (lane >> 4);
+        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * grp;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * c);
@@ -100,125 +188,189 @@ void prefill_full_mfma_kernel(
     }
   }
 
+  // The O^T accumulator is kept as acc_stored with acc = acc_stored * S: a
+  // tile's rescale multiplies S, and the weights entering the MFMA are
+  // divided by the new S, so the 64 accumulators are not rescaled per
+  // iteration.  When S would fall below 2^-64 the accumulators take it over
+  // (acc_stored *= S, S = 1) for the whole wave.
   f32x4_t acc[16];
 #pragma unroll
   for (int b = 0; b < 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = kNegBig, l = 0.0f;
+  float m = kNegBig, l = 0.0f, S = 1.0f;
 
-  // Global -> register staging of one tile: 16 keys x 512 B of K and of V =
-  // 512 chunks of 16 B each; thread tid takes chunk tid of K and of V.  Chunk
-  // c -> key c/32, dims 8*(c%32) .. +7.  Two register sets keep the loads of
-  // tiles j+1 and j+2 in flight while tile j is computed from LDS.
-  static_assert(kPWaves * 64 == 512, "one 16-byte chunk of K and V per thread");
+  // The run's page table, staged once (the host routes runs with more than
+  // kPrefillLdsPages pages elsewhere): the K/V loads of an iteration then
+  // wait on an LDS read rather than on a global load.
+  const int n_pages = count_max > 0 ? ((count_max - 1) >> shift) + 1 : 0;
+  for (int i = tid; i < n_pages; i += 64 * kPWaves) page_rows[i] = rows[i];
+  __syncthreads();
+
+  // Staging of one iteration: kKeys keys x 512 B of K and of V, 16-byte
+  // chunks; thread tid takes dims 8*(tid%32) of keys tid/32 + kKeyStep*r
+  // (32 consecutive lanes read one key's 512 contiguous bytes).  Keys past
+  // count_max read the last key (in bounds) and are stored as zeros.
   const uint16_t* kbase = kc + static_cast<int64_t>(g) * kPD;
   const uint16_t* vbase = vc + static_cast<int64_t>(g) * kPD;
   const int ckey = tid >> 5, cd0 = 8 * (tid & 31);
-  uint4 kreg[2], vreg[2];
-  auto gload = [&](int tile, int set) {
-    const int key = tile * 16 + ckey;
-    if (key < count_max) {
-      const int64_t slot = static_cast<int64_t>(rows[key >> shift]) + (key & row_mask);
+  uint4 kreg[kChunksPerThread], vreg[kChunksPerThread];
+  uint32_t in_range = 0;  // bit r: chunk r holds a key below count_max
+  // All page-table reads first, then all K/V loads: no load waits on
+  // another, and the zero fill of keys past count_max happens at the LDS
+  // store, when the loaded data is needed anyway.
+  auto gload = [&](int it) {
+    int32_t page_row[kChunksPerThread];
+    in_range = 0;
+#pragma unroll
+    for (int r = 0; r < kChunksPerThread; ++r) {
+      const int key = it * kKeys + ckey + kKeyStep * r;
+      in_range |= (key < count_max ? 1u : 0u) << r;
+      const int kk = min(key, count_max - 1);
+      page_row[r] = kk;
+    }
+#pragma unroll
+    for (int r = 0; r < kChunksPerThread; ++r) page_row[r] = page_rows[page_row[r] >> shift];
+#pragma unroll
+    for (int r = 0; r < kChunksPerThread; ++r) {
+      const int kk = min(it * kKeys + ckey + kKeyStep * r, count_max - 1);
+      const int64_t slot = static_cast<int64_t>(page_row[r]) + (kk & row_mask);
       const int64_t off = slot * kv_stride + cd0;
-      kreg[set] = *reinterpret_cast<const uint4*>(kbase + off);
-      vreg[set] = *reinterpret_cast<const uint4*>(vbase + off);
-    } else {
-      kreg[set] = make_uint4(0, 0, 0, 0);
-      vreg[set] = make_uint4(0, 0, 0, 0);
+      kreg[r] = *reinterpret_cast<const uint4*>(kbase + off);
+      vreg[r] = *reinterpret_cast<const uint4*>(vbase + off);
     }
   };
-  auto lstore = [&](int buf, int set) {
+  auto lstore = [&](int buf) {
     uint8_t* kl = lds + buf * kBufBytes;
     uint8_t* vl = kl + kKBytes;
-    *reinterpret_cast<uint4*>(kl + ckey * kKPitch + 2 * cd0) = kreg[set];
-    const uint32_t w[4] = {vreg[set].x, vreg[set].y, vreg[set].z, vreg[set].w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      *reinterpret_cast<uint16_t*>(vl + (cd0 + 2 * e) * kVPitch + 2 * ckey) =
-          static_cast<uint16_t>(w[e] & 0xFFFFu);
-      *reinterpret_cast<uint16_t*>(vl + (cd0 + 2 * e + 1) * kVPitch + 2 * ckey) =
-          static_cast<uint16_t>(w[e] >> 16);
+    for (int r = 0; r < kChunksPerThread; ++r) {
+      const uint32_t keep = ((in_range >> r) & 1u) ? 0xFFFFFFFFu : 0u;
+      const uint4 kv = make_uint4(kreg[r].x & keep, kreg[r].y & keep, kreg[r].z & keep,
+                                  kreg[r].w & keep);
+      const uint4 vv = make_uint4(vreg[r].x & keep, vreg[r].y & keep, vreg[r].z & keep,
+                                  vreg[r].w & keep);
+      *reinterpret_cast<uint4*>(kl + (ckey + kKeyStep * r) * kKPitch + 2 * cd0) = kv;
+      *reinterpret_cast<uint4*>(vl + (ckey + kKeyStep * r) * kVPitch + 2 * cd0) = vv;
     }
   };
 
-  if (n_tiles > 0) {
-    gload(0, 0);
-    lstore(0, 0);
+  if (n_iters > 0) {
+    gload(0);
+    lstore(0);
   }
-  if (n_tiles > 1) gload(1, 1);
+  if (n_iters > 1) gload(1);
   __syncthreads();
 
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int buf = tile & 1;
-    // set (tile+1)&1 holds tile+1 (issued last iteration); reuse set tile&1
-    // for tile+2.
-    if (tile + 2 < n_tiles) gload(tile + 2, tile & 1);
+  // Transposing-read address of this lane inside a 16-key tile of V: lane
+  // R = l%16 of group grp addresses key 4*grp + R/4, dims 4*(R%4) .. +3;
+  // the read returns, in lane R, keys 4*grp .. +3 of dim R (per 16 dims).
+  const int tr_off = (4 * grp + (row >> 2)) * kVPitch + 8 * (row & 3);
+  const int key0 = 4 * grp;
+  // Settle every load issued so far (the Q fragments among them) before the
+  // loop, so that the loop's own waits track only the K/V prefetch and the
+  // prefetch stays in flight across a whole iteration.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  for (int it = 0; it < n_iters; ++it) {
+    const int buf = it & 1;
     const uint8_t* kl = lds + buf * kBufBytes;
     const uint8_t* vl = kl + kKBytes;
+    const int key_base = it * kKeys;
 
-    if (tile * 16 < wave_count) {
-      // ---- S^T = K . Q^T ----
-      f32x4_t s = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (key_base < wave_count) {
+      // ---- S^T for the 4 tiles ----
+      f32x4_t s[kTiles];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(kl + row * kKPitch + 64 * c +
-                                                         16 * (lane >> 4));
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qf[c],
-                                                    s, 0, 0, 0);
+      for (int t = 0; t < kTiles; ++t) {
+        s[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        if (key_base + 16 * t < wave_count) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const uint4 kv = *reinterpret_cast<const uint4*>(
+                kl + (16 * t + row) * kKPitch + 64 * c + 16 * grp);
+            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv),
+                                                           qf[c], s[t], 0, 0, 0);
+          }
+        }
       }
-      // ---- online softmax of this tile for row (lane & 15) ----
-      const int valid = min(16, max(0, count - tile * 16));
-      const int key0 = 4 * (lane >> 4);
-      float sc[4];
+      // ---- online softmax, tile by tile, for row (lane & 15) ----
+      float w[kTiles][4];
+      float corr[kTiles];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[j] = key0 + j < valid ? s[j] : kNegBig;
-      float mx = max_ref(max_ref(sc[0], sc[1]), max_ref(sc[2], sc[3]));
-      mx = max_ref(mx, shfl_xor_f32(mx, 16));
-      mx = max_ref(mx, shfl_xor_f32(mx, 32));
-      float corr = 1.0f;
-      float w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (valid > 0) {
-        const float m_new = mx > m ? mx : m;
-        corr = fexp(max_ref(-87.0f, m - m_new));
+      for (int t = 0; t < kTiles; ++t) {
+        const int tile_key0 = key_base + 16 * t;
+        corr[t] = 1.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sc[j] - m_new));
-        float a[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = w[j] + shfl_xor_f32(w[j], 32);  // key ^ 8
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = a[j] + shfl_xor_f32(a[j], 16);  // key ^ 4
-        const float t0s = a[0] + a[2];                                      // key ^ 2
-        const float t1s = a[1] + a[3];
-        const float ts = t0s + t1s;                                         // key ^ 1
-        const float lc = l * corr;
-        l = lc + ts;
-        m = m_new;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (key0 + j >= valid) w[j] = 0.0f;  // pads enter l only
+        for (int j = 0; j < 4; ++j) w[t][j] = 0.0f;
+        if (tile_key0 < wave_count) {  // wave-uniform
+          if (tile_key0 + 16 <= wave_min) {
+            softmax_tile<false>(s[t], 16, key0, m, l, corr[t], w[t]);
+          } else {
+            const int valid = min(16, max(0, count - tile_key0));
+            softmax_tile<true>(s[t], valid, key0, m, l, corr[t], w[t]);
+          }
+        }
       }
-      // ---- P^T as bf16 hi + lo ----
-      uint32_t hi[4], lo[4];
+      // ---- fold the rescales into S and the weights ----
+      // acc*c0*..*c_{T-1} + sum_t w_t * prod_{s>t} c_s  =  S' * (acc_stored +
+      // sum_t w_t * f_t / S'),  S' = S * c0*..*c_{T-1},  f_t = prod_{s>t} c_s.
+      float f[kTiles];
+      f[kTiles - 1] = 1.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        hi[j] = bf16_rne_bits(w[j]);
-        lo[j] = bf16_rne_bits(w[j] - __uint_as_float(hi[j] << 16));
+      for (int t = kTiles - 2; t >= 0; --t) f[t] = corr[t + 1] * f[t + 1];
+      const float a = corr[0] * f[0];
+      float S_new = S * a;
+      if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
+#pragma unroll
+        for (int b = 0; b < 16; ++b) acc[b] = acc[b] * S_new;
+        S_new = 1.0f;
       }
-      const s16x4_t phi = s16x4_t{static_cast<short>(hi[0]), static_cast<short>(hi[1]),
-                                  static_cast<short>(hi[2]), static_cast<short>(hi[3])};
-      const s16x4_t plo = s16x4_t{static_cast<short>(lo[0]), static_cast<short>(lo[1]),
-                                  static_cast<short>(lo[2]), static_cast<short>(lo[3])};
-      // ---- O^T = O^T * corr + V^T . P^T ----
+      S = S_new;
+      const float inv_s = 1.0f / S_new;
+      float fs[kTiles];
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) fs[t] = f[t] * inv_s;
+      // P''^T as bf16 hi + lo, two tiles per 32-key MFMA operand: k index
+      // 8*grp + i holds tile 2h key 4*grp + i (i < 4), tile 2h+1 key
+      // 4*grp + i - 4 (i >= 4), the order the V^T reads below produce.
+      bf16x8_t phi[kHalves], plo[kHalves];
+#pragma unroll
+      for (int h = 0; h < kHalves; ++h) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          const int t = 2 * h + (i >> 2);
+          const float p0 = w[t][i & 3] * fs[t];
+          const float p1 = w[t][(i & 3) + 1] * fs[t];
+          const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
+          const float r0 = p0 - static_cast<float>(hb[0]);
+          const float r1 = p1 - static_cast<float>(hb[1]);
+          const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+          phi[h][i] = hb[0];
+          phi[h][i + 1] = hb[1];
+          plo[h][i] = lb[0];
+          plo[h][i + 1] = lb[1];
+        }
+      }
+      // ---- acc_stored += V^T . P''^T ----
 #pragma unroll
       for (int b = 0; b < 16; ++b) {
-        acc[b] = acc[b] * corr;
-        const uint2 vv = *reinterpret_cast<const uint2*>(vl + (16 * b + row) * kVPitch +
-                                                         8 * (lane >> 4));
-        const s16x4_t va = __builtin_bit_cast(s16x4_t, vv);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
+#pragma unroll
+        for (int h = 0; h < kHalves; ++h) {
+          if (key_base + 32 * h >= wave_count) continue;  // wave-uniform
+          const uint8_t* va = vl + (32 * h) * kVPitch + tr_off + 32 * b;
+          const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(va));
+          const s16x4_t v1 =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(va + 16 * kVPitch));
+          const s16x8_t a8 = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+          const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a8);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, phi[h], acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, plo[h], acc[b], 0, 0, 0);
+        }
       }
     }
-    if (tile + 1 < n_tiles) lstore(buf ^ 1, (tile + 1) & 1);
+    if (it + 1 < n_iters) {
+      lstore(buf ^ 1);
+      if (it + 2 < n_iters) gload(it + 2);
+    }
     __syncthreads();
   }
 
@@ -228,14 +380,14 @@ void prefill_full_mfma_kernel(
     const float gl = l * c0;
     const bool live = gl > 0.0f;
     const float inv_l = live ? 1.0f / gl : 0.0f;
-    uint16_t* dst = out + (static_cast<int64_t>(tok) * num_q + head) * kPD + 4 * (lane >> 4);
+    uint16_t* dst = out + (static_cast<int64_t>(tok) * num_q + head) * kPD + 4 * grp;
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
       uint32_t e[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float a = acc[b][j] * c0;
-        e[j] = live ? f32_to_bf16_bits(a * inv_l) : 0u;
+        const float av = (acc[b][j] * S) * c0;
+        e[j] = live ? f32_to_bf16_bits(av * inv_l) : 0u;
       }
       *reinterpret_cast<uint2*>(dst + 16 * b) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
     }
@@ -250,7 +402,7 @@ hipError_t launch_prefill_full_mfma(const int32_t* image, int num_qblocks, const
                                     hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(prefill_full_mfma_kernel, dim3(num_qblocks * num_kv), dim3(64 * kPWaves),
-                     2 * kBufBytes, stream, image, static_cast<const uint16_t*>(q),
+                     0, stream, image, static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
                      geom.row_mask);
