@@ -20,11 +20,11 @@
 // past its position (the reference never visits them), pads of its last
 // tile score -1e30 (their fexp(-87) enters l, not PV), and m, corr, w use
 // the biased exp; l is updated tile by tile.  The accumulator rescales of
-// an iteration's tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 (two
-// tiles shown) equals the reference's nested (acc*c0 + w0 V0)*c1 + w1 V1
-// up to f32 rounding, and the product of the rescales is carried as a
-// per-row scale S (acc = acc_stored * S) that divides the weights instead
-// of multiplying the 64 accumulators.  P' enters the bf16 MFMA as hi + lo bf16 parts (~16
+// a pair of tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 equals the
+// reference's nested (acc*c0 + w0 V0)*c1 + w1 V1 up to f32 rounding, and
+// the product of the rescales is carried as a per-row scale S (acc =
+// acc_stored * S) that divides the weights instead of multiplying the 64
+// accumulators.  P' enters the bf16 MFMA as hi + lo bf16 parts (~16
 // significant bits per weight); QK^T products are exact in f32.
 //
 // K and V tiles are staged row-major in LDS; V^T operands come from
@@ -292,78 +292,69 @@ void prefill_full_mfma_kernel(
           }
         }
       }
-      // ---- online softmax, tile by tile, for row (lane & 15) ----
-      float w[kTiles][4];
-      float corr[kTiles];
-#pragma unroll
-      for (int t = 0; t < kTiles; ++t) {
-        const int tile_key0 = key_base + 16 * t;
-        corr[t] = 1.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[t][j] = 0.0f;
-        if (tile_key0 < wave_count) {  // wave-uniform
-          if (tile_key0 + 16 <= wave_min) {
-            softmax_tile<false>(s[t], 16, key0, m, l, corr[t], w[t]);
-          } else {
-            const int valid = min(16, max(0, count - tile_key0));
-            softmax_tile<true>(s[t], valid, key0, m, l, corr[t], w[t]);
-          }
-        }
-      }
-      // ---- fold the rescales into S and the weights ----
-      // acc*c0*..*c_{T-1} + sum_t w_t * prod_{s>t} c_s  =  S' * (acc_stored +
-      // sum_t w_t * f_t / S'),  S' = S * c0*..*c_{T-1},  f_t = prod_{s>t} c_s.
-      float f[kTiles];
-      f[kTiles - 1] = 1.0f;
-#pragma unroll
-      for (int t = kTiles - 2; t >= 0; --t) f[t] = corr[t + 1] * f[t + 1];
-      const float a = corr[0] * f[0];
-      float S_new = S * a;
-      if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
-#pragma unroll
-        for (int b = 0; b < 16; ++b) acc[b] = acc[b] * S_new;
-        S_new = 1.0f;
-      }
-      S = S_new;
-      const float inv_s = 1.0f / S_new;
-      float fs[kTiles];
-#pragma unroll
-      for (int t = 0; t < kTiles; ++t) fs[t] = f[t] * inv_s;
-      // P''^T as bf16 hi + lo, two tiles per 32-key MFMA operand: k index
-      // 8*grp + i holds tile 2h key 4*grp + i (i < 4), tile 2h+1 key
-      // 4*grp + i - 4 (i >= 4), the order the V^T reads below produce.
-      bf16x8_t phi[kHalves], plo[kHalves];
+      // ---- per pair of tiles: online softmax, fold, acc_stored += V^T P''^T ----
+      // The pair's MFMAs depend only on its own tiles, so they run while
+      // the next pair's softmax is computed.
 #pragma unroll
       for (int h = 0; h < kHalves; ++h) {
+        if (key_base + 32 * h >= wave_count) continue;  // wave-uniform
+        float w[2][4];
+        float corr[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int t = 2 * h + u;
+          const int tile_key0 = key_base + 16 * t;
+          corr[u] = 1.0f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[u][j] = 0.0f;
+          if (tile_key0 < wave_count) {  // wave-uniform
+            if (tile_key0 + 16 <= wave_min) {
+              softmax_tile<false>(s[t], 16, key0, m, l, corr[u], w[u]);
+            } else {
+              const int valid = min(16, max(0, count - tile_key0));
+              softmax_tile<true>(s[t], valid, key0, m, l, corr[u], w[u]);
+            }
+          }
+        }
+        // acc*c_a*c_b + w_a*c_b V_a + w_b V_b = S' (acc_stored + (w_a*c_b V_a +
+        // w_b V_b) / S'),  S' = S*c_a*c_b.
+        float S_new = S * (corr[0] * corr[1]);
+        if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
+#pragma unroll
+          for (int b = 0; b < 16; ++b) acc[b] = acc[b] * S_new;
+          S_new = 1.0f;
+        }
+        S = S_new;
+        const float inv_s = 1.0f / S_new;
+        const float fs[2] = {corr[1] * inv_s, inv_s};
+        // P''^T as bf16 hi + lo: k index 8*grp + i holds tile a key 4*grp + i
+        // (i < 4), tile b key 4*grp + i - 4 (i >= 4), the order the V^T
+        // reads below produce.
+        bf16x8_t phi, plo;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
-          const int t = 2 * h + (i >> 2);
-          const float p0 = w[t][i & 3] * fs[t];
-          const float p1 = w[t][(i & 3) + 1] * fs[t];
+          const int u = i >> 2;
+          const float p0 = w[u][i & 3] * fs[u];
+          const float p1 = w[u][(i & 3) + 1] * fs[u];
           const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
           const float r0 = p0 - static_cast<float>(hb[0]);
           const float r1 = p1 - static_cast<float>(hb[1]);
           const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
-          phi[h][i] = hb[0];
-          phi[h][i + 1] = hb[1];
-          plo[h][i] = lb[0];
-          plo[h][i + 1] = lb[1];
+          phi[i] = hb[0];
+          phi[i + 1] = hb[1];
+          plo[i] = lb[0];
+          plo[i + 1] = lb[1];
         }
-      }
-      // ---- acc_stored += V^T . P''^T ----
 #pragma unroll
-      for (int b = 0; b < 16; ++b) {
-#pragma unroll
-        for (int h = 0; h < kHalves; ++h) {
-          if (key_base + 32 * h >= wave_count) continue;  // wave-uniform
+        for (int b = 0; b < 16; ++b) {
           const uint8_t* va = vl + (32 * h) * kVPitch + tr_off + 32 * b;
           const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(va));
           const s16x4_t v1 =
               __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(va + 16 * kVPitch));
           const s16x8_t a8 = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
           const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a8);
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, phi[h], acc[b], 0, 0, 0);
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, plo[h], acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, phi, acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, plo, acc[b], 0, 0, 0);
         }
       }
     }
