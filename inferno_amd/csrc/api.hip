@@ -710,7 +710,8 @@ int32_t ifr_merge_flash_partials(const void* image_dev, const int64_t* info,
   if (partials_bytes < info[3] * partial_stride * 4)
     return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
   IFR_HIP(ifr::launch_merge(static_cast<const int32_t*>(image_dev), static_cast<int>(info[1]),
-                            static_cast<int>(info[2]), static_cast<const float*>(partials),
+                            static_cast<int>(info[3]), static_cast<int>(info[2]),
+                            static_cast<const float*>(partials),
                             output, partial_stride, static_cast<int>(num_q),
                             static_cast<int>(head_dim), as_stream(stream)),
           "merge_flash_partials");

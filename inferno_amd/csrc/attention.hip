@@ -380,6 +380,105 @@ __global__ __launch_bounds__(256) void merge_kernel(
   }
 }
 
+template <int D>
+__global__ __launch_bounds__(256) void merge_sliced_kernel(
+    const int32_t* __restrict__ image, const float* __restrict__ partials,
+    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode) {
+  // The same merge with the head's dims spread over D/64 waves (blockIdx.z
+  // picks a 64-dim slice, a lane owns one dim): for units with many splits,
+  // whose acc chain is long, this puts D/64 times more waves on the loads.
+  constexpr int kAhead = 32;  // split loads in flight ahead of the fma chain
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * 4 + wave;
+  if (h >= num_q) return;
+  const int dim = 64 * blockIdx.z + lane;
+  const int32_t* unit = image + image[kHdrOffUnits] + blockIdx.x * kUnitWords;
+  const int out_row = unit[0];
+  const int stripe_base = unit[1];
+  const int n = unit[2];
+  const float* base = partials + static_cast<int64_t>(stripe_base) * partial_stride;
+  const int m_off = num_q * D;
+  const int l_off = m_off + num_q;
+  float acc = 0.0f;
+  float inv_l = 0.0f;
+  bool live = false;
+
+  if (mode == 1) {
+    const float lv = base[l_off + h];
+    if (lv > 0.0f) {
+      live = true;
+      inv_l = 1.0f / lv;
+      acc = base[static_cast<int64_t>(h) * D + dim];
+    }
+  } else {
+    // Lanes own splits.  Global max: wave max per 64-split chunk (exact in any
+    // order).  Corrections and L: the reference sums the splits in batches
+    // of 16, each batch by the halving tree (lane ^ 8, ^ 4, ^ 2, ^ 1 inside
+    // 16-lane groups), batches in order.  acc: the splits in order, loads
+    // issued kAhead at a time ahead of the fma chain.
+    float gm = kNegBig;
+    for (int s0 = 0; s0 < n; s0 += 64) {
+      float sm = kNegBig;
+      if (s0 + lane < n)
+        sm = base[static_cast<int64_t>(s0 + lane) * partial_stride + m_off + h];
+#pragma unroll
+      for (int msk = 1; msk < 64; msk <<= 1) sm = max_ref(sm, shfl_xor_f32(sm, msk));
+      gm = max_ref(gm, sm);
+    }
+    float gl = 0.0f;
+    bool first = true;
+    for (int s0 = 0; s0 < n; s0 += 64) {
+      float delta = kNegBig, ls = 0.0f;
+      if (s0 + lane < n) {
+        const float* sp = base + static_cast<int64_t>(s0 + lane) * partial_stride;
+        delta = sp[m_off + h] - gm;
+        ls = sp[l_off + h];
+      }
+      float cv = fexp(max_ref(-87.0f, delta));
+      cv = ls > 0.0f ? cv : 0.0f;
+      float prod = ls * cv;
+      prod = prod + shfl_xor_f32(prod, 8);
+      prod = prod + shfl_xor_f32(prod, 4);
+      prod = prod + shfl_xor_f32(prod, 2);
+      prod = prod + shfl_xor_f32(prod, 1);
+      const int cnt = min(64, n - s0);
+      for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
+      for (int j = 0; j < cnt; j += kAhead) {
+        float src[kAhead];
+        float cs[kAhead];
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+          cs[u] = 0.0f;
+          src[u] = 0.0f;
+          if (j + u < cnt) {
+            cs[u] = readlane_f32(cv, j + u);
+            src[u] = base[static_cast<int64_t>(s0 + j + u) * partial_stride +
+                          static_cast<int64_t>(h) * D + dim];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+          if (cs[u] <= 0.0f) continue;
+          if (first) {
+            acc = src[u] * cs[u];
+            first = false;
+          } else {
+            acc = fmaf(src[u], cs[u], acc);
+          }
+        }
+      }
+    }
+    if (gl > 0.0f) {
+      live = true;
+      inv_l = 1.0f / gl;
+    }
+  }
+
+  uint16_t* dst = out + (static_cast<int64_t>(out_row) * num_q + h) * D + dim;
+  *dst = static_cast<uint16_t>(live ? f32_to_bf16_bits(acc * inv_l) : 0u);
+}
+
 template <int D, int G>
 hipError_t launch_partials(const int32_t* image, int num_items, const void* q,
                            const void* k, const void* v, float* partials,
@@ -401,19 +500,31 @@ bool attention_shape_supported(int head_dim, int gqa) {
   return (head_dim == 256 || head_dim == 512) && (gqa == 1 || gqa == 2);
 }
 
-hipError_t launch_merge(const int32_t* image, int num_units, int mode,
+hipError_t launch_merge(const int32_t* image, int num_units, int num_stripes, int mode,
                         const float* partials, void* output, int64_t ps,
                         int num_q, int head_dim, hipStream_t stream) {
   if (num_units <= 0) return hipSuccess;
-  dim3 grid(num_units, (num_q + 3) / 4);
-  if (head_dim == 256)
-    hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image,
-                       partials, static_cast<uint16_t*>(output), ps, num_q,
-                       mode);
-  else
-    hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image,
-                       partials, static_cast<uint16_t*>(output), ps, num_q,
-                       mode);
+  // Measured on MI355X: a unit with 64 splits merges in half the time with
+  // one dim per lane over D/64 waves; with 8-16 splits per unit (batched
+  // decode) the one-wave-per-head kernel is faster.
+  const bool sliced = mode != 1 && num_stripes >= 32 * num_units;
+  dim3 grid(num_units, (num_q + 3) / 4, sliced ? head_dim / 64 : 1);
+  uint16_t* o = static_cast<uint16_t*>(output);
+  if (head_dim == 256) {
+    if (sliced)
+      hipLaunchKernelGGL(merge_sliced_kernel<256>, grid, dim3(256), 0, stream, image,
+                         partials, o, ps, num_q, mode);
+    else
+      hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image, partials, o,
+                         ps, num_q, mode);
+  } else {
+    if (sliced)
+      hipLaunchKernelGGL(merge_sliced_kernel<512>, grid, dim3(256), 0, stream, image,
+                         partials, o, ps, num_q, mode);
+    else
+      hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image, partials, o,
+                         ps, num_q, mode);
+  }
   return hipGetLastError();
 }
 
@@ -447,7 +558,7 @@ hipError_t launch_attention_bf16(const int32_t* image, int num_items,
                                         num_q, num_kv, head_dim, kv_stride,
                                         geom, stream);
   if (err != hipSuccess) return err;
-  return launch_merge(image, num_units, mode, partials, output, ps, num_q,
+  return launch_merge(image, num_units, num_items, mode, partials, output, ps, num_q,
                       head_dim, stream);
 }
 

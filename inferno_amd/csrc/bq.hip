@@ -426,7 +426,8 @@ hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_unit
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
-  return launch_merge(image, num_units, mode, partials, output, ps, num_q, head_dim, stream);
+  return launch_merge(image, num_units, num_items, mode, partials, output, ps, num_q, head_dim,
+                      stream);
 }
 
 }  // namespace ifr

@@ -48,7 +48,8 @@ hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
                                int head_dim, int64_t kv_stride, PagedGeom geom,
                                hipStream_t stream);
 
-hipError_t launch_merge(const int32_t* image_dev, int num_units, int mode,
+// num_stripes: partial stripes of the plan (one per split).
+hipError_t launch_merge(const int32_t* image_dev, int num_units, int num_stripes, int mode,
                         const float* partials, void* output,
                         int64_t partial_stride, int num_q, int head_dim,
                         hipStream_t stream);
