@@ -144,6 +144,33 @@ int32_t ifr_rope_cache_write(const void* image_dev, const int64_t* info,
                              int64_t page_mask, int64_t seq_len, int64_t half,
                              int64_t pair_stride, int64_t head_dim,
                              uint64_t stream);
+/* dispatch_rms_norm_qkv_heads (kernels/rmsnorm.mojo:168-215), in place: every
+ * q head scaled by q_weight, every k head by k_weight, every v head unscaled,
+ * each as rms_norm_row (:37-48): sum of squares in the reference's
+ * VDPBF16PS/accumulator/halving-tree order, inv = sqrt_n / sqrt(ssq + n_eps),
+ * y = bf16((x * inv) * w).  q, k, v: [seq_len][heads][head_dim] bf16;
+ * weights: [head_dim] bf16. */
+int32_t ifr_rms_norm_qkv_heads(void* q, void* k, void* v, const void* q_weight,
+                               const void* k_weight, int64_t num_q, int64_t num_kv,
+                               int64_t seq_len, int64_t head_dim, float sqrt_n,
+                               float n_eps, uint64_t stream);
+/* dispatch_rms_norm_qkv_heads followed by dispatch_rope_cache_write
+ * (kernels/rope.mojo:128-171), fused: one pass reads q/k/v once.  q ends
+ * normalised and rotated (as after the two reference calls); the k and v
+ * cache rows receive the normalised (k: rotated) rows.  Unlike the reference,
+ * k_src and v_src are left as passed (the reference normalises them in place
+ * and nothing reads them afterwards). */
+int32_t ifr_rms_norm_rope_cache_write(const void* image_dev, const int64_t* info,
+                                      void* q, const void* k_src, const void* v_src,
+                                      void* k_cache, void* v_cache,
+                                      const void* q_weight, const void* k_weight,
+                                      const float* cos_table, const float* sin_table,
+                                      int64_t num_q, int64_t num_kv,
+                                      int64_t page_shift, int64_t row_mask,
+                                      int64_t page_mask, int64_t seq_len,
+                                      int64_t half, int64_t pair_stride,
+                                      int64_t head_dim, float sqrt_n, float n_eps,
+                                      uint64_t stream);
 
 /* ---- bf16 paged attention (plan already uploaded) --------------------------
  * FlashAttentionKernel / FlashPrefill*Kernel (kernels/flash_attention.mojo,

@@ -42,6 +42,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                  I64, I64, I64, I64, I64, P_I64]),
     "ifr_rope_cache_write": (I32, [VP, P_I64, VP, VP, VP, VP, VP, VP, VP, I64, I64,
                                    I64, I64, I64, I64, I64, I64, I64, U64]),
+    "ifr_rms_norm_qkv_heads": (I32, [VP, VP, VP, VP, VP, I64, I64, I64, I64, F32, F32, U64]),
+    "ifr_rms_norm_rope_cache_write": (I32, [VP, P_I64, VP, VP, VP, VP, VP, VP, VP, VP, VP,
+                                            I64, I64, I64, I64, I64, I64, I64, I64, I64,
+                                            F32, F32, U64]),
     "ifr_attention_bf16": (I32, [VP, P_I64, VP, VP, VP, VP, VP, I64, I64, I64, I64,
                                  I64, I64, I64, I64, U64]),
     "ifr_flash_partials_bf16": (I32, [VP, P_I64, VP, VP, VP, VP, I64, I64, I64, I64, I64,

@@ -45,6 +45,29 @@ def dispatch_rope_cache_write(plan: AttentionPlan, q, k_src, v_src, k_cache, v_c
         plan.seq_len, half, pair_stride, head_dim, _stream()))
 
 
+def dispatch_rms_norm_qkv_heads(q, k, v, q_weight, k_weight, *, num_q: int, num_kv: int,
+                                seq_len: int, head_dim: int, sqrt_n: float,
+                                n_eps: float) -> None:
+    """dispatch_rms_norm_qkv_heads (kernels/rmsnorm.mojo:168-215), in place."""
+    check(lib().ifr_rms_norm_qkv_heads(_ptr(q), _ptr(k), _ptr(v), _ptr(q_weight),
+                                       _ptr(k_weight), num_q, num_kv, seq_len, head_dim,
+                                       sqrt_n, n_eps, _stream()))
+
+
+def dispatch_rms_norm_rope_cache_write(plan: AttentionPlan, q, k_src, v_src, k_cache, v_cache,
+                                       q_weight, k_weight, cos_table, sin_table, *,
+                                       num_q: int, num_kv: int, half: int, pair_stride: int,
+                                       head_dim: int, sqrt_n: float, n_eps: float) -> None:
+    """dispatch_rms_norm_qkv_heads fused ahead of dispatch_rope_cache_write
+    (kernels/rmsnorm.mojo:168-215, kernels/rope.mojo:128-171); k_src and
+    v_src are only read."""
+    check(lib().ifr_rms_norm_rope_cache_write(
+        _ptr(plan.image), plan.info_ptr, _ptr(q), _ptr(k_src), _ptr(v_src), _ptr(k_cache),
+        _ptr(v_cache), _ptr(q_weight), _ptr(k_weight), _ptr(cos_table), _ptr(sin_table),
+        num_q, num_kv, plan.page_shift, plan.page_len - 1, plan.page_mask, plan.seq_len,
+        half, pair_stride, head_dim, sqrt_n, n_eps, _stream()))
+
+
 def attention_bf16(plan: AttentionPlan, q, k_base, v_base, output, partials,
                    partial_stride: int, *, num_q: int, num_kv: int, head_dim: int,
                    kv_stride: int) -> None:

@@ -616,6 +616,62 @@ int32_t ifr_rope_cache_write(const void* image_dev, const int64_t* info,
   return ok();
 }
 
+int32_t ifr_rms_norm_qkv_heads(void* q, void* k, void* v, const void* q_weight,
+                               const void* k_weight, int64_t num_q, int64_t num_kv,
+                               int64_t seq_len, int64_t head_dim, float sqrt_n, float n_eps,
+                               uint64_t stream) {
+  if (!q || !k || !v || !q_weight || !k_weight) return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4))
+    return fail(IFR_EINVAL, "q, k and v must be 4-byte aligned");
+  if (num_q <= 0 || num_kv <= 0 || seq_len < 0 || num_q + 2 * num_kv > 192)
+    return fail(IFR_EINVAL, "need num_q, num_kv > 0 and num_q + 2*num_kv <= 192");
+  if (head_dim < 32 || head_dim > 1024 || head_dim % 32 != 0)
+    return fail(IFR_EINVAL, "head_dim must be a multiple of 32 in [32, 1024]");
+  IFR_HIP(ifr::launch_rms_norm_qkv(q, k, v, q_weight, k_weight, static_cast<int>(seq_len),
+                                   static_cast<int>(num_q), static_cast<int>(num_kv),
+                                   static_cast<int>(head_dim), sqrt_n, n_eps,
+                                   as_stream(stream)),
+          "rms_norm_qkv_heads");
+  return ok();
+}
+
+int32_t ifr_rms_norm_rope_cache_write(const void* image_dev, const int64_t* info, void* q,
+                                      const void* k_src, const void* v_src, void* k_cache,
+                                      void* v_cache, const void* q_weight,
+                                      const void* k_weight, const float* cos_table,
+                                      const float* sin_table, int64_t num_q, int64_t num_kv,
+                                      int64_t page_shift, int64_t row_mask, int64_t page_mask,
+                                      int64_t seq_len, int64_t half, int64_t pair_stride,
+                                      int64_t head_dim, float sqrt_n, float n_eps,
+                                      uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (seq_len != info[5]) return fail(IFR_EINVAL, "seq_len differs from the plan");
+  if (!image_dev || !q || !k_src || !v_src || !k_cache || !v_cache || !cos_table ||
+      !sin_table || !q_weight || !k_weight)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q, 4) || !aligned(k_src, 4) || !aligned(v_src, 4))
+    return fail(IFR_EINVAL, "q, k_src and v_src must be 4-byte aligned");
+  if (num_q <= 0 || num_kv <= 0 || num_q + 2 * num_kv > 192)
+    return fail(IFR_EINVAL, "need num_q, num_kv > 0 and num_q + 2*num_kv <= 192");
+  if (head_dim < 32 || head_dim > 1024 || head_dim % 32 != 0)
+    return fail(IFR_EINVAL, "head_dim must be a multiple of 32 in [32, 1024]");
+  if (half <= 0 || half > pair_stride || pair_stride + half > head_dim)
+    return fail(IFR_EINVAL, "bad rope geometry");
+  st = check_geometry(info, page_shift, row_mask, page_mask);
+  if (st) return st;
+  ifr::PagedGeom g{static_cast<int>(page_shift), static_cast<int>(row_mask),
+                   static_cast<int>(page_mask)};
+  IFR_HIP(ifr::launch_rms_rope_cache_write(
+              static_cast<const int32_t*>(image_dev), static_cast<int>(seq_len), q, k_src,
+              v_src, k_cache, v_cache, q_weight, k_weight, cos_table, sin_table,
+              static_cast<int>(num_q), static_cast<int>(num_kv), g, static_cast<int>(half),
+              static_cast<int>(pair_stride), static_cast<int>(head_dim), sqrt_n, n_eps,
+              as_stream(stream)),
+          "rms_norm_rope_cache_write");
+  return ok();
+}
+
 int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
                            const void* q, const void* k_base,
                            const void* v_base, void* output, void* partials,

@@ -63,6 +63,20 @@ hipError_t launch_rope_cache_write(const int32_t* image_dev, int seq_len,
                                    int pair_stride, int head_dim,
                                    hipStream_t stream);
 
+// In-place head RMS norm of q, k (with gains) and v.
+hipError_t launch_rms_norm_qkv(void* q, void* k, void* v, const void* q_w, const void* k_w,
+                               int seq_len, int num_q, int num_kv, int head_dim, float sqrt_n,
+                               float n_eps, hipStream_t stream);
+
+// The head RMS norm fused ahead of rope_cache_write.
+hipError_t launch_rms_rope_cache_write(const int32_t* image_dev, int seq_len, void* q,
+                                       const void* k_src, const void* v_src, void* k_cache,
+                                       void* v_cache, const void* q_w, const void* k_w,
+                                       const float* cos_table, const float* sin_table,
+                                       int num_q, int num_kv, PagedGeom geom, int half,
+                                       int pair_stride, int head_dim, float sqrt_n,
+                                       float n_eps, hipStream_t stream);
+
 hipError_t launch_bq_attn_prep(const int32_t* image_dev, int seq_len,
                                const void* q_src, const void* k_src,
                                const void* v_src, const void* q_norm,

@@ -41,6 +41,7 @@ _SIG = {
                                 I64, I64, I64, I64, I64]),
     "ifo_rope_cache_write": (None, [VP, I64, VP, VP, VP, VP, VP, VP, VP, VP, I64, I64, I64,
                                     I64, I64, I64, I64, I64, I64, I64, I64]),
+    "ifo_rms_norm_qkv_heads": (None, [VP, VP, VP, VP, VP, I64, I64, I64, I64, F32, F32]),
     "ifo_copy_jobs": (None, [VP, VP, I64]),
     "ifo_gather_rows": (None, [VP, VP, VP, I64, I64]),
     "ifo_fwht": (None, [VP, I64]),
@@ -164,6 +165,13 @@ def rope_cache_write(runs, base_rows, q, k_src, v_src, k_cache, v_cache, cos, si
                                _p(v_src), _p(k_cache), _p(v_cache), _p(cos), _p(sin),
                                num_q, num_kv, 1, 0, page_shift, row_mask, page_mask,
                                seq_len, half, pair_stride, head_dim)
+
+
+def rms_norm_qkv_heads(q, k, v, q_weight, k_weight, *, num_q, num_kv, seq_len, head_dim,
+                       sqrt_n, n_eps) -> None:
+    """dispatch_rms_norm_qkv_heads (kernels/rmsnorm.mojo:168-215), in place."""
+    lib().ifo_rms_norm_qkv_heads(_p(q), _p(k), _p(v), _p(q_weight), _p(k_weight), num_q,
+                                 num_kv, seq_len, head_dim, sqrt_n, n_eps)
 
 
 def copy_jobs(arena: np.ndarray, jobs) -> None:

@@ -812,6 +812,43 @@ static void rotate_pair_to(const uint16_t* src, uint16_t* dst,
     }
 }
 
+/* rms_norm_row over one head (kernels/rmsnorm.mojo:15-48) as
+ * ScaledNormKernel applies it per head row (:130-153):
+ *   sum_sq = dot_to_scalar[head_dim](x, x) (kernels/dot_products.mojo:
+ *     181-191): VDPBF16PS into pick_port_unroll(32, head_dim) accumulators
+ *     of 16 lanes, the accumulators added in order per lane
+ *     (panel_accs_to_scalars), then the halving-tree reduce_add;
+ *   inv = sqrt_n / sqrt(sum_sq + n_eps);
+ *   y = bf16((x * inv) * w)  (scaled: q and k heads), bf16(x * inv) (v). */
+static void rms_norm_head(uint16_t* row, const uint16_t* w, int64_t head_dim,
+                          float sqrt_n, float n_eps) {
+    int64_t pu = pick_port_unroll(2 * W, head_dim);
+    float ssq = bf16_dot_vdpbf16(row, row, head_dim, pu);
+    float inv = sqrt_n / sqrtf(ssq + n_eps);
+    for (int64_t e = 0; e < head_dim; e++) {
+        float x = ifo_bf16_to_f32(row[e]);
+        float y = x * inv;
+        if (w) y = y * ifo_bf16_to_f32(w[e]);
+        row[e] = ifo_f32_to_bf16(y);
+    }
+}
+
+/* dispatch_rms_norm_qkv_heads (kernels/rmsnorm.mojo:168-215), in place:
+ * q heads and k heads with their gains, v heads unscaled. */
+void ifo_rms_norm_qkv_heads(uint16_t* q, uint16_t* k, uint16_t* v,
+                            const uint16_t* q_weight, const uint16_t* k_weight,
+                            int64_t num_q, int64_t num_kv, int64_t seq_len,
+                            int64_t head_dim, float sqrt_n, float n_eps) {
+    for (int64_t t = 0; t < seq_len; t++) {
+        for (int64_t h = 0; h < num_q; h++)
+            rms_norm_head(q + (t * num_q + h) * head_dim, q_weight, head_dim, sqrt_n, n_eps);
+        for (int64_t h = 0; h < num_kv; h++) {
+            rms_norm_head(k + (t * num_kv + h) * head_dim, k_weight, head_dim, sqrt_n, n_eps);
+            rms_norm_head(v + (t * num_kv + h) * head_dim, NULL, head_dim, sqrt_n, n_eps);
+        }
+    }
+}
+
 void ifo_rope_cache_write(const int32_t* runs, int64_t num_runs,
                           const int32_t* base_rows, uint16_t* q,
                           const uint16_t* k_src, const uint16_t* v_src,

@@ -85,6 +85,10 @@ int ifo_attention(int64_t kind, const int32_t* runs, int64_t num_runs,
                   int64_t cap, int64_t threads);
 
 /* ---- append, page copy, gather ---------------------------------------- */
+void ifo_rms_norm_qkv_heads(uint16_t* q, uint16_t* k, uint16_t* v,
+                            const uint16_t* q_weight, const uint16_t* k_weight,
+                            int64_t num_q, int64_t num_kv, int64_t seq_len,
+                            int64_t head_dim, float sqrt_n, float n_eps);
 void ifo_rope_cache_write(const int32_t* runs, int64_t num_runs,
                           const int32_t* base_rows, uint16_t* q,
                           const uint16_t* k_src, const uint16_t* v_src,
