@@ -145,10 +145,31 @@ class DecodeBf16:
         self.out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
         self.q_host = self.q.cpu().numpy().view(np.uint16).copy()
         self.cap = a.cap
+        # Optional head RMS norm ahead of the append (dispatch_rms_norm_qkv_heads):
+        # "separate" runs it as its own in-place pass, "fused" folds it into the
+        # append kernel.
+        self.norm = a.norm
+        if self.norm != "none":
+            self.qw = torch.empty(HEAD_DIM, dtype=torch.int16, device=dev)
+            self.kw = torch.empty_like(self.qw)
+            _fill(self.qw, self.seed * 16 + 7, sid)
+            _fill(self.kw, self.seed * 16 + 8, sid)
+            self.name += f", head RMS norm {self.norm}"
+        if self.norm == "separate":
+            self.phases = ("norm",) + DecodeBf16.phases
 
     def launch(self, phase):
         A, p = self.A, self.plan
-        if phase == "append":
+        if phase == "norm":
+            A.dispatch_rms_norm_qkv_heads(self.q, self.ks, self.vs, self.qw, self.kw,
+                                          num_q=NUM_Q, num_kv=NUM_KV, seq_len=len(self.pos),
+                                          head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
+        elif phase == "append" and self.norm == "fused":
+            A.dispatch_rms_norm_rope_cache_write(
+                p, self.q, self.ks, self.vs, self.k, self.v, self.qw, self.kw, self.cos,
+                self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128, pair_stride=128,
+                head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
+        elif phase == "append":
             A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
                                         self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
                                         pair_stride=128, head_dim=HEAD_DIM)
@@ -506,6 +527,9 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--norm", choices=("none", "separate", "fused"), default="none",
+                    help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
+                         "own pass or fused into the append kernel")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="one 1 GiB device-to-device copy (torch's copy kernel): the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")

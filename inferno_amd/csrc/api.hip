@@ -623,8 +623,8 @@ int32_t ifr_rms_norm_qkv_heads(void* q, void* k, void* v, const void* q_weight,
   if (!q || !k || !v || !q_weight || !k_weight) return fail(IFR_EINVAL, "null pointer");
   if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4))
     return fail(IFR_EINVAL, "q, k and v must be 4-byte aligned");
-  if (num_q <= 0 || num_kv <= 0 || seq_len < 0 || num_q + 2 * num_kv > 192)
-    return fail(IFR_EINVAL, "need num_q, num_kv > 0 and num_q + 2*num_kv <= 192");
+  if (num_q <= 0 || num_kv <= 0 || seq_len < 0)
+    return fail(IFR_EINVAL, "need num_q, num_kv > 0 and seq_len >= 0");
   if (head_dim < 32 || head_dim > 1024 || head_dim % 32 != 0)
     return fail(IFR_EINVAL, "head_dim must be a multiple of 32 in [32, 1024]");
   IFR_HIP(ifr::launch_rms_norm_qkv(q, k, v, q_weight, k_weight, static_cast<int>(seq_len),
@@ -652,8 +652,7 @@ int32_t ifr_rms_norm_rope_cache_write(const void* image_dev, const int64_t* info
     return fail(IFR_EINVAL, "null pointer");
   if (!aligned(q, 4) || !aligned(k_src, 4) || !aligned(v_src, 4))
     return fail(IFR_EINVAL, "q, k_src and v_src must be 4-byte aligned");
-  if (num_q <= 0 || num_kv <= 0 || num_q + 2 * num_kv > 192)
-    return fail(IFR_EINVAL, "need num_q, num_kv > 0 and num_q + 2*num_kv <= 192");
+  if (num_q <= 0 || num_kv <= 0) return fail(IFR_EINVAL, "need num_q, num_kv > 0");
   if (head_dim < 32 || head_dim > 1024 || head_dim % 32 != 0)
     return fail(IFR_EINVAL, "head_dim must be a multiple of 32 in [32, 1024]");
   if (half <= 0 || half > pair_stride || pair_stride + half > head_dim)
