@@ -309,10 +309,22 @@ class DecodeBq:
         self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
         self.out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
         self.cap = a.cap
+        # Optional o_proj input quantisation (dispatch_bq_block_quant,
+        # block = head_dim): its own pass over the output, or fused into the merge.
+        self.oquant = a.oquant
+        if self.oquant != "none":
+            self.o_i8 = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int8, device=dev)
+            self.o_sa = torch.empty(B * NUM_Q, dtype=torch.float32, device=dev)
+            self.name += f", o_proj int8 block quant {self.oquant}"
+        if self.oquant == "separate":
+            self.phases = DecodeBq.phases + ("oquant",)
 
     def launch(self, phase):
         A, p = self.A, self.plan
-        if phase == "append":
+        if phase == "oquant":
+            A.dispatch_bq_block_quant(self.out, self.o_i8, self.o_sa, cols=NUM_Q * HEAD_DIM,
+                                      block=HEAD_DIM, seq_len=len(self.pos))
+        elif phase == "append":
             A.dispatch_bq_attn_prep(p, self.qs, self.kss, self.vss, self.qn, self.kn,
                                     self.q_i8, self.qb, self.fq, self.kc, self.ksc, self.vc,
                                     self.vsc, self.cos, self.sin, num_q=NUM_Q, num_kv=NUM_KV,
@@ -320,9 +332,12 @@ class DecodeBq:
                                     sqrt_n=16.0,
                                     n_eps=float(np.float32(256) * np.float32(1e-6)))
         else:
+            fused = self.oquant == "fused"
             A.bq_attention(p, self.q_i8, self.qb, self.fq, self.kc, self.ksc, self.vc,
                            self.vsc, self.out, self.partials, self.ps, num_q=NUM_Q,
-                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE)
+                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE,
+                           o_i8=self.o_i8 if fused else None,
+                           o_sa=self.o_sa if fused else None)
 
     def dominant_bytes(self) -> int:
         B = len(self.pos)
@@ -333,7 +348,11 @@ class DecodeBq:
     def step_bytes(self) -> int:
         B = len(self.pos)
         append = B * ((NUM_Q + 2 * NUM_KV) * HEAD_DIM * 2 + (NUM_Q + 2 * NUM_KV) * HEAD_DIM)
-        return self.dominant_bytes() + append
+        # o_proj quant: int8 codes + f32 scales written; the separate pass
+        # also re-reads the bf16 output.
+        oquant = {"none": 0, "fused": B * NUM_Q * (HEAD_DIM + 4),
+                  "separate": B * NUM_Q * (3 * HEAD_DIM + 4)}[self.oquant]
+        return self.dominant_bytes() + append + oquant
 
     def config(self) -> dict:
         return {"workload": self.name, "batch": len(self.pos),
@@ -530,6 +549,9 @@ def main() -> None:
     ap.add_argument("--norm", choices=("none", "separate", "fused"), default="none",
                     help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
                          "own pass or fused into the append kernel")
+    ap.add_argument("--oquant", choices=("none", "separate", "fused"), default="none",
+                    help="config 5: int8 block quant of the attention output for o_proj, "
+                         "as its own pass or fused into the merge")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="one 1 GiB device-to-device copy (torch's copy kernel): the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")

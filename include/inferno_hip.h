@@ -275,6 +275,30 @@ int32_t ifr_bq_attention(const void* image_dev, const int64_t* info,
                          int64_t num_kv, int64_t head_dim,
                          int64_t partial_stride, int64_t kv_stride,
                          int64_t page_len, int64_t page_mask, uint64_t stream);
+/* ifr_bq_attention followed by the o_proj input quantisation
+ * dispatch_bq_block_quant[block=head_dim, apply_fwht=False]
+ * (butterquant_kernels/linear.mojo:182-206, called at
+ * modeling/gemma_4_moe_bq.mojo:515-517 and :618-620), fused into the merge:
+ * o_i8[row][h*head_dim + d] and o_sa[row][h] = amax of head h of the bf16
+ * output row (quant_segment[store_divided=False], butterquant/kernels.mojo:
+ * 83-92).  `output` is written as by ifr_bq_attention. */
+int32_t ifr_bq_attention_block_quant(const void* image_dev, const int64_t* info,
+                                     const void* q_i8, const float* qi_bias,
+                                     const float* f_q, const void* k_base,
+                                     const float* k_scale, const void* v_base,
+                                     const float* v_scale, void* output, void* partials,
+                                     int64_t partials_bytes, int64_t num_q,
+                                     int64_t num_kv, int64_t head_dim,
+                                     int64_t partial_stride, int64_t kv_stride,
+                                     int64_t page_len, int64_t page_mask, void* o_i8,
+                                     float* o_sa, uint64_t stream);
+/* dispatch_bq_block_quant[apply_fwht=False] (butterquant_kernels/linear.mojo:
+ * 182-206, prepare_block_activation butterquant/runtime.mojo:63-80): for each
+ * of seq_len bf16 rows of `cols` elements and each block of `block` columns,
+ * x_sa[row][b] = amax and x_i8 = clamp(roundeven(x * 127/amax), -128, 127)
+ * (0 when amax is 0).  The FWHT variant (apply_fwht=True) is not provided. */
+int32_t ifr_bq_block_quant(const void* src, void* x_i8, float* x_sa, int64_t cols,
+                           int64_t block, int64_t seq_len, uint64_t stream);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                F32, U64]),
     "ifr_bq_attention": (I32, [VP, P_I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, I64, I64,
                                I64, I64, I64, I64, I64, I64, U64]),
+    "ifr_bq_attention_block_quant": (I32, [VP, P_I64, VP, VP, VP, VP, VP, VP, VP, VP, VP,
+                                           I64, I64, I64, I64, I64, I64, I64, I64, VP, VP,
+                                           U64]),
+    "ifr_bq_block_quant": (I32, [VP, VP, VP, I64, I64, I64, U64]),
     # ---- host-side page state (include/inferno_host.h) ----
     "ifr_splitmix64": (U64, [U64]),
     "ifr_hash_token_block": (U64, [VP, I64, I64]),

@@ -207,14 +207,28 @@ def dispatch_bq_attn_prep(plan: AttentionPlan, q_src, k_src, v_src, q_norm, k_no
 
 def bq_attention(plan: AttentionPlan, q_i8, qi_bias, f_q, k_base, k_scale, v_base,
                  v_scale, output, partials, partial_stride: int, *, num_q: int,
-                 num_kv: int, head_dim: int, kv_stride: int) -> None:
+                 num_kv: int, head_dim: int, kv_stride: int, o_i8=None, o_sa=None) -> None:
     """dispatch_bq_sliding_attention / dispatch_bq_full_attention
-    (butterquant_kernels/attention.mojo:354-491) on an uploaded plan."""
-    check(lib().ifr_bq_attention(
-        _ptr(plan.image), plan.info_ptr, _ptr(q_i8), _ptr(qi_bias), _ptr(f_q),
-        _ptr(k_base), _ptr(k_scale), _ptr(v_base), _ptr(v_scale), _ptr(output),
-        _ptr(partials), partials.numel() * 4, num_q, num_kv, head_dim, partial_stride,
-        kv_stride, plan.page_len, plan.page_mask, _stream()))
+    (butterquant_kernels/attention.mojo:354-491) on an uploaded plan.
+
+    With o_i8/o_sa, the o_proj input quantisation that follows it
+    (dispatch_bq_block_quant[block=head_dim], modeling/gemma_4_moe_bq.mojo:
+    515-517) is fused into the merge."""
+    args = (_ptr(plan.image), plan.info_ptr, _ptr(q_i8), _ptr(qi_bias), _ptr(f_q),
+            _ptr(k_base), _ptr(k_scale), _ptr(v_base), _ptr(v_scale), _ptr(output),
+            _ptr(partials), partials.numel() * 4, num_q, num_kv, head_dim, partial_stride,
+            kv_stride, plan.page_len, plan.page_mask)
+    if o_i8 is None and o_sa is None:
+        check(lib().ifr_bq_attention(*args, _stream()))
+    else:
+        check(lib().ifr_bq_attention_block_quant(*args, _ptr(o_i8), _ptr(o_sa), _stream()))
+
+
+def dispatch_bq_block_quant(src, x_i8, x_sa, *, cols: int, block: int, seq_len: int) -> None:
+    """dispatch_bq_block_quant[apply_fwht=False] (butterquant_kernels/linear.mojo:
+    182-206): per-block absmax int8 of seq_len bf16 rows."""
+    check(lib().ifr_bq_block_quant(_ptr(src), _ptr(x_i8), _ptr(x_sa), cols, block, seq_len,
+                                   _stream()))
 
 
 __all__ = [
@@ -222,5 +236,5 @@ __all__ = [
     "dispatch_rope_cache_write", "attention_bf16", "flash_partials_bf16",
     "merge_flash_partials", "dispatch_sliding_attention",
     "dispatch_full_attention", "dispatch_copy_jobs", "dispatch_gather_rows",
-    "dispatch_bq_attn_prep", "bq_attention",
+    "dispatch_bq_attn_prep", "bq_attention", "dispatch_bq_block_quant",
 ]

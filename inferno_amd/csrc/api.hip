@@ -930,13 +930,16 @@ int32_t ifr_bq_attn_prep(const void* image_dev, const int64_t* info,
   return ok();
 }
 
-int32_t ifr_bq_attention(const void* image_dev, const int64_t* info,
-                         const void* q_i8, const float* qi_bias, const float* f_q,
-                         const void* k_base, const float* k_scale, const void* v_base,
-                         const float* v_scale, void* output, void* partials,
-                         int64_t partials_bytes, int64_t num_q, int64_t num_kv,
-                         int64_t head_dim, int64_t partial_stride, int64_t kv_stride,
-                         int64_t page_len, int64_t page_mask, uint64_t stream) {
+}  // extern "C"
+
+namespace {
+int32_t bq_attention(const void* image_dev, const int64_t* info, const void* q_i8,
+                     const float* qi_bias, const float* f_q, const void* k_base,
+                     const float* k_scale, const void* v_base, const float* v_scale,
+                     void* output, void* partials, int64_t partials_bytes, int64_t num_q,
+                     int64_t num_kv, int64_t head_dim, int64_t partial_stride,
+                     int64_t kv_stride, int64_t page_len, int64_t page_mask,
+                     uint64_t stream, void* o_i8, float* o_sa) {
   int32_t st = check_info(info);
   if (st) return st;
   st = check_attention_shapes(num_q, num_kv, head_dim, partial_stride, kv_stride, 1);
@@ -963,8 +966,59 @@ int32_t ifr_bq_attention(const void* image_dev, const int64_t* info,
                                    static_cast<float*>(partials), partial_stride,
                                    static_cast<int>(num_q), static_cast<int>(num_kv),
                                    static_cast<int>(head_dim), kv_stride, g,
-                                   as_stream(stream)),
+                                   as_stream(stream), static_cast<int8_t*>(o_i8), o_sa),
           "bq_attention");
+  return ok();
+}
+}  // namespace
+
+extern "C" {
+
+int32_t ifr_bq_attention(const void* image_dev, const int64_t* info,
+                         const void* q_i8, const float* qi_bias, const float* f_q,
+                         const void* k_base, const float* k_scale, const void* v_base,
+                         const float* v_scale, void* output, void* partials,
+                         int64_t partials_bytes, int64_t num_q, int64_t num_kv,
+                         int64_t head_dim, int64_t partial_stride, int64_t kv_stride,
+                         int64_t page_len, int64_t page_mask, uint64_t stream) {
+  return bq_attention(image_dev, info, q_i8, qi_bias, f_q, k_base, k_scale, v_base, v_scale,
+                      output, partials, partials_bytes, num_q, num_kv, head_dim,
+                      partial_stride, kv_stride, page_len, page_mask, stream, nullptr,
+                      nullptr);
+}
+
+int32_t ifr_bq_attention_block_quant(const void* image_dev, const int64_t* info,
+                                     const void* q_i8, const float* qi_bias,
+                                     const float* f_q, const void* k_base,
+                                     const float* k_scale, const void* v_base,
+                                     const float* v_scale, void* output, void* partials,
+                                     int64_t partials_bytes, int64_t num_q, int64_t num_kv,
+                                     int64_t head_dim, int64_t partial_stride,
+                                     int64_t kv_stride, int64_t page_len, int64_t page_mask,
+                                     void* o_i8, float* o_sa, uint64_t stream) {
+  if (!o_i8 || !o_sa) return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(o_i8, 16) || !aligned(o_sa, 4))
+    return fail(IFR_EINVAL, "o_i8 must be 16-byte aligned, o_sa 4-byte aligned");
+  return bq_attention(image_dev, info, q_i8, qi_bias, f_q, k_base, k_scale, v_base, v_scale,
+                      output, partials, partials_bytes, num_q, num_kv, head_dim,
+                      partial_stride, kv_stride, page_len, page_mask, stream, o_i8, o_sa);
+}
+
+int32_t ifr_bq_block_quant(const void* src, void* x_i8, float* x_sa, int64_t cols,
+                           int64_t block, int64_t seq_len, uint64_t stream) {
+  if (seq_len < 0) return fail(IFR_EINVAL, "seq_len must be >= 0");
+  if (block <= 0 || block % 16 != 0 || block > (1 << 20))
+    return fail(IFR_EINVAL, "block must be a positive multiple of 16 (the f32 SIMD width)");
+  if (cols <= 0 || cols % block != 0) return fail(IFR_EINVAL, "cols must be block-aligned");
+  if (seq_len == 0) return ok();
+  if (!src || !x_i8 || !x_sa) return fail(IFR_EINVAL, "null pointer");
+  if (seq_len > (int64_t{1} << 31) || seq_len * (cols / block) > (int64_t{1} << 32))
+    return fail(IFR_EINVAL, "too many blocks for one launch");
+  if (!aligned(src, 2) || !aligned(x_sa, 4))
+    return fail(IFR_EINVAL, "src must be 2-byte aligned, x_sa 4-byte aligned");
+  IFR_HIP(ifr::launch_bq_block_quant(src, x_i8, x_sa, cols, static_cast<int>(block),
+                                     seq_len, as_stream(stream)),
+          "bq_block_quant");
   return ok();
 }
 

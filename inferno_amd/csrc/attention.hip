@@ -263,7 +263,8 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(
     const int32_t* __restrict__ image, const float* __restrict__ partials,
-    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode) {
+    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode,
+    int8_t* __restrict__ q_out, float* __restrict__ q_scale) {
   constexpr int DPL = D / 64;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -377,6 +378,41 @@ __global__ __launch_bounds__(256) void merge_kernel(
   } else {
     *reinterpret_cast<uint4*>(dst) =
         make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  }
+  if (q_out) {
+    // The o_proj input step fused in: per-head absmax int8 of the bf16
+    // outputs just stored (dispatch_bq_block_quant[block=head_dim,
+    // apply_fwht=False], butterquant_kernels/linear.mojo:182-206; quant_segment,
+    // butterquant/kernels.mojo:83-92).
+    float vals[DPL];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; e += 2) {
+      vals[e] = bf16_lo(packed[e / 2]);
+      vals[e + 1] = bf16_hi(packed[e / 2]);
+      amax = fmaxf(amax, fmaxf(fabsf(vals[e]), fabsf(vals[e + 1])));
+    }
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, msk));
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t codes[DPL / 4];
+#pragma unroll
+    for (int c = 0; c < DPL / 4; ++c) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float r = fminf(fmaxf(rintf(vals[4 * c + b] * inv), -128.0f), 127.0f);
+        word |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xFFu) << (8 * b);
+      }
+      codes[c] = word;
+    }
+    int8_t* qd = q_out + (static_cast<int64_t>(out_row) * num_q + h) * D + DPL * lane;
+    if constexpr (DPL == 4) {
+      *reinterpret_cast<uint32_t*>(qd) = codes[0];
+    } else {
+      *reinterpret_cast<uint2*>(qd) = make_uint2(codes[0], codes[1]);
+    }
+    if (lane == 0) q_scale[static_cast<int64_t>(out_row) * num_q + h] = amax;
   }
 }
 
@@ -502,12 +538,14 @@ bool attention_shape_supported(int head_dim, int gqa) {
 
 hipError_t launch_merge(const int32_t* image, int num_units, int num_stripes, int mode,
                         const float* partials, void* output, int64_t ps,
-                        int num_q, int head_dim, hipStream_t stream) {
+                        int num_q, int head_dim, hipStream_t stream, int8_t* q_out,
+                        float* q_scale) {
   if (num_units <= 0) return hipSuccess;
   // Measured on MI355X: a unit with 64 splits merges in half the time with
   // one dim per lane over D/64 waves; with 8-16 splits per unit (batched
-  // decode) the one-wave-per-head kernel is faster.
-  const bool sliced = mode != 1 && num_stripes >= 32 * num_units;
+  // decode) the one-wave-per-head kernel is faster.  The fused int8 epilogue
+  // needs a whole head per wave.
+  const bool sliced = mode != 1 && num_stripes >= 32 * num_units && q_out == nullptr;
   dim3 grid(num_units, (num_q + 3) / 4, sliced ? head_dim / 64 : 1);
   uint16_t* o = static_cast<uint16_t*>(output);
   if (head_dim == 256) {
@@ -516,14 +554,14 @@ hipError_t launch_merge(const int32_t* image, int num_units, int num_stripes, in
                          partials, o, ps, num_q, mode);
     else
       hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image, partials, o,
-                         ps, num_q, mode);
+                         ps, num_q, mode, q_out, q_scale);
   } else {
     if (sliced)
       hipLaunchKernelGGL(merge_sliced_kernel<512>, grid, dim3(256), 0, stream, image,
                          partials, o, ps, num_q, mode);
     else
       hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image, partials, o,
-                         ps, num_q, mode);
+                         ps, num_q, mode, q_out, q_scale);
   }
   return hipGetLastError();
 }

@@ -415,7 +415,7 @@ hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_unit
                                const void* v_base, const float* v_scale, void* output,
                                float* partials, int64_t ps, int num_q, int num_kv,
                                int head_dim, int64_t kv_stride, PagedGeom geom,
-                               hipStream_t stream) {
+                               hipStream_t stream, int8_t* q_out, float* q_scale) {
   if (num_items > 0) {
     dim3 grid(num_items, (num_kv + 3) / 4);
     hipLaunchKernelGGL(bq_partial_kernel<2>, grid, dim3(256), 0, stream, image,
@@ -427,7 +427,44 @@ hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_unit
     if (err != hipSuccess) return err;
   }
   return launch_merge(image, num_units, num_items, mode, partials, output, ps, num_q, head_dim,
-                      stream);
+                      stream, q_out, q_scale);
+}
+
+namespace {
+// quant_segment[store_divided=False] (butterquant/kernels.mojo:83-92) on one
+// block of one token: sa = amax, inv = 127/amax (0 if amax is 0), codes =
+// clamp(roundeven(x * inv), -128, 127).  One wave per (token, block).
+__global__ __launch_bounds__(256) void bq_block_quant_kernel(
+    const uint16_t* __restrict__ src, int8_t* __restrict__ x_i8, float* __restrict__ x_sa,
+    int64_t cols, int block, int64_t n_pairs) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t pair = static_cast<int64_t>(blockIdx.x) * 4 + wave;  // (token, block)
+  if (pair >= n_pairs) return;
+  const int64_t base = pair * block;  // blocks tile each row: token*cols + b*block
+  const uint16_t* s = src + base;
+  float amax = 0.0f;
+  for (int i = lane; i < block; i += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(s[i])));
+#pragma unroll
+  for (int msk = 1; msk < 64; msk <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, msk));
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  int8_t* d = x_i8 + base;
+  for (int i = lane; i < block; i += 64) {
+    const float r = fminf(fmaxf(rintf(bf16_to_f32(s[i]) * inv), -128.0f), 127.0f);
+    d[i] = static_cast<int8_t>(static_cast<int32_t>(r));
+  }
+  if (lane == 0) x_sa[pair] = amax;
+}
+}  // namespace
+
+hipError_t launch_bq_block_quant(const void* src, void* x_i8, float* x_sa, int64_t cols,
+                                 int block, int64_t seq_len, hipStream_t stream) {
+  if (seq_len <= 0) return hipSuccess;
+  const int64_t pairs = static_cast<int64_t>(seq_len) * (cols / block);
+  hipLaunchKernelGGL(bq_block_quant_kernel, dim3(static_cast<unsigned>((pairs + 3) / 4)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(src),
+                     static_cast<int8_t*>(x_i8), x_sa, cols, block, pairs);
+  return hipGetLastError();
 }
 
 }  // namespace ifr

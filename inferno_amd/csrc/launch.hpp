@@ -46,13 +46,21 @@ hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
                                void* output, float* partials,
                                int64_t partial_stride, int num_q, int num_kv,
                                int head_dim, int64_t kv_stride, PagedGeom geom,
-                               hipStream_t stream);
+                               hipStream_t stream, int8_t* q_out = nullptr,
+                               float* q_scale = nullptr);
 
-// num_stripes: partial stripes of the plan (one per split).
+// dispatch_bq_block_quant[apply_fwht=False]: per-block absmax int8 of bf16
+// rows [seq_len][cols]; cols a multiple of block.
+hipError_t launch_bq_block_quant(const void* src, void* x_i8, float* x_sa, int64_t cols,
+                                 int block, int64_t seq_len, hipStream_t stream);
+
+// num_stripes: partial stripes of the plan (one per split).  q_out / q_scale
+// (optional): per-head absmax int8 of the merged outputs, fused.
 hipError_t launch_merge(const int32_t* image_dev, int num_units, int num_stripes, int mode,
                         const float* partials, void* output,
                         int64_t partial_stride, int num_q, int head_dim,
-                        hipStream_t stream);
+                        hipStream_t stream, int8_t* q_out = nullptr,
+                        float* q_scale = nullptr);
 
 hipError_t launch_rope_cache_write(const int32_t* image_dev, int seq_len,
                                    void* q, const void* k_src,

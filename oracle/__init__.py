@@ -47,6 +47,7 @@ _SIG = {
     "ifo_fwht": (None, [VP, I64]),
     "ifo_head_inv_rms": (F32, [VP, I64, F32, F32]),
     "ifo_absmax_quantize": (F32, [VP, I64, VP, VP]),
+    "ifo_bq_block_quant": (None, [VP, VP, VP, I64, I64, I64]),
     "ifo_bq_attn_prep": (None, [VP, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP,
                                 VP, VP, VP, I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                 I64, I64, F32, F32]),
@@ -198,6 +199,16 @@ def absmax_quantize(x) -> tuple[np.ndarray, float, int]:
     qs = np.zeros(1, dtype=np.int32)
     amax = lib().ifo_absmax_quantize(_p(x), x.size, _p(q), _p(qs))
     return q, float(amax), int(qs[0])
+
+
+def bq_block_quant(src, cols: int, block: int) -> tuple[np.ndarray, np.ndarray]:
+    """Per-block absmax int8 of bf16 rows: (codes [rows][cols], scales [rows][cols/block])."""
+    src = np.ascontiguousarray(src, dtype=np.uint16).reshape(-1, cols)
+    rows = src.shape[0]
+    x_i8 = np.zeros((rows, cols), dtype=np.int8)
+    x_sa = np.zeros((rows, cols // block), dtype=np.float32)
+    lib().ifo_bq_block_quant(_p(src), _p(x_i8), _p(x_sa), cols, block, rows)
+    return x_i8, x_sa
 
 
 def head_inv_rms(x, sqrt_n, n_eps) -> float:

@@ -34,6 +34,11 @@
  *                       impulse/constant special cases.
  *   ifo_absmax_quantize definition (butterquant.md:15-21): max code 127,
  *                       |code| <= 128, dequantized error <= amax/254.
+ *   ifo_bq_block_quant  known answers with exact scales (amax 127 and 254 give
+ *                       inv 1 and 0.5, so ties land on .5 and must go to
+ *                       even), the all-zero block (codes 0, scale 0), the
+ *                       amax element's code +-127, the half-step error bound,
+ *                       and blocks that do not see each other's values.
  *   ifo_bq_attention    the reference's own scalar reference_head with exact
  *                       exp (tests/test_sliding_attention_degree_parity.mojo:
  *                       93-141) on the reference test's 10-step schedule at
@@ -965,6 +970,36 @@ float ifo_absmax_quantize(const float* x, int64_t n, int8_t* out,
     }
     if (qsum) *qsum = s;
     return amax;
+}
+
+/* dispatch_bq_block_quant[apply_fwht=False] (butterquant_kernels/linear.mojo:
+ * 151-206): per token, prepare_block_activation (butterquant/runtime.mojo:
+ * 63-80) widens the bf16 row to f32 and quantize_activation_per_block
+ * (butterquant/quantize.mojo:13-23) runs quant_segment[store_divided=False]
+ * (butterquant/kernels.mojo:83-92) on each block: sa = amax (row_absmax
+ * :63-70), inv = 127/amax or 0, code = quantize_i8 (simd_math/ops.mojo:26-31)
+ * = clamp(roundeven(x * inv), -128, 127). */
+void ifo_bq_block_quant(const uint16_t* src, int8_t* x_i8, float* x_sa,
+                        int64_t cols, int64_t block, int64_t seq_len) {
+    int64_t nb = cols / block;
+    for (int64_t t = 0; t < seq_len; t++) {
+        for (int64_t b = 0; b < nb; b++) {
+            const uint16_t* s = src + t * cols + b * block;
+            int8_t* d = x_i8 + t * cols + b * block;
+            float amax = 0.0f;
+            for (int64_t i = 0; i < block; i++) {
+                float a = fabsf(ifo_bf16_to_f32(s[i]));
+                amax = a > amax ? a : amax;
+            }
+            x_sa[t * nb + b] = amax;
+            float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+            for (int64_t i = 0; i < block; i++) {
+                float r = rintf(ifo_bf16_to_f32(s[i]) * inv);
+                r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+                d[i] = (int8_t)(int32_t)r;
+            }
+        }
+    }
 }
 
 /* prep_head_qk_i8 (butterquant/head_prep.mojo:39-70). */

@@ -108,6 +108,8 @@ void  ifo_fwht(float* v, int64_t n);
 float ifo_head_inv_rms(const float* x, int64_t n, float sqrt_n, float n_eps);
 float ifo_absmax_quantize(const float* x, int64_t n, int8_t* out,
                           int32_t* qsum);
+void  ifo_bq_block_quant(const uint16_t* src, int8_t* x_i8, float* x_sa,
+                         int64_t cols, int64_t block, int64_t seq_len);
 void ifo_bq_attn_prep(const int32_t* runs, int64_t num_runs,
                       const int32_t* base_rows, const uint16_t* q_src,
                       const uint16_t* k_src, const uint16_t* v_src,

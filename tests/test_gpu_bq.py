@@ -67,6 +67,21 @@ def _prep_and_attend(state, runs, rows, q, k, v, norm_q, norm_k, cos, sin, *, ki
     partials, ps = A.partials_buffer(plan, nq, d)
     A.bq_attention(plan, dq_i8, dqb, dfq, state.dk, state.dks, state.dv, state.dvs, out,
                    partials, ps, num_q=nq, num_kv=nkv, head_dim=d, kv_stride=nkv * d)
+    # The same attention with the o_proj input quantisation fused into the
+    # merge: identical bf16 output, and codes/scales bit-exact with the
+    # oracle's block quant of that output (head_dim blocks).
+    out2 = empty_dev(seq_len * nq * d, np.uint16)
+    o_i8 = empty_dev(seq_len * nq * d, np.int8)
+    o_sa = empty_dev(seq_len * nq, np.float32)
+    A.bq_attention(plan, dq_i8, dqb, dfq, state.dk, state.dks, state.dv, state.dvs, out2,
+                   partials, ps, num_q=nq, num_kv=nkv, head_dim=d, kv_stride=nkv * d,
+                   o_i8=o_i8, o_sa=o_sa)
+    got_out = from_dev(out, np.uint16)
+    assert np.array_equal(from_dev(out2, np.uint16), got_out), "fused quant changed output"
+    want_i8, want_sa = oracle.bq_block_quant(got_out, cols=nq * d, block=d)
+    assert np.array_equal(from_dev(o_i8, np.int8).reshape(seq_len, nq * d), want_i8)
+    assert np.array_equal(from_dev(o_sa, np.float32).view(np.uint32),
+                          want_sa.reshape(-1).view(np.uint32))
 
     q_i8 = np.zeros(seq_len * nq * d, dtype=np.int8)
     qb = np.zeros(seq_len * nq, dtype=np.float32)
@@ -184,3 +199,30 @@ def test_bq_batched_decode_with_outliers(cap):
     r = compare_bf16(got, ref)
     print(f"  bq decode cap={cap}: {r}", flush=True)
     assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+
+
+@pytest.mark.parametrize("cols,block,rows", [(8 * 256, 256, 37), (4 * 512, 512, 5),
+                                             (3 * 64, 64, 129), (2 * 256, 256, 0)])
+def test_block_quant_bit_exact(cols, block, rows):
+    """dispatch_bq_block_quant standalone: codes and scales bit-exact with the
+    oracle, including an all-zero block, a single loud outlier and exact .5
+    ties (values 0.5/1.5/2.5 under amax 127)."""
+    announce(f"bq block quant cols={cols} block={block} rows={rows}")
+    rng = np.random.default_rng(cols + rows)
+    x = (rng.standard_normal((rows, cols)) * rng.uniform(0.01, 30, (rows, 1))).astype(
+        np.float32)
+    if rows >= 3:
+        x[0, :block] = 0.0
+        x[1, block + 3] = 3e4
+        x[2, :block] = np.resize(np.array([127.0, 0.5, 1.5, 2.5, -0.5, -2.5], np.float32),
+                                 block)
+    src = bq.to_bf16_bits(x)
+    x_i8 = empty_dev(max(rows * cols, 1), np.int8)
+    x_sa = empty_dev(max(rows * cols // block, 1), np.float32)
+    A.dispatch_bq_block_quant(to_dev(src), x_i8, x_sa, cols=cols, block=block, seq_len=rows)
+    if rows == 0:
+        return
+    want_i8, want_sa = oracle.bq_block_quant(src, cols=cols, block=block)
+    assert np.array_equal(from_dev(x_i8, np.int8).reshape(rows, cols), want_i8)
+    assert np.array_equal(from_dev(x_sa, np.float32).view(np.uint32),
+                          want_sa.reshape(-1).view(np.uint32))

@@ -191,6 +191,50 @@ def test_absmax_quantize_definition():
     assert amax == np.float32(1e-10) and not q.any()
 
 
+def _bf16(vals) -> np.ndarray:
+    return oracle.f32_to_bf16(np.asarray(vals, dtype=np.float32))
+
+
+def test_bq_block_quant_known_answers():
+    # amax 127 gives inv exactly 1 and amax 254 gives 0.5, so the codes are
+    # the values themselves (halved); ties at .5 go to even, not away from 0.
+    block = 16
+    row0 = [127.0, 0.5, 1.5, 2.5, 3.5, -0.5, -1.5, -2.5, -3.5, 4.0, -127.0, 0, 0, 0, 0, 0]
+    row1 = [254.0, 5.0, 7.0, -5.0, -7.0, 1.0, 3.0, 0, 0, 0, 0, 0, 0, 0, 0, -254.0]
+    zero = [0.0] * block
+    src = _bf16(row0 + row1 + zero + row1)
+    codes, scales = oracle.bq_block_quant(src, cols=2 * block, block=block)
+    assert codes.shape == (2, 32) and scales.shape == (2, 2)
+    assert list(codes[0, :16]) == [127, 0, 2, 2, 4, 0, -2, -2, -4, 4, -127, 0, 0, 0, 0, 0]
+    assert list(codes[0, 16:]) == [127, 2, 4, -2, -4, 0, 2, 0, 0, 0, 0, 0, 0, 0, 0, -127]
+    assert not codes[1, :16].any()
+    assert list(codes[1, 16:]) == list(codes[0, 16:])
+    assert scales.tolist() == [[127.0, 254.0], [0.0, 254.0]]
+
+
+def test_bq_block_quant_bounds_and_block_independence():
+    rng = np.random.default_rng(5)
+    cols, block = 512, 256
+    x = (rng.standard_normal((7, cols)) * rng.uniform(0.01, 50, (7, 1))).astype(np.float32)
+    x[3, :block] *= 1e4  # a loud block must not change its neighbour's codes
+    src = _bf16(x)
+    xf = oracle.bf16_to_f32(src).astype(np.float64).reshape(7, cols)
+    codes, scales = oracle.bq_block_quant(src, cols=cols, block=block)
+    for t in range(7):
+        for b in range(2):
+            blk = xf[t, b * block:(b + 1) * block]
+            amax = np.max(np.abs(blk))
+            assert scales[t, b] == np.float32(amax)
+            c = codes[t, b * block:(b + 1) * block].astype(np.int64)
+            i = int(np.argmax(np.abs(blk)))
+            assert c[i] == (127 if blk[i] > 0 else -127)
+            assert np.all(np.abs(c) <= 127)
+            assert np.max(np.abs(c * amax / 127 - blk)) <= amax / 254 * (1 + 1e-5)
+    alone, alone_sa = oracle.bq_block_quant(src.reshape(7, cols)[3, block:], cols=block,
+                                            block=block)
+    assert np.array_equal(alone[0], codes[3, block:]) and alone_sa[0, 0] == scales[3, 1]
+
+
 def test_head_inv_rms_chain():
     rng = np.random.default_rng(3)
     x = rng.standard_normal(256).astype(np.float32)
