@@ -34,6 +34,9 @@
  *                       impulse/constant special cases.
  *   ifo_absmax_quantize definition (butterquant.md:15-21): max code 127,
  *                       |code| <= 128, dequantized error <= amax/254.
+ *   ifo_rms_norm_qkv_heads closed forms on constant rows, exact power-of-two
+ *                       scale invariance, unit RMS of the output, gains on q
+ *                       and k only, float64 RMS norm to one bf16 rounding.
  *   ifo_bq_block_quant  known answers with exact scales (amax 127 and 254 give
  *                       inv 1 and 0.5, so ties land on .5 and must go to
  *                       even), the all-zero block (codes 0, scale 0), the
@@ -47,7 +50,9 @@
  * Parity left unpinned (no way to run Mojo here): the lane order of Mojo's
  * SIMD.reduce_add (taken as the halving tree of SIMD.reduce), FMA contraction
  * of `a*b - c*d` in RoPE and of `l*corr + sum` (taken as not contracted), the
- * f32->bf16 cast (taken as RNE, butterquant/convert.mojo:14-17) and fptosi in
+ * f32->bf16 cast (taken as RNE, butterquant/convert.mojo:14-17), the order of
+ * the sum of squares in the head RMS norm (VDPBF16PS pairs into port_unroll
+ * accumulators, below float64 agreement) and fptosi in
  * the fast exp (taken as truncation toward zero).
  *
  * The reference targets AVX-512, so its f32 SIMD width W, and with it the
