@@ -30,6 +30,7 @@ import numpy as np
 METRIC = "paged decode-attn GB/s (% HBM peak) + µs/layer, B=64 ctx≤32k bf16"
 HBM_PEAK_GBS = 8000.0
 NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
+HIDDEN = 2816  # Gemma 4 26B-A4B hidden size: o_proj maps 16 x 256 -> 2816
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
 DEFAULT_CAP = {1: 64, 2: 512, 3: 512, 4: 16, 5: 2048}
@@ -157,10 +158,24 @@ class DecodeBf16:
             self.name += f", head RMS norm {self.norm}"
         if self.norm == "separate":
             self.phases = ("norm",) + DecodeBf16.phases
+        # Optional o_proj after the merge (dispatch_gemm_cols, rows = HIDDEN):
+        # a random bf16 weight [HIDDEN][num_q * head_dim].
+        self.oproj = a.oproj
+        if self.oproj:
+            self.o_w = torch.empty(HIDDEN * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+            _fill(self.o_w, self.seed * 16 + 9, sid, scale=0.02)
+            self.o_out = torch.empty(B * HIDDEN, dtype=torch.int16, device=dev)
+            self.o_ws = A.gemm_cols_workspace(HIDDEN, NUM_Q * HEAD_DIM, B, device=dev)
+            self.phases = self.phases + ("oproj",)
+            self.name += ", o_proj bf16 GEMM"
 
     def launch(self, phase):
         A, p = self.A, self.plan
-        if phase == "norm":
+        if phase == "oproj":
+            A.dispatch_gemm_cols(self.out, self.o_w, self.o_out, rows=HIDDEN,
+                                 cols=NUM_Q * HEAD_DIM, seq_len=len(self.pos),
+                                 workspace=self.o_ws)
+        elif phase == "norm":
             A.dispatch_rms_norm_qkv_heads(self.q, self.ks, self.vs, self.qw, self.kw,
                                           num_q=NUM_Q, num_kv=NUM_KV, seq_len=len(self.pos),
                                           head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
@@ -197,7 +212,10 @@ class DecodeBf16:
         """Whole step: the partial kernel's bytes, the output and the append."""
         B = len(self.pos)
         append = B * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 2)
-        return self.dominant_bytes() + B * NUM_Q * HEAD_DIM * 2 + append
+        # o_proj: its weight, the attention output read back, the bf16 result.
+        oproj = (HIDDEN * NUM_Q * HEAD_DIM * 2 + B * NUM_Q * HEAD_DIM * 2 + B * HIDDEN * 2
+                 if self.oproj else 0)
+        return self.dominant_bytes() + B * NUM_Q * HEAD_DIM * 2 + append + oproj
 
     def config(self) -> dict:
         return {"workload": self.name, "batch": len(self.pos),
@@ -549,6 +567,8 @@ def main() -> None:
     ap.add_argument("--norm", choices=("none", "separate", "fused"), default="none",
                     help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
                          "own pass or fused into the append kernel")
+    ap.add_argument("--oproj", action="store_true",
+                    help="configs 1-3: the bf16 o_proj GEMM after the merge")
     ap.add_argument("--oquant", choices=("none", "separate", "fused"), default="none",
                     help="config 5: int8 block quant of the attention output for o_proj, "
                          "as its own pass or fused into the merge")

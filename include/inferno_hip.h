@@ -248,6 +248,20 @@ int32_t ifr_dispatch_gather_rows(const void* src, void* dst,
                                  const int32_t* rows, int64_t num_rows,
                                  int64_t cols, uint64_t stream);
 
+/* ---- o_proj (the step after the attention) ----------------------------------
+ * dispatch_gemm_cols[rows] (kernels/gemm.mojo:198-225; called at
+ * modeling/gemma_4_moe.mojo:387-392 and :485-490 with rows = HIDDEN):
+ * output[m][n] = bf16(sum_k x[m][k] * weight[n][k]) for bf16 x [seq_len][cols],
+ * weight [rows][cols], f32 accumulation.  rows % 16 == 0, cols % 128 == 0
+ * (the reference also takes a scalar tail of cols % 32; not provided).  Small
+ * seq_len splits the contraction over workgroups into f32 partials in
+ * `workspace` (ifr_gemm_cols_workspace_bytes; 0 means none is needed). */
+int64_t ifr_gemm_cols_workspace_bytes(int64_t rows, int64_t cols, int64_t seq_len);
+int32_t ifr_dispatch_gemm_cols(const void* x, const void* weight, void* output,
+                               int64_t rows, int64_t cols, int64_t seq_len,
+                               void* workspace, int64_t workspace_bytes,
+                               uint64_t stream);
+
 /* ---- butterquant int8 KV ----------------------------------------------------
  * dispatch_bq_attn_prep (butterquant_kernels/attention.mojo:585-632): RMS
  * norm, gain, RoPE, FWHT over head_dim and absmax int8 for q and k, FWHT and

@@ -224,6 +224,26 @@ def bq_attention(plan: AttentionPlan, q_i8, qi_bias, f_q, k_base, k_scale, v_bas
         check(lib().ifr_bq_attention_block_quant(*args, _ptr(o_i8), _ptr(o_sa), _stream()))
 
 
+def gemm_cols_workspace(rows: int, cols: int, seq_len: int, device="cuda"):
+    """f32 workspace for dispatch_gemm_cols at this shape (None if unneeded)."""
+    import torch
+
+    n = lib().ifr_gemm_cols_workspace_bytes(rows, cols, seq_len)
+    if n < 0:
+        raise ValueError("bad gemm_cols shape")
+    return torch.empty(max(n // 4, 1), dtype=torch.float32, device=device) if n else None
+
+
+def dispatch_gemm_cols(x, weight, output, *, rows: int, cols: int, seq_len: int,
+                       workspace=None) -> None:
+    """dispatch_gemm_cols[rows] (kernels/gemm.mojo:198-225): the o_proj after the
+    attention, output[m][n] = bf16(sum_k x[m][k] * weight[n][k])."""
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib().ifr_dispatch_gemm_cols(_ptr(x), _ptr(weight), _ptr(output), rows, cols,
+                                       seq_len, _ptr(workspace) if workspace is not None
+                                       else None, ws_bytes, _stream()))
+
+
 def dispatch_bq_block_quant(src, x_i8, x_sa, *, cols: int, block: int, seq_len: int) -> None:
     """dispatch_bq_block_quant[apply_fwht=False] (butterquant_kernels/linear.mojo:
     182-206): per-block absmax int8 of seq_len bf16 rows."""
@@ -237,4 +257,5 @@ __all__ = [
     "merge_flash_partials", "dispatch_sliding_attention",
     "dispatch_full_attention", "dispatch_copy_jobs", "dispatch_gather_rows",
     "dispatch_bq_attn_prep", "bq_attention", "dispatch_bq_block_quant",
+    "gemm_cols_workspace", "dispatch_gemm_cols",
 ]

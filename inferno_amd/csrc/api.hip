@@ -1004,6 +1004,33 @@ int32_t ifr_bq_attention_block_quant(const void* image_dev, const int64_t* info,
                       partial_stride, kv_stride, page_len, page_mask, stream, o_i8, o_sa);
 }
 
+int64_t ifr_gemm_cols_workspace_bytes(int64_t rows, int64_t cols, int64_t seq_len) {
+  if (rows <= 0 || cols <= 0 || seq_len < 0) return -1;
+  return ifr::gemm_cols_workspace_bytes(seq_len, rows, cols);
+}
+
+int32_t ifr_dispatch_gemm_cols(const void* x, const void* weight, void* output, int64_t rows,
+                               int64_t cols, int64_t seq_len, void* workspace,
+                               int64_t workspace_bytes, uint64_t stream) {
+  if (rows <= 0 || rows % 16 != 0 || rows > (int64_t{1} << 24))
+    return fail(IFR_EINVAL, "rows must be a positive multiple of 16");
+  if (cols <= 0 || cols % 128 != 0 || cols > (int64_t{1} << 24))
+    return fail(IFR_EINVAL, "cols must be a positive multiple of 128");
+  if (seq_len < 0 || seq_len > (int64_t{1} << 21))
+    return fail(IFR_EINVAL, "seq_len must be in [0, 2^21]");
+  if (seq_len == 0) return ok();
+  if (!x || !weight || !output) return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(output, 16))
+    return fail(IFR_EINVAL, "x, weight and output must be 16-byte aligned");
+  const int64_t need = ifr::gemm_cols_workspace_bytes(seq_len, rows, cols);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
+    return fail(IFR_ESPACE, "workspace needs %lld bytes, 16-byte aligned", (long long)need);
+  IFR_HIP(ifr::launch_gemm_cols(x, weight, output, static_cast<float*>(workspace), seq_len,
+                                rows, cols, as_stream(stream)),
+          "gemm_cols");
+  return ok();
+}
+
 int32_t ifr_bq_block_quant(const void* src, void* x_i8, float* x_sa, int64_t cols,
                            int64_t block, int64_t seq_len, uint64_t stream) {
   if (seq_len < 0) return fail(IFR_EINVAL, "seq_len must be >= 0");

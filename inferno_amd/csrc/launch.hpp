@@ -54,6 +54,13 @@ hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
 hipError_t launch_bq_block_quant(const void* src, void* x_i8, float* x_sa, int64_t cols,
                                  int block, int64_t seq_len, hipStream_t stream);
 
+// dispatch_gemm_cols: out[m][n] = bf16(sum_k x[m][k] * w[n][k]); N % 16 == 0,
+// K % 128 == 0.  k splits (and with them the workspace) depend on the shape.
+int gemm_cols_splits(int64_t M, int64_t N, int64_t K);
+int64_t gemm_cols_workspace_bytes(int64_t M, int64_t N, int64_t K);
+hipError_t launch_gemm_cols(const void* x, const void* w, void* out, float* workspace,
+                            int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
 // num_stripes: partial stripes of the plan (one per split).  q_out / q_scale
 // (optional): per-head absmax int8 of the merged outputs, fused.
 hipError_t launch_merge(const int32_t* image_dev, int num_units, int num_stripes, int mode,

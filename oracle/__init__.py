@@ -48,6 +48,7 @@ _SIG = {
     "ifo_head_inv_rms": (F32, [VP, I64, F32, F32]),
     "ifo_absmax_quantize": (F32, [VP, I64, VP, VP]),
     "ifo_bq_block_quant": (None, [VP, VP, VP, I64, I64, I64]),
+    "ifo_gemm_cols": (None, [VP, VP, VP, I64, I64, I64]),
     "ifo_bq_attn_prep": (None, [VP, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP,
                                 VP, VP, VP, I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                 I64, I64, F32, F32]),
@@ -199,6 +200,15 @@ def absmax_quantize(x) -> tuple[np.ndarray, float, int]:
     qs = np.zeros(1, dtype=np.int32)
     amax = lib().ifo_absmax_quantize(_p(x), x.size, _p(q), _p(qs))
     return q, float(amax), int(qs[0])
+
+
+def gemm_cols(x, w, *, rows: int, cols: int) -> np.ndarray:
+    """o_proj: bf16 [seq][rows] = x [seq][cols] . w [rows][cols]^T (bf16 bits)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16).reshape(-1, cols)
+    w = np.ascontiguousarray(w, dtype=np.uint16).reshape(rows, cols)
+    out = np.zeros((x.shape[0], rows), dtype=np.uint16)
+    lib().ifo_gemm_cols(_p(x), _p(w), _p(out), rows, cols, x.shape[0])
+    return out
 
 
 def bq_block_quant(src, cols: int, block: int) -> tuple[np.ndarray, np.ndarray]:

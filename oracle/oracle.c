@@ -37,6 +37,10 @@
  *   ifo_rms_norm_qkv_heads closed forms on constant rows, exact power-of-two
  *                       scale invariance, unit RMS of the output, gains on q
  *                       and k only, float64 RMS norm to one bf16 rounding.
+ *   ifo_gemm_cols       integer-valued operands (exact sums, so the bf16
+ *                       result is the rounded integer matmul), the identity
+ *                       weight, and float64 matmul within one bf16 rounding
+ *                       on random operands, with and without a k tail.
  *   ifo_bq_block_quant  known answers with exact scales (amax 127 and 254 give
  *                       inv 1 and 0.5, so ties land on .5 and must go to
  *                       even), the all-zero block (codes 0, scale 0), the
@@ -977,6 +981,31 @@ float ifo_absmax_quantize(const float* x, int64_t n, int8_t* out,
     return amax;
 }
 
+/* dispatch_gemm_cols[rows] (kernels/gemm.mojo:198-225): GemmColKernel over
+ * bf16_microtile_runtime (kernels/panel.mojo:85-133).  Each (token, column)
+ * has one W-lane f32 accumulator fed by VDPBF16PS over 32-element chunks of
+ * the contraction (bf16_pair_dot, kernels/dot_products.mojo:10-35), lanes
+ * reduced by the halving tree, then a scalar tail over cols % 32 added, and
+ * the f32 sum cast to bf16 (emit_gemm_col_panel, gemm.mojo:122-150). */
+void ifo_gemm_cols(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                   int64_t rows, int64_t cols, int64_t seq_len) {
+    int64_t body = cols - cols % (2 * W);
+    for (int64_t m = 0; m < seq_len; m++) {
+        const uint16_t* xr = x + m * cols;
+        for (int64_t n = 0; n < rows; n++) {
+            const uint16_t* wr = w + n * cols;
+            float v = bf16_dot_vdpbf16(wr, xr, body, 1);
+            if (body < cols) {
+                float tail = 0.0f;
+                for (int64_t k = body; k < cols; k++)
+                    tail = tail + ifo_bf16_to_f32(xr[k]) * ifo_bf16_to_f32(wr[k]);
+                v = v + tail;
+            }
+            out[m * rows + n] = ifo_f32_to_bf16(v);
+        }
+    }
+}
+
 /* dispatch_bq_block_quant[apply_fwht=False] (butterquant_kernels/linear.mojo:
  * 151-206): per token, prepare_block_activation (butterquant/runtime.mojo:
  * 63-80) widens the bf16 row to f32 and quantize_activation_per_block
@@ -1013,7 +1042,7 @@ static float prep_head_qk(const uint16_t* src, const uint16_t* gamma,
                           int8_t* out, int32_t* qsum, int64_t D,
                           int64_t rope_half, int64_t pair_stride,
                           float sqrt_n, float n_eps) {
-    float r[512];
+    float r[512] = {0};
     for (int64_t i = 0; i < D; i++) r[i] = ifo_bf16_to_f32(src[i]);
     float inv_rms = ifo_head_inv_rms(r, D, sqrt_n, n_eps);
     for (int64_t i = 0; i < D; i++) {

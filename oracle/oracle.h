@@ -103,6 +103,9 @@ void ifo_copy_jobs(uint8_t* arena, const int64_t* jobs /* [n][3] */,
 void ifo_gather_rows(const uint16_t* src, uint16_t* dst, const int32_t* rows,
                      int64_t num_rows, int64_t cols);
 
+void ifo_gemm_cols(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                   int64_t rows, int64_t cols, int64_t seq_len);
+
 /* ---- butterquant int8 KV ------------------------------------------------ */
 void  ifo_fwht(float* v, int64_t n);
 float ifo_head_inv_rms(const float* x, int64_t n, float sqrt_n, float n_eps);
