@@ -49,6 +49,13 @@ _SIG = {
     "ifo_absmax_quantize": (F32, [VP, I64, VP, VP]),
     "ifo_bq_block_quant": (None, [VP, VP, VP, I64, I64, I64]),
     "ifo_gemm_cols": (None, [VP, VP, VP, I64, I64, I64]),
+    "ifo_index_block_scores": (None, [VP, I64, VP, VP, VP, VP, I64, I64, I64, I64, F32, I64,
+                                      I64]),
+    "ifo_select_blocks": (None, [VP, I64, I64, I64, I64, VP]),
+    "ifo_lightning_indexer": (None, [VP, I64, VP, VP, VP, VP, VP, I64, I64, I64, I64, I64,
+                                     I64, I64, F32, I64, I64]),
+    "ifo_block_sparse_attention": (C.c_int, [VP, I64, VP, VP, VP, VP, VP, VP, I64, I64, I64,
+                                             I64, I64, I64, I64, I64]),
     "ifo_bq_attn_prep": (None, [VP, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP,
                                 VP, VP, VP, I64, I64, I64, I64, I64, I64, I64, I64, I64,
                                 I64, I64, F32, F32]),
@@ -200,6 +207,66 @@ def absmax_quantize(x) -> tuple[np.ndarray, float, int]:
     qs = np.zeros(1, dtype=np.int32)
     amax = lib().ifo_absmax_quantize(_p(x), x.size, _p(q), _p(qs))
     return q, float(amax), int(qs[0])
+
+
+def index_block_stride(runs, seq_len: int, block_size: int) -> int:
+    """Blocks per (token, head) score row: the largest position's block count,
+    rounded up to 16 (lightning_indexer.mojo:424-426 for one run)."""
+    runs = np.asarray(runs, dtype=np.int64).reshape(-1, 4)
+    last = 0
+    for i, r in enumerate(runs):
+        end = runs[i + 1][0] if i + 1 < len(runs) else seq_len
+        last = max(last, int(r[1]) + int(end - r[0]) - 1)
+    return (last // block_size + 1 + 15) // 16 * 16
+
+
+def index_block_scores(runs, base_rows, index_q, index_k, *, num_heads, head_dim,
+                       block_size, scale, page_len, seq_len) -> np.ndarray:
+    runs = np.ascontiguousarray(runs, dtype=np.int32)
+    rows = np.ascontiguousarray(base_rows, dtype=np.int32)
+    bs = index_block_stride(runs, seq_len, block_size)
+    scores = np.full(seq_len * num_heads * bs, np.nan, dtype=np.float32)
+    lib().ifo_index_block_scores(_p(runs), runs.shape[0], _p(rows), _p(index_q), _p(index_k),
+                                 _p(scores), bs, num_heads, head_dim, block_size,
+                                 np.float32(scale), page_len, seq_len)
+    return scores.reshape(seq_len, num_heads, bs)
+
+
+def select_blocks(row_scores, num_blocks: int, *, topk: int, local_blocks: int,
+                  init_blocks: int) -> np.ndarray:
+    row = np.ascontiguousarray(row_scores, dtype=np.float32)
+    out = np.zeros(topk, dtype=np.int32)
+    lib().ifo_select_blocks(_p(row), num_blocks, topk, local_blocks, init_blocks, _p(out))
+    return out
+
+
+def lightning_indexer(runs, base_rows, index_q, index_k, *, num_heads, head_dim, block_size,
+                      topk, local_blocks, init_blocks, scale, page_len, seq_len):
+    """Returns (block_idx [seq][heads][topk] int32, scores [seq][heads][stride])."""
+    runs = np.ascontiguousarray(runs, dtype=np.int32)
+    rows = np.ascontiguousarray(base_rows, dtype=np.int32)
+    bs = index_block_stride(runs, seq_len, block_size)
+    scores = np.full(seq_len * num_heads * bs, np.nan, dtype=np.float32)
+    idx = np.full(seq_len * num_heads * topk, -2, dtype=np.int32)
+    lib().ifo_lightning_indexer(_p(runs), runs.shape[0], _p(rows), _p(index_q), _p(index_k),
+                                _p(idx), _p(scores), bs, num_heads, head_dim, block_size, topk,
+                                local_blocks, init_blocks, np.float32(scale), page_len,
+                                seq_len)
+    return idx.reshape(seq_len, num_heads, topk), scores.reshape(seq_len, num_heads, bs)
+
+
+def block_sparse_attention(runs, base_rows, q, k, v, block_idx, *, num_q, num_kv, head_dim,
+                           kv_stride, block_size, topk, page_len, seq_len) -> np.ndarray:
+    runs = np.ascontiguousarray(runs, dtype=np.int32)
+    rows = np.ascontiguousarray(base_rows, dtype=np.int32)
+    bi = np.ascontiguousarray(block_idx, dtype=np.int32)
+    out = np.zeros(seq_len * num_q * head_dim, dtype=np.uint16)
+    st = lib().ifo_block_sparse_attention(_p(runs), runs.shape[0], _p(rows), _p(q), _p(k),
+                                          _p(v), _p(bi), _p(out), num_q, num_kv, head_dim,
+                                          kv_stride, block_size, topk, page_len, seq_len)
+    if st != 0:
+        raise ValueError(f"oracle sparse attention rejected the arguments ({st})")
+    return out
 
 
 def gemm_cols(x, w, *, rows: int, cols: int) -> np.ndarray:

@@ -388,8 +388,8 @@ static void process_tile(const attn_ctx* c, const attn_item* it,
     int64_t pu = reuse_panel_pu(D, c->gqa);
     const float inv127 = 1.0f / 127.0f;
     const float inv127sq = inv127 * inv127;
-    float scores[TILE * 8];
-    float weights[TILE * 8];
+    float scores[TILE * 64];   /* gqa <= 64 */
+    float weights[TILE * 64];
     for (int64_t g = 0; g < groups; g++) {
         int64_t base_q = g * c->gqa;
         int64_t head_off = g * D;
@@ -439,7 +439,7 @@ static void process_tile(const attn_ctx* c, const attn_item* it,
             } else {
                 const int8_t* v_head = c->vi + slots[t] * c->kv_stride + head_off;
                 float vs = c->v_scale[slots[t] * c->num_kv + g];
-                float wts[8];
+                float wts[64];
                 for (int64_t r = 0; r < c->gqa; r++) {
                     float w = weights[t * c->gqa + r] * vs;
                     wts[r] = w * inv127;
@@ -806,6 +806,244 @@ int ifo_bq_attention(int64_t kind, const int32_t* runs, int64_t num_runs,
     c.v_scale = v_scale;
     return run_dispatch(&c, kind, runs, num_runs, base_rows, out, window,
                         seq_len, cap, threads, 1);
+}
+
+/* ------------------------------------------------------------------------ */
+/* MiniMax-M3 block-sparse attention (prototypes/, degree 1)                 */
+/* ------------------------------------------------------------------------ */
+
+/* The run a token belongs to, advancing `ri` as the reference's kernels do
+ * (prototypes/lightning_indexer.mojo:158-163); returns the absolute position. */
+static int64_t token_position(const int32_t* runs, int64_t num_runs, int64_t t,
+                              int64_t* ri) {
+    while (*ri + 1 < num_runs && t >= runs[4 * (*ri + 1)]) (*ri)++;
+    return (int64_t)runs[4 * *ri + 1] + (t - runs[4 * *ri]);
+}
+
+/* IndexBlockScoreKernel.execute (prototypes/lightning_indexer.mojo:134-202):
+ * per token, each causal position's index key is scored against every index
+ * head's query (bf16_panel_dot_to_scalars, port unroll
+ * pick_port_unroll(32, head_dim)), scaled, and max-folded (strict >) into its
+ * block's cell, which starts at -1e30.  Rows are [token][head][block_stride]. */
+void ifo_index_block_scores(const int32_t* runs, int64_t num_runs,
+                            const int32_t* base_rows, const uint16_t* index_q,
+                            const uint16_t* index_k, float* scores,
+                            int64_t block_stride, int64_t num_heads,
+                            int64_t head_dim, int64_t block_size, float scale,
+                            int64_t page_len, int64_t seq_len) {
+    int64_t shift = ifo_pow2_shift(page_len), row_mask = page_len - 1;
+    int64_t pu = pick_port_unroll(2 * W, head_dim);
+    int64_t ri = 0;
+    for (int64_t t = 0; t < seq_len; t++) {
+        int64_t abs_pos = token_position(runs, num_runs, t, &ri);
+        if (abs_pos < 0) continue;
+        int64_t nb = abs_pos / block_size + 1;
+        float* tok = scores + t * num_heads * block_stride;
+        for (int64_t h = 0; h < num_heads; h++)
+            for (int64_t b = 0; b < nb; b++) tok[h * block_stride + b] = NEG_BIG;
+        const int32_t* rows = base_rows + runs[4 * ri + 2];
+        for (int64_t pos = 0; pos <= abs_pos; pos++) {
+            int64_t slot = ifo_paged_slot(rows, shift, row_mask, -1, 0, pos);
+            const uint16_t* kr = index_k + slot * head_dim;
+            int64_t b = pos / block_size;
+            for (int64_t h = 0; h < num_heads; h++) {
+                float d = bf16_dot_vdpbf16(kr, index_q + (t * num_heads + h) * head_dim,
+                                           head_dim, pu);
+                float sh = d * scale;
+                float* cell = tok + h * block_stride + b;
+                if (sh > *cell) *cell = sh;
+            }
+        }
+    }
+}
+
+/* reduce_argmax's winner (simd_math/matrixops.mojo:125-166) over a bank of
+ * `cap` slots in cap/16 registers of 16 lanes: the across-register tree keeps
+ * the lower register on ties, the in-lane butterfly the lower lane, so ties
+ * go to the smaller lane (slot % 16), then the smaller register. */
+static int64_t bank_argmax(const float* v, int64_t cap) {
+    int64_t best = 0;
+    for (int64_t s = 1; s < cap; s++) {
+        if (v[s] > v[best]) {
+            best = s;
+        } else if (v[s] == v[best]) {
+            int64_t ls = s % W, lb = best % W;
+            if (ls < lb || (ls == lb && s / W < best / W)) best = s;
+        }
+    }
+    return best;
+}
+
+/* reduce_top_k (matrixops.mojo:170-218): k argmax passes, each winner masked
+ * to the sentinel in a copy of the bank. */
+static void bank_top_k(const float* bank_v, const int32_t* bank_b, int64_t cap,
+                       int64_t k, int32_t* keep_b, float* keep_v) {
+    float work[256];
+    for (int64_t s = 0; s < cap; s++) work[s] = bank_v[s];
+    for (int64_t sel = 0; sel < k; sel++) {
+        int64_t w = bank_argmax(work, cap);
+        keep_v[sel] = work[w];
+        keep_b[sel] = bank_b[w];
+        work[w] = NEG_BIG;
+    }
+}
+
+/* stream_select_blocks (prototypes/lightning_indexer.mojo:48-126) over one
+ * row of block scores: blocks enter a bank of bank_cap(topk, 16) slots in
+ * order (the last local_blocks and first init_blocks forced to 1e30); a full
+ * bank keeps its top topk, in selection order, and refills from slot topk;
+ * the final top topk with a score above -1e30 are written sorted ascending,
+ * -1 padded. */
+void ifo_select_blocks(const float* row_scores, int64_t num_blocks, int64_t topk,
+                       int64_t local_blocks, int64_t init_blocks, int32_t* out_row) {
+    int64_t cap = 1;
+    while (cap < 2 * topk) cap <<= 1;
+    if (cap < W) cap = W;
+    float bank_v[256];
+    int32_t bank_b[256], keep_b[128], ids[128];
+    float keep_v[128];
+    for (int64_t s = 0; s < cap; s++) {
+        bank_v[s] = NEG_BIG;
+        bank_b[s] = -1;
+    }
+    int64_t local_start = num_blocks - local_blocks;
+    if (local_start < 0) local_start = 0;
+    int64_t fill = 0;
+    for (int64_t b = 0; b < num_blocks; b++) {
+        float score = (b >= local_start || b < init_blocks) ? 1.0e30f : row_scores[b];
+        bank_v[fill] = score;
+        bank_b[fill] = (int32_t)b;
+        fill++;
+        if (fill == cap) {
+            bank_top_k(bank_v, bank_b, cap, topk, keep_b, keep_v);
+            for (int64_t s = 0; s < cap; s++) {
+                bank_v[s] = NEG_BIG;
+                bank_b[s] = -1;
+            }
+            for (int64_t s = 0; s < topk; s++) {
+                bank_v[s] = keep_v[s];
+                bank_b[s] = keep_b[s];
+            }
+            fill = topk;
+        }
+    }
+    bank_top_k(bank_v, bank_b, cap, topk, keep_b, keep_v);
+    int64_t n = 0;
+    for (int64_t s = 0; s < topk; s++) ids[s] = -1;
+    for (int64_t s = 0; s < topk; s++)
+        if (keep_v[s] > NEG_BIG) ids[n++] = keep_b[s];
+    for (int64_t i = 1; i < n; i++) {
+        int32_t v = ids[i];
+        int64_t j = i - 1;
+        while (j >= 0 && ids[j] > v) {
+            ids[j + 1] = ids[j];
+            j--;
+        }
+        ids[j + 1] = v;
+    }
+    for (int64_t s = 0; s < topk; s++) out_row[s] = ids[s];
+}
+
+/* dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-441) at
+ * degree 1: block scores, then IndexTopkMergeKernel (:222-262) per (token,
+ * head) row.  The reference's merge takes every token's position from the
+ * first run (base_pos + t, :244, a one-sequence prototype); here each token's
+ * own run gives it, which is the same for one run. */
+void ifo_lightning_indexer(const int32_t* runs, int64_t num_runs,
+                           const int32_t* base_rows, const uint16_t* index_q,
+                           const uint16_t* index_k, int32_t* block_idx,
+                           float* scores, int64_t block_stride, int64_t num_heads,
+                           int64_t head_dim, int64_t block_size, int64_t topk,
+                           int64_t local_blocks, int64_t init_blocks, float scale,
+                           int64_t page_len, int64_t seq_len) {
+    ifo_index_block_scores(runs, num_runs, base_rows, index_q, index_k, scores,
+                           block_stride, num_heads, head_dim, block_size, scale,
+                           page_len, seq_len);
+    int64_t ri = 0;
+    for (int64_t t = 0; t < seq_len; t++) {
+        int64_t abs_pos = token_position(runs, num_runs, t, &ri);
+        if (abs_pos < 0) continue;
+        int64_t nb = abs_pos / block_size + 1;
+        for (int64_t h = 0; h < num_heads; h++)
+            ifo_select_blocks(scores + (t * num_heads + h) * block_stride, nb, topk,
+                              local_blocks, init_blocks,
+                              block_idx + (t * num_heads + h) * topk);
+    }
+}
+
+/* BlockSparseFlashKernel.execute (prototypes/sparse_attention.mojo:58-125) at
+ * degree 1: per token and kv head, the selected blocks in order (stopping at
+ * the first -1), each clipped to the causal count and walked in 16-position
+ * process_kv_tile steps from its first position over the head's gqa q heads;
+ * then PrefillMergeKernel (kernels/flash_attention_prefill.mojo:221-240):
+ * write_finalized_head over the token's one stripe. */
+int ifo_block_sparse_attention(const int32_t* runs, int64_t num_runs,
+                               const int32_t* base_rows, const uint16_t* q,
+                               const uint16_t* k_base, const uint16_t* v_base,
+                               const int32_t* block_idx, uint16_t* out,
+                               int64_t num_q, int64_t num_kv, int64_t head_dim,
+                               int64_t kv_stride, int64_t block_size, int64_t topk,
+                               int64_t page_len, int64_t seq_len) {
+    if (num_q <= 0 || num_kv <= 0 || num_q % num_kv != 0 || num_q > 64) return -1;
+    if (head_dim % (2 * W) != 0 || head_dim > 512) return -1;
+    if (page_len <= 0 || (page_len & (page_len - 1)) != 0) return -1;
+    int64_t D = head_dim, gqa = num_q / num_kv;
+    int64_t stride = ifo_flash_partial_stride(num_q, D);
+    float* part = (float*)calloc((size_t)stride, sizeof(float));
+    float* acc = (float*)malloc(sizeof(float) * (size_t)(gqa * D));
+    attn_ctx c;
+    memset(&c, 0, sizeof(c));
+    c.num_q = gqa;
+    c.num_kv = 1;
+    c.gqa = gqa;
+    c.head_dim = D;
+    c.kv_stride = kv_stride;
+    c.shift = ifo_pow2_shift(page_len);
+    c.row_mask = page_len - 1;
+    c.page_mask = -1;
+    c.q = q;
+    int64_t ri = 0;
+    for (int64_t t = 0; t < seq_len; t++) {
+        int64_t abs_pos = token_position(runs, num_runs, t, &ri);
+        if (abs_pos < 0) continue;
+        int64_t cap = abs_pos + 1;   /* full_local_kv_count(0, abs_pos, 1) */
+        attn_item it = {t, base_rows + runs[4 * ri + 2], 0, 0, 0, 0};
+        for (int64_t h = 0; h < num_kv; h++) {
+            float m[64], l[64];
+            int64_t q_off[64];
+            for (int64_t r = 0; r < gqa; r++) {
+                m[r] = NEG_BIG;
+                l[r] = 0.0f;
+                q_off[r] = (t * num_q + h * gqa + r) * D;
+            }
+            memset(acc, 0, sizeof(float) * (size_t)(gqa * D));
+            c.k = k_base + h * D;
+            c.v = v_base + h * D;
+            const int32_t* row = block_idx + (t * num_kv + h) * topk;
+            for (int64_t s = 0; s < topk; s++) {
+                int64_t b = row[s];
+                if (b < 0) break;
+                int64_t plo = b * block_size;
+                int64_t phi = (b + 1) * block_size;
+                if (phi > cap) phi = cap;
+                for (int64_t pos = plo; pos < phi; pos += TILE) {
+                    int64_t tl = phi - pos < TILE ? phi - pos : TILE;
+                    process_tile(&c, &it, q_off, pos, tl, m, l, acc);
+                }
+            }
+            for (int64_t r = 0; r < gqa; r++) {
+                int64_t qh = h * gqa + r;
+                memcpy(part + qh * D, acc + r * D, sizeof(float) * (size_t)D);
+                part[num_q * D + qh] = m[r];
+                part[num_q * D + num_q + qh] = l[r];
+            }
+        }
+        for (int64_t qh = 0; qh < num_q; qh++)
+            ifo_finalize_head(out + (t * num_q + qh) * D, part, stride, 1, num_q, D, qh);
+    }
+    free(part);
+    free(acc);
+    return 0;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -103,6 +103,30 @@ void ifo_copy_jobs(uint8_t* arena, const int64_t* jobs /* [n][3] */,
 void ifo_gather_rows(const uint16_t* src, uint16_t* dst, const int32_t* rows,
                      int64_t num_rows, int64_t cols);
 
+/* ---- MiniMax-M3 block-sparse attention (degree 1) ---------------------- */
+void ifo_index_block_scores(const int32_t* runs, int64_t num_runs,
+                            const int32_t* base_rows, const uint16_t* index_q,
+                            const uint16_t* index_k, float* scores,
+                            int64_t block_stride, int64_t num_heads,
+                            int64_t head_dim, int64_t block_size, float scale,
+                            int64_t page_len, int64_t seq_len);
+void ifo_select_blocks(const float* row_scores, int64_t num_blocks, int64_t topk,
+                       int64_t local_blocks, int64_t init_blocks, int32_t* out_row);
+void ifo_lightning_indexer(const int32_t* runs, int64_t num_runs,
+                           const int32_t* base_rows, const uint16_t* index_q,
+                           const uint16_t* index_k, int32_t* block_idx,
+                           float* scores, int64_t block_stride, int64_t num_heads,
+                           int64_t head_dim, int64_t block_size, int64_t topk,
+                           int64_t local_blocks, int64_t init_blocks, float scale,
+                           int64_t page_len, int64_t seq_len);
+int ifo_block_sparse_attention(const int32_t* runs, int64_t num_runs,
+                               const int32_t* base_rows, const uint16_t* q,
+                               const uint16_t* k_base, const uint16_t* v_base,
+                               const int32_t* block_idx, uint16_t* out,
+                               int64_t num_q, int64_t num_kv, int64_t head_dim,
+                               int64_t kv_stride, int64_t block_size, int64_t topk,
+                               int64_t page_len, int64_t seq_len);
+
 void ifo_gemm_cols(const uint16_t* x, const uint16_t* w, uint16_t* out,
                    int64_t rows, int64_t cols, int64_t seq_len);
 
