@@ -115,7 +115,7 @@ int64_t ifr_plan_bytes(int64_t num_runs, int64_t num_rows, int64_t seq_len,
  *   info[6] = num_runs                    info[7] = page shift
  *   info[8] = row mask                    info[9] = page mask (-1 = full)
  *   info[10] = cache_rows                 info[11] = kind
- *   info[12] = window                     info[13] = 0
+ *   info[12] = window                     info[13] = highest token position
  *   info[14] = MFMA prefill query blocks (token plans of full attention)
  *   info[15] = 0
  * Every launch entry point below takes the same info and refuses a page
@@ -247,6 +247,41 @@ int32_t ifr_dispatch_copy_jobs(void* arena, const int64_t* jobs,
 int32_t ifr_dispatch_gather_rows(const void* src, void* dst,
                                  const int32_t* rows, int64_t num_rows,
                                  int64_t cols, uint64_t stream);
+
+/* ---- MiniMax-M3 block-sparse attention (prototypes/, degree 1) -------------
+ * Both calls read a full-attention plan image of the step (kind 1,
+ * ifr_plan_attention): its run table, page table and token->run map.
+ *
+ * dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-441):
+ * block scores (IndexBlockScoreKernel :129-219: per token and index head, the
+ * max over each block's causal positions of scale * dot(index_q, index_k)),
+ * then top-k block selection (IndexTopkMergeKernel :222-262 over
+ * stream_select_blocks :48-126).  index_q [seq][4][128] bf16, index_k
+ * [rows][128] bf16 paged like the plan, block_idx [seq][4][topk] int32
+ * ascending with -1 padding, scores scratch of ifr_index_scores_bytes.
+ * The reference's top-k pass takes positions from the first run only
+ * (:244, a one-sequence prototype); here each token's run gives its
+ * position, which is the same for one run. */
+int64_t ifr_index_scores_bytes(const int64_t* info, int64_t num_index_heads,
+                               int64_t block_size);
+int32_t ifr_lightning_indexer(const void* image_dev, const int64_t* info,
+                              const void* index_q, const void* index_k,
+                              int32_t* block_idx, float* scores, int64_t scores_bytes,
+                              int64_t num_index_heads, int64_t index_head_dim,
+                              int64_t block_size, int64_t topk_blocks,
+                              int64_t local_blocks, int64_t init_blocks, float scale,
+                              int64_t page_len, uint64_t stream);
+/* dispatch_block_sparse_attention (prototypes/sparse_attention.mojo:164-199):
+ * BlockSparseFlashKernel (:41-125) over each (token, kv head)'s block list in
+ * order, then the one-stripe PrefillMergeKernel finalisation
+ * (kernels/flash_attention_prefill.mojo:208-248).  head_dim 128, 16 q heads
+ * per kv head; output [seq][num_q][128] bf16. */
+int32_t ifr_block_sparse_attention(const void* image_dev, const int64_t* info,
+                                   const void* q, const void* k_base, const void* v_base,
+                                   const int32_t* block_idx, void* output, int64_t num_q,
+                                   int64_t num_kv, int64_t head_dim, int64_t kv_stride,
+                                   int64_t block_size, int64_t topk_blocks,
+                                   int64_t page_len, uint64_t stream);
 
 /* ---- o_proj (the step after the attention) ----------------------------------
  * dispatch_gemm_cols[rows] (kernels/gemm.mojo:198-225; called at

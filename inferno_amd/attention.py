@@ -224,6 +224,46 @@ def bq_attention(plan: AttentionPlan, q_i8, qi_bias, f_q, k_base, k_scale, v_bas
         check(lib().ifr_bq_attention_block_quant(*args, _ptr(o_i8), _ptr(o_sa), _stream()))
 
 
+def index_scores_buffer(plan: AttentionPlan, num_index_heads: int, block_size: int,
+                        device="cuda"):
+    """f32 scratch for the indexer's block scores at this plan."""
+    import torch
+
+    n = lib().ifr_index_scores_bytes(plan.info_ptr, num_index_heads, block_size)
+    if n < 0:
+        raise ValueError("bad indexer shape")
+    return torch.empty(max(n // 4, 1), dtype=torch.float32, device=device)
+
+
+def dispatch_lightning_indexer(plan: AttentionPlan, index_q, index_k, block_idx, scores, *,
+                               num_index_heads: int = 4, index_head_dim: int = 128,
+                               block_size: int = 128, topk_blocks: int = 16,
+                               local_blocks: int = 1, init_blocks: int = 0,
+                               scale: float | None = None) -> None:
+    """dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-441),
+    defaults of dispatch_minimax_m3_indexer (:456-477)."""
+    import numpy as np
+
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(index_head_dim)))
+    check(lib().ifr_lightning_indexer(
+        _ptr(plan.image), plan.info_ptr, _ptr(index_q), _ptr(index_k), _ptr(block_idx),
+        _ptr(scores), scores.numel() * 4, num_index_heads, index_head_dim, block_size,
+        topk_blocks, local_blocks, init_blocks, scale, plan.page_len, _stream()))
+
+
+def dispatch_block_sparse_attention(plan: AttentionPlan, q, k_base, v_base, block_idx, output, *,
+                                    num_q: int = 64, num_kv: int = 4, head_dim: int = 128,
+                                    kv_stride: int = 512, block_size: int = 128,
+                                    topk_blocks: int = 16) -> None:
+    """dispatch_block_sparse_attention (prototypes/sparse_attention.mojo:164-199),
+    defaults of dispatch_minimax_m3_sparse_attention (:211-234)."""
+    check(lib().ifr_block_sparse_attention(
+        _ptr(plan.image), plan.info_ptr, _ptr(q), _ptr(k_base), _ptr(v_base), _ptr(block_idx),
+        _ptr(output), num_q, num_kv, head_dim, kv_stride, block_size, topk_blocks,
+        plan.page_len, _stream()))
+
+
 def gemm_cols_workspace(rows: int, cols: int, seq_len: int, device="cuda"):
     """f32 workspace for dispatch_gemm_cols at this shape (None if unneeded)."""
     import torch
@@ -257,5 +297,6 @@ __all__ = [
     "merge_flash_partials", "dispatch_sliding_attention",
     "dispatch_full_attention", "dispatch_copy_jobs", "dispatch_gather_rows",
     "dispatch_bq_attn_prep", "bq_attention", "dispatch_bq_block_quant",
-    "gemm_cols_workspace", "dispatch_gemm_cols",
+    "gemm_cols_workspace", "dispatch_gemm_cols", "index_scores_buffer",
+    "dispatch_lightning_indexer", "dispatch_block_sparse_attention",
 ]

@@ -30,7 +30,7 @@ OBJ_DIR = PKG.parent / "_build" / "obj"
 ARCH = "gfx950"
 
 SOURCES = ["api.hip", "attention.hip", "append.hip", "copy.hip", "bq.hip", "prefill.hip",
-           "gemm.hip"]
+           "gemm.hip", "sparse.hip"]
 # Host-only C++ (page state, scheduler): built with the host compiler.
 HOST_SOURCES = ["host_state.cpp", "host_api.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}"]

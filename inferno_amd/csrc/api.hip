@@ -245,6 +245,11 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   if (need > INT32_MAX) return fail(IFR_EINVAL, "plan too large");
 
   const bool sliding = kind == 0;
+  int64_t max_pos = 0;  // highest token position of the step
+  for (int64_t i = 0; i < num_runs; ++i) {
+    const int64_t next = i + 1 < num_runs ? runs[4 * (i + 1)] : seq_len;
+    if (next > runs[4 * i]) max_pos = std::max<int64_t>(max_pos, runs[4 * i + 1] + next - 1 - runs[4 * i]);
+  }
   int32_t* hdr = img;
   memset(hdr, 0, sizeof(int32_t) * kHdrWords);
   int64_t off = kHdrWords;
@@ -401,7 +406,7 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   info[10] = cache_rows;
   info[11] = kind;
   info[12] = window;
-  info[13] = 0;
+  info[13] = max_pos;
   info[14] = n_qblocks;
   info[15] = 0;
   return ok();
@@ -1002,6 +1007,84 @@ int32_t ifr_bq_attention_block_quant(const void* image_dev, const int64_t* info,
   return bq_attention(image_dev, info, q_i8, qi_bias, f_q, k_base, k_scale, v_base, v_scale,
                       output, partials, partials_bytes, num_q, num_kv, head_dim,
                       partial_stride, kv_stride, page_len, page_mask, stream, o_i8, o_sa);
+}
+
+int64_t ifr_index_scores_bytes(const int64_t* info, int64_t num_index_heads,
+                               int64_t block_size) {
+  if (check_info(info) != IFR_OK || num_index_heads <= 0 || block_size <= 0) return -1;
+  return info[5] * num_index_heads * ifr::index_block_stride(info[13], block_size) * 4;
+}
+
+int32_t ifr_lightning_indexer(const void* image_dev, const int64_t* info, const void* index_q,
+                              const void* index_k, int32_t* block_idx, float* scores,
+                              int64_t scores_bytes, int64_t num_index_heads,
+                              int64_t index_head_dim, int64_t block_size, int64_t topk_blocks,
+                              int64_t local_blocks, int64_t init_blocks, float scale,
+                              int64_t page_len, uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (info[11] != 1) return fail(IFR_EINVAL, "the indexer needs a full-attention plan");
+  if (num_index_heads != 4 || index_head_dim != 128)
+    return fail(IFR_EUNSUPPORTED, "the indexer is compiled for 4 index heads of dim 128");
+  if (block_size <= 0 || block_size > (1 << 20))
+    return fail(IFR_EINVAL, "block_size must be in [1, 2^20]");
+  if (topk_blocks <= 0 || topk_blocks > 32) return fail(IFR_EINVAL, "topk_blocks must be in [1, 32]");
+  if (local_blocks < 0 || init_blocks < 0) return fail(IFR_EINVAL, "negative forced blocks");
+  if (!image_dev || !index_q || !index_k || !block_idx || !scores)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(index_q, 16) || !aligned(index_k, 16) || !aligned(block_idx, 4) ||
+      !aligned(scores, 4))
+    return fail(IFR_EINVAL, "index_q and index_k must be 16-byte aligned");
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
+  st = check_geometry(info, pow2_shift(page_len), page_len - 1, -1);
+  if (st) return st;
+  const int64_t stride = ifr::index_block_stride(info[13], block_size);
+  const int64_t need = info[5] * num_index_heads * stride * 4;
+  if (scores_bytes < need)
+    return fail(IFR_ESPACE, "scores need %lld bytes", (long long)need);
+  IFR_HIP(ifr::launch_lightning_indexer(
+              static_cast<const int32_t*>(image_dev), static_cast<int>(info[5]), index_q,
+              index_k, block_idx, scores, static_cast<int>(stride),
+              static_cast<int>(num_index_heads), static_cast<int>(index_head_dim),
+              static_cast<int>(block_size), static_cast<int>(topk_blocks),
+              static_cast<int>(local_blocks), static_cast<int>(init_blocks), scale,
+              static_cast<int>(info[7]), static_cast<int>(info[8]), as_stream(stream)),
+          "lightning_indexer");
+  return ok();
+}
+
+int32_t ifr_block_sparse_attention(const void* image_dev, const int64_t* info, const void* q,
+                                   const void* k_base, const void* v_base,
+                                   const int32_t* block_idx, void* output, int64_t num_q,
+                                   int64_t num_kv, int64_t head_dim, int64_t kv_stride,
+                                   int64_t block_size, int64_t topk_blocks, int64_t page_len,
+                                   uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (info[11] != 1) return fail(IFR_EINVAL, "sparse attention needs a full-attention plan");
+  if (head_dim != 128 || num_kv <= 0 || num_q != 16 * num_kv || num_q > 1024)
+    return fail(IFR_EUNSUPPORTED, "sparse attention is compiled for head_dim 128, gqa 16");
+  if (kv_stride < num_kv * head_dim || kv_stride % 8 != 0)
+    return fail(IFR_EINVAL, "kv_stride must cover num_kv heads and keep 16-byte rows");
+  if (block_size <= 0 || block_size > (1 << 20))
+    return fail(IFR_EINVAL, "block_size must be in [1, 2^20]");
+  if (topk_blocks <= 0 || topk_blocks > (1 << 16)) return fail(IFR_EINVAL, "bad topk_blocks");
+  if (!image_dev || !q || !k_base || !v_base || !block_idx || !output)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q, 16) || !aligned(k_base, 16) || !aligned(v_base, 16) || !aligned(output, 4) ||
+      !aligned(block_idx, 4))
+    return fail(IFR_EINVAL, "q, k and v must be 16-byte aligned");
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
+  st = check_geometry(info, pow2_shift(page_len), page_len - 1, -1);
+  if (st) return st;
+  IFR_HIP(ifr::launch_block_sparse_attention(
+              static_cast<const int32_t*>(image_dev), static_cast<int>(info[5]), q, k_base,
+              v_base, block_idx, output, kv_stride, static_cast<int>(num_q),
+              static_cast<int>(num_kv), static_cast<int>(block_size),
+              static_cast<int>(topk_blocks), static_cast<int>(info[7]),
+              static_cast<int>(info[8]), as_stream(stream)),
+          "block_sparse_attention");
+  return ok();
 }
 
 int64_t ifr_gemm_cols_workspace_bytes(int64_t rows, int64_t cols, int64_t seq_len) {

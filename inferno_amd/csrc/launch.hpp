@@ -61,6 +61,23 @@ int64_t gemm_cols_workspace_bytes(int64_t M, int64_t N, int64_t K);
 hipError_t launch_gemm_cols(const void* x, const void* w, void* out, float* workspace,
                             int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
+// MiniMax-M3 lightning indexer (block scores + top-k) and block-sparse
+// attention over a full-attention plan image.
+int index_block_stride(int64_t max_pos, int64_t block_size);
+int select_bank_cap(int topk);
+hipError_t launch_lightning_indexer(const int32_t* image, int seq_len, const void* index_q,
+                                    const void* index_k, int32_t* block_idx, float* scores,
+                                    int block_stride, int num_heads, int head_dim,
+                                    int block_size, int topk, int local_blocks,
+                                    int init_blocks, float scale, int shift, int row_mask,
+                                    hipStream_t stream);
+hipError_t launch_block_sparse_attention(const int32_t* image, int seq_len, const void* q,
+                                         const void* k_base, const void* v_base,
+                                         const int32_t* block_idx, void* output,
+                                         int64_t kv_stride, int num_q, int num_kv,
+                                         int block_size, int topk, int shift, int row_mask,
+                                         hipStream_t stream);
+
 // num_stripes: partial stripes of the plan (one per split).  q_out / q_scale
 // (optional): per-head absmax int8 of the merged outputs, fused.
 hipError_t launch_merge(const int32_t* image_dev, int num_units, int num_stripes, int mode,
