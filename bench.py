@@ -33,7 +33,7 @@ NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 HIDDEN = 2816  # Gemma 4 26B-A4B hidden size: o_proj maps 16 x 256 -> 2816
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
-DEFAULT_CAP = {1: 64, 2: 512, 3: 512, 4: 16, 5: 2048}
+DEFAULT_CAP = {1: 64, 2: 512, 3: 512, 4: 16, 5: 2048, 6: 0}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -382,6 +382,152 @@ class DecodeBq:
         return None
 
 
+class SparseM3:
+    """Config 6 (widening row, no BASELINE counterpart): MiniMax-M3 block-sparse
+    decode -- lightning indexer (block scores over every cached position + top-16
+    blocks per index head) then block-sparse attention over the selected blocks
+    (prototypes/benchmark_sparse_attention.mojo's decode sweep, batched)."""
+
+    dtype = "bf16 (indexer VDPBF16PS-order f32 dots; attention MFMA QK, f32 PV)"
+    phases = ("indexer", "sparse")
+    dominant = "index_scores_kernel + select_blocks_kernel"
+    dominant_phase = "indexer"
+    NQ, NKV, HD, IH, BLOCK, TOPK, PLEN = 64, 4, 128, 4, 128, 16, 128
+
+    def __init__(self, seed: int):
+        self.seed = seed
+        self.pos = uniform_ints(seed, 64, 1024, 131071)
+        self.name = ("config6: MiniMax-M3 block-sparse decode, B=64, ctx ~ U[1024,131072], "
+                     "lightning indexer (4 heads x 128, 128-position blocks, top 16) + sparse "
+                     "attention 64q/4kv hd128 bf16, 128-token pages")
+
+    def setup(self, dev, a):
+        import torch
+
+        from inferno_amd import attention as A
+        from inferno_amd.kv import AttentionPlan, KVRunTable
+
+        self.A = A
+        B, P = len(self.pos), self.PLEN
+        need = [(p + 1 + P - 1) // P for p in self.pos]
+        pool = sum(need)
+        perm = np.random.default_rng(self.seed).permutation(pool)
+        table = KVRunTable()
+        off = 0
+        self.pages = []
+        for i, p in enumerate(self.pos):
+            table.begin_run(i, p)
+            pg = [int(x) for x in perm[off:off + need[i]]]
+            self.pages.append(pg)
+            for x in pg:
+                table.add_base_row(x * P)
+            off += need[i]
+        rows = pool * P
+        self.pool, self.table, self.rows = pool, table, rows
+        self.stream = torch.cuda.current_stream()
+        sid = int(self.stream.cuda_stream)
+        kvs = self.NKV * self.HD
+        self.index_k = torch.empty(rows * self.HD, dtype=torch.int16, device=dev)
+        self.index_q = torch.empty(B * self.IH * self.HD, dtype=torch.int16, device=dev)
+        self.k = torch.empty(rows * kvs, dtype=torch.int16, device=dev)
+        self.v = torch.empty_like(self.k)
+        self.q = torch.empty(B * self.NQ * self.HD, dtype=torch.int16, device=dev)
+        _fill(self.index_k, self.seed * 16 + 1, sid)
+        _fill(self.index_q, self.seed * 16 + 2, sid)
+        _fill(self.k, self.seed * 16 + 3, sid)
+        _fill(self.v, self.seed * 16 + 4, sid)
+        _fill(self.q, self.seed * 16 + 5, sid, scale=float(1.0 / np.sqrt(self.HD)))
+        self.plan = AttentionPlan(table, B, kind=1, window=0, cache_size=P, page_len=P,
+                                  cache_rows=rows, cap=16, kv_row_bytes=kvs * 2, device=dev)
+        self.scores = A.index_scores_buffer(self.plan, self.IH, self.BLOCK, device=dev)
+        self.block_idx = torch.empty(B * self.IH * self.TOPK, dtype=torch.int32, device=dev)
+        self.out = torch.empty(B * self.NQ * self.HD, dtype=torch.int16, device=dev)
+        self.cap = 0
+
+    def launch(self, phase):
+        A, p = self.A, self.plan
+        if phase == "indexer":
+            A.dispatch_lightning_indexer(p, self.index_q, self.index_k, self.block_idx,
+                                         self.scores)
+        else:
+            A.dispatch_block_sparse_attention(p, self.q, self.k, self.v, self.block_idx,
+                                              self.out)
+
+    def dominant_bytes(self) -> int:
+        """Indexer: every cached position's index key, the queries, the score
+        rows written and read back, the page table."""
+        B = len(self.pos)
+        return (sum(p + 1 for p in self.pos) * self.HD * 2 + B * self.IH * self.HD * 2
+                + 2 * self.scores.numel() * 4 + 4 * len(self.table.base_rows))
+
+    def attended(self) -> int:
+        """Positions the sparse attention reads per kv head: the local block and
+        15 full blocks (every context here has more than 16 blocks)."""
+        return sum(min(self.TOPK - 1, p // self.BLOCK) * self.BLOCK + p % self.BLOCK + 1
+                   for p in self.pos)
+
+    def step_bytes(self) -> int:
+        B = len(self.pos)
+        attn = (self.attended() * self.NKV * self.HD * 2 * 2 + B * self.NQ * self.HD * 2 * 2
+                + B * self.IH * self.TOPK * 4)
+        return self.dominant_bytes() + attn
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": len(self.pos),
+                "indexed_positions": sum(p + 1 for p in self.pos),
+                "attended_positions_per_kv_head": self.attended(), "pool_pages": self.pool,
+                "page_len": self.PLEN, "num_q": self.NQ, "num_kv": self.NKV,
+                "head_dim": self.HD, "index_heads": self.IH, "block": self.BLOCK,
+                "topk_blocks": self.TOPK, "seed": self.seed}
+
+    def cpu_baseline(self, budget_s):
+        """The oracle's indexer + sparse attention on the first sequences of the
+        batch, one thread."""
+        import torch
+
+        import oracle
+
+        n_seq = 4
+        pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
+        idx = torch.from_numpy(pages.astype(np.int64)).to(self.k.device)
+        P, kvs = self.PLEN, self.NKV * self.HD
+        ik = self.index_k.view(-1, P * self.HD).index_select(0, idx).cpu().numpy()
+        kp = self.k.view(-1, P * kvs).index_select(0, idx).cpu().numpy()
+        vp = self.v.view(-1, P * kvs).index_select(0, idx).cpu().numpy()
+        ik, kp, vp = (np.ascontiguousarray(x.view(np.uint16).reshape(-1)) for x in (ik, kp, vp))
+        runs, rows, off = [], [], 0
+        for i in range(n_seq):
+            n = len(self.pages[i])
+            runs.append([i, self.pos[i], off, n])
+            rows.extend((off + j) * P for j in range(n))
+            off += n
+        runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
+        iq = self.index_q.cpu().numpy().view(np.uint16)[:n_seq * self.IH * self.HD].copy()
+        q = self.q.cpu().numpy().view(np.uint16)[:n_seq * self.NQ * self.HD].copy()
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(self.HD)))
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 3 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            bi, _ = oracle.lightning_indexer(runs, rows, iq, ik, num_heads=self.IH,
+                                             head_dim=self.HD, block_size=self.BLOCK,
+                                             topk=self.TOPK, local_blocks=1, init_blocks=0,
+                                             scale=scale, page_len=P, seq_len=n_seq)
+            oracle.block_sparse_attention(runs, rows, q, kp, vp, bi, num_q=self.NQ,
+                                          num_kv=self.NKV, head_dim=self.HD, kv_stride=kvs,
+                                          block_size=self.BLOCK, topk=self.TOPK, page_len=P,
+                                          seq_len=n_seq)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        frac = n_seq / len(self.pos)
+        sample_bytes = self.step_bytes() * sum(self.pos[:n_seq]) / sum(self.pos)
+        return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port",
+                "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
+                           f"({frac:.3f} of the batch by count), indexer + sparse attention, "
+                           f"one thread, median of {len(times)}")}
+
+
 class PrefillBf16:
     """Config 4: chunked prefill -- 8 sequences append 2048 tokens each onto
     prefixes ~ U[0, 16384] (RoPE + cache write), then causal full-attention
@@ -559,7 +705,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5))
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6))
     ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -588,9 +734,11 @@ def main() -> None:
     if a.copy_calibration:
         copy_calibration(dev)
         return
-    if a.cap <= 0:
+    if a.cap <= 0 and a.config != 6:
         a.cap = DEFAULT_CAP[a.config]
-    if a.config == 5:
+    if a.config == 6:
+        w = SparseM3(a.seed)
+    elif a.config == 5:
         w = DecodeBq(a.seed)
     elif a.config == 4:
         w = PrefillBf16(a.seed)
@@ -601,7 +749,7 @@ def main() -> None:
     wall, per = measure(w, a.steps, a.warmup)
     ms_per_step = wall / a.steps * 1e3
     value = w.step_bytes() / (wall / a.steps) / 1e9
-    dom_us = per["partials"] if "partials" in per else per["attention"]
+    dom_us = per[getattr(w, "dominant_phase", "partials" if "partials" in per else "attention")]
     if getattr(w, "bound", "hbm") == "mfma":
         tflops = w.flops() / (dom_us * 1e-6) / 1e12
         roof = {"bound": "mfma", "kernel": w.dominant, "achieved": round(tflops, 1),

@@ -13,10 +13,10 @@
 //                       32-slot streaming bank, each reduction done as a rank
 //                       count under reduce_argmax's order (value, then slot
 //                       lane, then slot register).
-// sparse_attention_kernel  one wave per (token, kv head): S = K.Q^T for the 16
-//                       q heads of the kv head on MFMA, the reference's
-//                       per-tile online softmax, P.V in f32 in position order,
-//                       and the one-stripe finalisation.
+// sparse_attention_kernel  one wave per (token, kv head): S = K.Q^T and P.V for
+//                       the 16 q heads of the kv head on MFMA around the
+//                       reference's per-tile online softmax, then the
+//                       one-stripe finalisation.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -211,17 +211,69 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
 // B = the 16 queries' dims, so lane l holds S[pos 4*(l/16)+j][head l%16].
 // Softmax per tile follows online_softmax_tile with the biased exp; the tile
 // weight sum uses the 16-position halving tree (xor 32, xor 16, then in-lane).
-// P.V: lane l owns dims 2l, 2l+1 of all 16 heads and adds w*v in position
-// order, as process_kv_tile's fma chain does per element.
+// P.V: v_mfma_f32_16x16x16_bf16 per 16-dim block with A = V^T (a transposing
+// LDS read of the tile's rows) and B = P^T, which is the softmax layout
+// itself, so the accumulator C[dim][head] rescales lane-locally.  P enters as
+// bf16 hi + lo parts (about 16 significant bits per weight); pad positions
+// carry their fexp(-87) into l but a zero weight into P.V, as in the
+// reference.  The next tile's keys and values load while a tile computes.
 // ---------------------------------------------------------------------------
-constexpr int kSD = 128;  // head_dim
-constexpr int kSG = 16;   // q heads per kv head
+constexpr int kSD = 128;                // head_dim
+constexpr int kSG = 16;                 // q heads per kv head
+constexpr int kSVPitch = kSD * 2 + 32;  // bytes per V row in LDS
+constexpr int kSVBytes = kTile * kSVPitch;
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// The tile walk: blocks in list order, stopping at the first -1, each from
+// its first position to min(end, cap) in 16-position steps.
+struct TileCursor {
+  int s;
+  int64_t pos, phi;
+  bool valid;
+};
+
+__device__ __forceinline__ TileCursor next_tile(TileCursor c, const int32_t* brow, int topk,
+                                                int block_size, int64_t cap) {
+  c.pos += kTile;
+  while (c.pos >= c.phi) {
+    ++c.s;
+    if (c.s >= topk) {
+      c.valid = false;
+      return c;
+    }
+    const int b = brow[c.s];
+    if (b < 0) {
+      c.valid = false;
+      return c;
+    }
+    c.pos = static_cast<int64_t>(b) * block_size;
+    c.phi = min(c.pos + block_size, cap);
+  }
+  c.valid = true;
+  return c;
+}
+
+struct TileRegs {
+  uint4 k0, k1, k2, k3;  // keys: row r16, dims 32c + 8g .. +8
+  uint4 v0, v1, v2, v3;  // values: rows g, g+4, g+8, g+12, 16 bytes at 16*r16
+};
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 __global__ __launch_bounds__(256) void sparse_attention_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k_base, const uint16_t* __restrict__ v_base,
     const int32_t* __restrict__ block_idx, uint16_t* __restrict__ out, int64_t kv_stride,
     int num_q, int num_kv, int block_size, int topk, int shift, int row_mask, int num_rows) {
+  __shared__ __align__(16) uint8_t vlds[4][2][kSVBytes];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
@@ -233,7 +285,7 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
   const int r16 = lane & 15;
   const int g = lane >> 4;
 
-  // B operand: Q[head r16][32c + 8g .. +8] for c = 0..3.
+  // B operand of the scores: Q[head r16][32c + 8g .. +8] for c = 0..3.
   bf16x8_t qf[4];
   {
     const uint16_t* qrow =
@@ -243,102 +295,132 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
       qf[c] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(qrow + 32 * c));
   }
   const uint16_t* kh = k_base + static_cast<int64_t>(h) * kSD;
-  const uint16_t* vh = v_base + static_cast<int64_t>(h) * kSD + 2 * lane;
-
-  float m = kNegBig;     // state of head r16 (same in the 4 lanes of the head)
-  float lsum = 0.0f;
-  float acc[kSG][2];     // dims 2*lane, 2*lane+1 of every head
-#pragma unroll
-  for (int hh = 0; hh < kSG; ++hh) acc[hh][0] = acc[hh][1] = 0.0f;
-
+  const uint16_t* vh = v_base + static_cast<int64_t>(h) * kSD;
   const int32_t* brow = block_idx + static_cast<int64_t>(row) * topk;
-  for (int s = 0; s < topk; ++s) {
-    const int b = brow[s];
-    if (b < 0) break;
-    const int64_t plo = static_cast<int64_t>(b) * block_size;
-    const int64_t phi = min(plo + block_size, cap);
-    for (int64_t pos = plo; pos < phi; pos += kTile) {
-      const int tl = static_cast<int>(min<int64_t>(kTile, phi - pos));
-      // K: row pos + r16 (a pad row repeats pos and is masked below).
-      const int pk = static_cast<int>(pos) + (r16 < tl ? r16 : 0);
-      const int64_t kslot = static_cast<int64_t>(tp.rows[pk >> shift]) + (pk & row_mask);
-      const uint16_t* kp = kh + kslot * kv_stride + 8 * g;
-      f32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+  // V staging: lane takes 16 bytes of rows g, g+4, g+8, g+12.
+  const int vcol = 16 * r16;
+  // Transposing read: lane r16 of group g addresses row 4g + r16/4, dims
+  // 4*(r16%4) .. +3 of a 16-dim block, and receives V[4g + k][16b + r16].
+  const int tr_off = (4 * g + (r16 >> 2)) * kSVPitch + 8 * (r16 & 3);
+
+  auto load_tile = [&](const TileCursor& c) {
+    TileRegs d;
+    const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
+    const int pk = static_cast<int>(c.pos) + (r16 < tl ? r16 : 0);
+    const int64_t kslot = static_cast<int64_t>(tp.rows[pk >> shift]) + (pk & row_mask);
+    const uint16_t* kp = kh + kslot * kv_stride + 8 * g;
+    d.k0 = *reinterpret_cast<const uint4*>(kp);
+    d.k1 = *reinterpret_cast<const uint4*>(kp + 32);
+    d.k2 = *reinterpret_cast<const uint4*>(kp + 64);
+    d.k3 = *reinterpret_cast<const uint4*>(kp + 96);
+    auto vrow = [&](int rr) {
+      const int pv = static_cast<int>(c.pos) + (rr < tl ? rr : 0);
+      const int64_t vslot = static_cast<int64_t>(tp.rows[pv >> shift]) + (pv & row_mask);
+      return *reinterpret_cast<const uint4*>(
+          reinterpret_cast<const uint8_t*>(vh + vslot * kv_stride) + vcol);
+    };
+    d.v0 = vrow(g);
+    d.v1 = vrow(g + 4);
+    d.v2 = vrow(g + 8);
+    d.v3 = vrow(g + 12);
+    return d;
+  };
+
+  float m = kNegBig;  // state of head r16 (the same in its four lanes)
+  float lsum = 0.0f;
+  f32x4_t acc[kSD / 16];  // acc[b][j] = O[dim 16b + 4g + j][head r16]
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kp + 32 * c));
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], sc, 0, 0, 0);
-      }
-      // V rows of the tile: 4 bytes (2 dims) each.
-      uint32_t vv[kTile];
+  for (int b = 0; b < kSD / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  TileCursor cur = next_tile(TileCursor{-1, 0, 0, false}, brow, topk, block_size, cap);
+  TileRegs rg{};
+  if (cur.valid) rg = load_tile(cur);
+  int buf = 0;
+  while (cur.valid) {
+    const TileCursor nxt = next_tile(cur, brow, topk, block_size, cap);
+    const int tl = static_cast<int>(min<int64_t>(kTile, cur.phi - cur.pos));
+    uint8_t* vb = vlds[wave][buf];
+    wave_sync();
+    *reinterpret_cast<uint4*>(vb + g * kSVPitch + vcol) = rg.v0;
+    *reinterpret_cast<uint4*>(vb + (g + 4) * kSVPitch + vcol) = rg.v1;
+    *reinterpret_cast<uint4*>(vb + (g + 8) * kSVPitch + vcol) = rg.v2;
+    *reinterpret_cast<uint4*>(vb + (g + 12) * kSVPitch + vcol) = rg.v3;
+    TileRegs rn{};
+    if (nxt.valid) rn = load_tile(nxt);
+
+    f32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k0), qf[0], sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k1), qf[1], sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k2), qf[2], sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k3), qf[3], sc, 0, 0, 0);
+    // Scores of pad positions are -1e30 (their fexp(-87) enters l only).
+    float sj[4];
 #pragma unroll
-      for (int j = 0; j < kTile; ++j) {
-        const int pj = static_cast<int>(pos) + (j < tl ? j : 0);
-        const int64_t vslot = static_cast<int64_t>(tp.rows[pj >> shift]) + (pj & row_mask);
-        vv[j] = *reinterpret_cast<const uint32_t*>(vh + vslot * kv_stride);
-      }
-      // Scores of pad positions are -1e30 (they enter l through fexp(-87)).
-      float sj[4];
+    for (int j = 0; j < 4; ++j) sj[j] = (4 * g + j < tl) ? sc[j] : kNegBig;
+    float tmax = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
+    tmax = max_ref(tmax, shfl_xor_f32(tmax, 16));
+    tmax = max_ref(tmax, shfl_xor_f32(tmax, 32));
+    const float m_new = tmax > m ? tmax : m;
+    const float corr = fexp(max_ref(-87.0f, m - m_new));
+    float w[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sj[j] = (4 * g + j < tl) ? sc[j] : kNegBig;
-      float tmax = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
-      tmax = max_ref(tmax, shfl_xor_f32(tmax, 16));
-      tmax = max_ref(tmax, shfl_xor_f32(tmax, 32));
-      const float m_new = tmax > m ? tmax : m;
-      const float corr = fexp(max_ref(-87.0f, m - m_new));
-      float w[4];
+    for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sj[j] - m_new));
+    // 16-position halving tree: t with t+8 (xor 32), t+4 (xor 16), then j+2, j+1.
+    float ws[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sj[j] - m_new));
-      // 16-position halving tree: t with t+8 (xor 32), t+4 (xor 16), then j+2, j+1.
-      float ws[4];
+    for (int j = 0; j < 4; ++j) ws[j] = w[j] + shfl_xor_f32(w[j], 32);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ws[j] = w[j] + shfl_xor_f32(w[j], 32);
+    for (int j = 0; j < 4; ++j) ws[j] = ws[j] + shfl_xor_f32(ws[j], 16);
+    const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
+    lsum = lsum * corr + wsum;
+    m = m_new;
+    // P^T as bf16 hi + lo, zero at pads.
+    s16x4_t phi, plo;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ws[j] = ws[j] + shfl_xor_f32(ws[j], 16);
-      const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
-      lsum = lsum * corr + wsum;
-      m = m_new;
-      // scale_unrolled, then the tile's P.V in position order.
-#pragma unroll
-      for (int hh = 0; hh < kSG; ++hh) {
-        const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), hh));
-        acc[hh][0] = acc[hh][0] * c;
-        acc[hh][1] = acc[hh][1] * c;
-      }
-#pragma unroll
-      for (int j = 0; j < kTile; ++j) {
-        if (j >= tl) break;
-        const float v0 = bf16_lo(vv[j]);
-        const float v1 = bf16_hi(vv[j]);
-#pragma unroll
-        for (int hh = 0; hh < kSG; ++hh) {
-          const float wj = __int_as_float(
-              __builtin_amdgcn_readlane(__float_as_int(w[j & 3]), 16 * (j >> 2) + hh));
-          acc[hh][0] = fmaf(v0, wj, acc[hh][0]);
-          acc[hh][1] = fmaf(v1, wj, acc[hh][1]);
-        }
-      }
+    for (int j = 0; j < 4; j += 2) {
+      const float p0 = (4 * g + j < tl) ? w[j] : 0.0f;
+      const float p1 = (4 * g + j + 1 < tl) ? w[j + 1] : 0.0f;
+      const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
+      const float r0 = p0 - static_cast<float>(hb[0]);
+      const float r1 = p1 - static_cast<float>(hb[1]);
+      const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+      const s16x4_t hs = __builtin_bit_cast(s16x4_t, __builtin_shufflevector(hb, hb, 0, 1, 0, 1));
+      const s16x4_t ls = __builtin_bit_cast(s16x4_t, __builtin_shufflevector(lb, lb, 0, 1, 0, 1));
+      phi[j] = hs[0];
+      phi[j + 1] = hs[1];
+      plo[j] = ls[0];
+      plo[j + 1] = ls[1];
     }
+    wave_sync();
+#pragma unroll
+    for (int b = 0; b < kSD / 16; ++b) {
+      acc[b] = acc[b] * corr;  // scale_unrolled for head r16
+      const s16x4_t va =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + tr_off + 32 * b));
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
+    }
+    rg = rn;
+    cur = nxt;
+    buf ^= 1;
   }
 
   // write_finalized_head over one stripe: cv = fexp(0) scales both acc and
-  // l (l > 0), out = (acc * cv) * (1 / (l * cv)).
-  uint16_t* orow = out + (static_cast<int64_t>(t) * num_q + h * kSG) * kSD + 2 * lane;
+  // l (l > 0), out = (acc * cv) * (1 / (0 + l * cv)).
+  const float gm = m > kNegBig ? m : kNegBig;
+  float cv = fexp(max_ref(-87.0f, m - gm));
+  cv = lsum > 0.0f ? cv : 0.0f;
+  const float gl = 0.0f + lsum * cv;
+  const float inv = gl > 0.0f ? 1.0f / gl : 0.0f;
+  uint16_t* orow = out + (static_cast<int64_t>(t) * num_q + h * kSG + r16) * kSD + 4 * g;
 #pragma unroll
-  for (int hh = 0; hh < kSG; ++hh) {
-    const float lh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), hh));
-    const float mh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), hh));
-    const float gm = mh > kNegBig ? mh : kNegBig;
-    float cv = fexp(max_ref(-87.0f, mh - gm));
-    cv = lh > 0.0f ? cv : 0.0f;
-    const float gl = 0.0f + lh * cv;
-    uint32_t packed = 0;
+  for (int b = 0; b < kSD / 16; ++b) {
+    uint32_t lo = 0, hi = 0;
     if (gl > 0.0f) {
-      const float inv = 1.0f / gl;
-      packed = f32_to_bf16_bits((acc[hh][0] * cv) * inv) |
-               (f32_to_bf16_bits((acc[hh][1] * cv) * inv) << 16);
+      lo = f32_to_bf16_bits((acc[b][0] * cv) * inv) | (f32_to_bf16_bits((acc[b][1] * cv) * inv) << 16);
+      hi = f32_to_bf16_bits((acc[b][2] * cv) * inv) | (f32_to_bf16_bits((acc[b][3] * cv) * inv) << 16);
     }
-    *reinterpret_cast<uint32_t*>(orow + static_cast<int64_t>(hh) * kSD) = packed;
+    *reinterpret_cast<uint2*>(orow + 16 * b) = make_uint2(lo, hi);
   }
 }
 
