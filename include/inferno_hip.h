@@ -283,6 +283,27 @@ int32_t ifr_block_sparse_attention(const void* image_dev, const int64_t* info,
                                    int64_t block_size, int64_t topk_blocks,
                                    int64_t page_len, uint64_t stream);
 
+/* dispatch_bq_block_sparse_attention (prototypes/bq_sparse_attention.mojo:
+ * 351-430): the int8 KV variant (codes and f32 scales as ifr_bq_attn_prep
+ * writes them, q codes with qi_bias and f_q).  seq_len > 1:
+ * BqBlockSparseFlashKernel (:94-186) per (token, kv head), blocks in order,
+ * -1 ends the list.  seq_len == 1: BqBlockSparseFlashDecodeKernel (:216-310):
+ * the num_kv * min(topk, causal blocks) (kv head, slot) units are banded over
+ * min(cap, units) workers (cap: the reference's worker capacity, which fixes
+ * the result as in ifr_plan_attention), -1 slots skipped, and the workers'
+ * partial stripes merged per head; partials of ifr_bq_sparse_partials_bytes
+ * (0 bytes for seq_len > 1). */
+int64_t ifr_bq_sparse_partials_bytes(const int64_t* info, int64_t num_q, int64_t num_kv,
+                                     int64_t head_dim, int64_t block_size,
+                                     int64_t topk_blocks, int64_t cap);
+int32_t ifr_bq_block_sparse_attention(
+    const void* image_dev, const int64_t* info, const void* q_i8, const float* qi_bias,
+    const float* f_q, const void* k_base, const float* k_scale, const void* v_base,
+    const float* v_scale, const int32_t* block_idx, void* output, void* partials,
+    int64_t partials_bytes, int64_t num_q, int64_t num_kv, int64_t head_dim,
+    int64_t kv_stride, int64_t block_size, int64_t topk_blocks, int64_t page_len,
+    int64_t cap, uint64_t stream);
+
 /* ---- o_proj (the step after the attention) ----------------------------------
  * dispatch_gemm_cols[rows] (kernels/gemm.mojo:198-225; called at
  * modeling/gemma_4_moe.mojo:387-392 and :485-490 with rows = HIDDEN):

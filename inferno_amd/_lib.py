@@ -74,6 +74,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                     I64, F32, I64, U64]),
     "ifr_block_sparse_attention": (I32, [VP, P_I64, VP, VP, VP, VP, VP, I64, I64, I64, I64,
                                          I64, I64, I64, U64]),
+    "ifr_bq_sparse_partials_bytes": (I64, [P_I64, I64, I64, I64, I64, I64, I64]),
+    "ifr_bq_block_sparse_attention": (I32, [VP, P_I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP,
+                                            I64, I64, I64, I64, I64, I64, I64, I64, I64,
+                                            U64]),
     "ifr_gemm_cols_workspace_bytes": (I64, [I64, I64, I64]),
     "ifr_dispatch_gemm_cols": (I32, [VP, VP, VP, I64, I64, I64, VP, I64, U64]),
     # ---- host-side page state (include/inferno_host.h) ----

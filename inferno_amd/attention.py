@@ -264,6 +264,31 @@ def dispatch_block_sparse_attention(plan: AttentionPlan, q, k_base, v_base, bloc
         plan.page_len, _stream()))
 
 
+def dispatch_bq_block_sparse_attention(plan: AttentionPlan, q_i8, qi_bias, f_q, k_base,
+                                       k_scale, v_base, v_scale, block_idx, output, *,
+                                       cap: int, num_q: int = 64, num_kv: int = 4,
+                                       head_dim: int = 128, kv_stride: int = 512,
+                                       block_size: int = 128, topk_blocks: int = 16,
+                                       partials=None) -> None:
+    """dispatch_bq_block_sparse_attention (prototypes/bq_sparse_attention.mojo:
+    351-430), defaults of dispatch_bq_minimax_m3_sparse_attention (:443-486).
+    `cap` is the reference's worker capacity (it bands a decode step's blocks)."""
+    import torch
+
+    n = lib().ifr_bq_sparse_partials_bytes(plan.info_ptr, num_q, num_kv, head_dim, block_size,
+                                          topk_blocks, cap)
+    if n < 0:
+        raise ValueError("bad bq sparse shape")
+    if partials is None and n > 0:
+        partials = torch.empty(n // 4, dtype=torch.float32, device=output.device)
+    pbytes = partials.numel() * 4 if partials is not None else 0
+    check(lib().ifr_bq_block_sparse_attention(
+        _ptr(plan.image), plan.info_ptr, _ptr(q_i8), _ptr(qi_bias), _ptr(f_q), _ptr(k_base),
+        _ptr(k_scale), _ptr(v_base), _ptr(v_scale), _ptr(block_idx), _ptr(output),
+        _ptr(partials) if partials is not None else None, pbytes, num_q, num_kv, head_dim,
+        kv_stride, block_size, topk_blocks, plan.page_len, cap, _stream()))
+
+
 def gemm_cols_workspace(rows: int, cols: int, seq_len: int, device="cuda"):
     """f32 workspace for dispatch_gemm_cols at this shape (None if unneeded)."""
     import torch
@@ -299,4 +324,5 @@ __all__ = [
     "dispatch_bq_attn_prep", "bq_attention", "dispatch_bq_block_quant",
     "gemm_cols_workspace", "dispatch_gemm_cols", "index_scores_buffer",
     "dispatch_lightning_indexer", "dispatch_block_sparse_attention",
+    "dispatch_bq_block_sparse_attention",
 ]

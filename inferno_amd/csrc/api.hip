@@ -1087,6 +1087,79 @@ int32_t ifr_block_sparse_attention(const void* image_dev, const int64_t* info, c
   return ok();
 }
 
+}  // extern "C"
+
+namespace {
+// The decode route's (kv head, block slot) units and worker count:
+// min(topk, causal blocks) slots per head, min(cap, units) workers.
+void bq_sparse_decode_shape(const int64_t* info, int64_t num_kv, int64_t block_size,
+                            int64_t topk, int64_t cap, int64_t* slots, int64_t* workers) {
+  *slots = std::min<int64_t>(topk, info[13] / block_size + 1);
+  *workers = std::min<int64_t>(cap, num_kv * *slots);
+}
+}  // namespace
+
+extern "C" {
+
+int64_t ifr_bq_sparse_partials_bytes(const int64_t* info, int64_t num_q, int64_t num_kv,
+                                     int64_t head_dim, int64_t block_size,
+                                     int64_t topk_blocks, int64_t cap) {
+  if (check_info(info) != IFR_OK || num_kv <= 0 || block_size <= 0 || topk_blocks <= 0 ||
+      cap < 1)
+    return -1;
+  if (info[5] != 1) return 0;
+  int64_t slots, workers;
+  bq_sparse_decode_shape(info, num_kv, block_size, topk_blocks, cap, &slots, &workers);
+  return workers * ifr_flash_partial_stride(num_q, head_dim) * 4;
+}
+
+int32_t ifr_bq_block_sparse_attention(
+    const void* image_dev, const int64_t* info, const void* q_i8, const float* qi_bias,
+    const float* f_q, const void* k_base, const float* k_scale, const void* v_base,
+    const float* v_scale, const int32_t* block_idx, void* output, void* partials,
+    int64_t partials_bytes, int64_t num_q, int64_t num_kv, int64_t head_dim,
+    int64_t kv_stride, int64_t block_size, int64_t topk_blocks, int64_t page_len,
+    int64_t cap, uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (info[11] != 1) return fail(IFR_EINVAL, "sparse attention needs a full-attention plan");
+  if (head_dim != 128 || num_kv <= 0 || num_q != 16 * num_kv || num_q > 1024)
+    return fail(IFR_EUNSUPPORTED, "bq sparse attention is compiled for head_dim 128, gqa 16");
+  if (kv_stride < num_kv * head_dim || kv_stride % 16 != 0)
+    return fail(IFR_EINVAL, "kv_stride must cover num_kv heads in 16-byte rows");
+  if (block_size <= 0 || block_size > (1 << 20))
+    return fail(IFR_EINVAL, "block_size must be in [1, 2^20]");
+  if (topk_blocks <= 0 || topk_blocks > (1 << 16)) return fail(IFR_EINVAL, "bad topk_blocks");
+  if (cap < 1 || cap > (1 << 20)) return fail(IFR_EINVAL, "cap must be in [1, 2^20]");
+  if (!image_dev || !q_i8 || !qi_bias || !f_q || !k_base || !k_scale || !v_base || !v_scale ||
+      !block_idx || !output)
+    return fail(IFR_EINVAL, "null pointer");
+  if (!aligned(q_i8, 16) || !aligned(k_base, 16) || !aligned(v_base, 16) ||
+      !aligned(output, 8) || !aligned(block_idx, 4))
+    return fail(IFR_EINVAL, "q, k and v codes must be 16-byte aligned");
+  if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
+  st = check_geometry(info, pow2_shift(page_len), page_len - 1, -1);
+  if (st) return st;
+  const int64_t ps = ifr_flash_partial_stride(num_q, head_dim);
+  int64_t slots = 0, workers = 1;
+  if (info[5] == 1) {
+    bq_sparse_decode_shape(info, num_kv, block_size, topk_blocks, cap, &slots, &workers);
+    if (!partials || !aligned(partials, 16) || partials_bytes < workers * ps * 4)
+      return fail(IFR_ESPACE, "partials need %lld bytes, 16-byte aligned",
+                  (long long)(workers * ps * 4));
+  }
+  IFR_HIP(ifr::launch_bq_block_sparse_attention(
+              static_cast<const int32_t*>(image_dev), static_cast<int>(info[5]), q_i8,
+              qi_bias, f_q, k_base, k_scale, v_base, v_scale, block_idx, output,
+              static_cast<float*>(partials), ps, kv_stride, static_cast<int>(num_q),
+              static_cast<int>(num_kv), static_cast<int>(block_size),
+              static_cast<int>(topk_blocks), static_cast<int>(slots),
+              static_cast<int>(workers), static_cast<int>(info[7]),
+              static_cast<int>(info[8]), as_stream(stream)),
+          "bq_block_sparse_attention");
+  return ok();
+}
+
 int64_t ifr_gemm_cols_workspace_bytes(int64_t rows, int64_t cols, int64_t seq_len) {
   if (rows <= 0 || cols <= 0 || seq_len < 0) return -1;
   return ifr::gemm_cols_workspace_bytes(seq_len, rows, cols);

@@ -419,7 +419,8 @@ __global__ __launch_bounds__(256) void merge_kernel(
 template <int D>
 __global__ __launch_bounds__(256) void merge_sliced_kernel(
     const int32_t* __restrict__ image, const float* __restrict__ partials,
-    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode) {
+    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode,
+    int direct_n) {
   // The same merge with the head's dims spread over D/64 waves (blockIdx.z
   // picks a 64-dim slice, a lane owns one dim): for units with many splits,
   // whose acc chain is long, this puts D/64 times more waves on the loads.
@@ -429,10 +430,14 @@ __global__ __launch_bounds__(256) void merge_sliced_kernel(
   const int h = blockIdx.y * 4 + wave;
   if (h >= num_q) return;
   const int dim = 64 * blockIdx.z + lane;
-  const int32_t* unit = image + image[kHdrOffUnits] + blockIdx.x * kUnitWords;
-  const int out_row = unit[0];
-  const int stripe_base = unit[1];
-  const int n = unit[2];
+  // direct_n > 0: one output row 0 over stripes [0, direct_n), no plan image.
+  int out_row = 0, stripe_base = 0, n = direct_n;
+  if (direct_n <= 0) {
+    const int32_t* unit = image + image[kHdrOffUnits] + blockIdx.x * kUnitWords;
+    out_row = unit[0];
+    stripe_base = unit[1];
+    n = unit[2];
+  }
   const float* base = partials + static_cast<int64_t>(stripe_base) * partial_stride;
   const int m_off = num_q * D;
   const int l_off = m_off + num_q;
@@ -536,6 +541,15 @@ bool attention_shape_supported(int head_dim, int gqa) {
   return (head_dim == 256 || head_dim == 512) && (gqa == 1 || gqa == 2);
 }
 
+hipError_t launch_merge_stripes(const float* partials, void* output, int64_t ps,
+                                int n_stripes, int num_q, hipStream_t stream) {
+  if (n_stripes <= 0) return hipSuccess;
+  dim3 grid(1, (num_q + 3) / 4, 128 / 64);
+  hipLaunchKernelGGL(merge_sliced_kernel<128>, grid, dim3(256), 0, stream, nullptr, partials,
+                     static_cast<uint16_t*>(output), ps, num_q, 0, n_stripes);
+  return hipGetLastError();
+}
+
 hipError_t launch_merge(const int32_t* image, int num_units, int num_stripes, int mode,
                         const float* partials, void* output, int64_t ps,
                         int num_q, int head_dim, hipStream_t stream, int8_t* q_out,
@@ -551,14 +565,14 @@ hipError_t launch_merge(const int32_t* image, int num_units, int num_stripes, in
   if (head_dim == 256) {
     if (sliced)
       hipLaunchKernelGGL(merge_sliced_kernel<256>, grid, dim3(256), 0, stream, image,
-                         partials, o, ps, num_q, mode);
+                         partials, o, ps, num_q, mode, 0);
     else
       hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image, partials, o,
                          ps, num_q, mode, q_out, q_scale);
   } else {
     if (sliced)
       hipLaunchKernelGGL(merge_sliced_kernel<512>, grid, dim3(256), 0, stream, image,
-                         partials, o, ps, num_q, mode);
+                         partials, o, ps, num_q, mode, 0);
     else
       hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image, partials, o,
                          ps, num_q, mode, q_out, q_scale);

@@ -78,6 +78,18 @@ hipError_t launch_block_sparse_attention(const int32_t* image, int seq_len, cons
                                          int block_size, int topk, int shift, int row_mask,
                                          hipStream_t stream);
 
+// write_finalized_head for every head of one output row over stripes
+// [0, n_stripes) of head_dim 128 partials (no plan image).
+hipError_t launch_merge_stripes(const float* partials, void* output, int64_t ps,
+                                int n_stripes, int num_q, hipStream_t stream);
+hipError_t launch_bq_block_sparse_attention(
+    const int32_t* image, int seq_len, const void* q_i8, const float* qi_bias,
+    const float* f_q, const void* k_base, const float* k_scale, const void* v_base,
+    const float* v_scale, const int32_t* block_idx, void* output, float* partials,
+    int64_t partial_stride, int64_t kv_stride, int num_q, int num_kv, int block_size,
+    int topk, int decode_slots, int decode_workers, int shift, int row_mask,
+    hipStream_t stream);
+
 // num_stripes: partial stripes of the plan (one per split).  q_out / q_scale
 // (optional): per-head absmax int8 of the merged outputs, fused.
 hipError_t launch_merge(const int32_t* image_dev, int num_units, int num_stripes, int mode,

@@ -424,6 +424,275 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// bq_process_kv_tile_head (prototypes/bq_sparse_attention.mojo:23-91) inside
+// BqBlockSparseFlashKernel (:94-186, one (token, kv head) per wave, blocks in
+// order, -1 ends the list, one-stripe finalisation) and
+// BqBlockSparseFlashDecodeKernel (:216-310, one (worker, kv head) per wave over
+// the worker's band of block slots, -1 skipped, a partial stripe per worker).
+//
+// Scores: raw = sum (k ^ 0x80) * q over u8 x i8 equals sum k*q + 128 * sum q,
+// both exact integers; sum k*q comes from v_mfma_i32_16x16x64_i8, so
+// ((raw - qi_bias) * f_q * k_scale) / 127^2 is the reference's value.
+// P.V: the tile's int8 values enter LDS as bf16 (exact), weights are
+// (w * v_scale) / 127 as in the reference, on the bf16 MFMA as hi + lo.
+// ---------------------------------------------------------------------------
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+struct BqTileRegs {
+  uint4 k0, k1;  // keys: row r16, bytes 16g and 64 + 16g
+  uint2 v0, v1;  // values: row r16/4 and 4 + r16/4 ... (see load)
+  uint2 v2, v3;
+};
+
+template <bool kDecode>
+__global__ __launch_bounds__(256) void bq_sparse_kernel(
+    const int32_t* __restrict__ image, const int8_t* __restrict__ q_i8,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const int8_t* __restrict__ k_base, const float* __restrict__ k_scale,
+    const int8_t* __restrict__ v_base, const float* __restrict__ v_scale,
+    const int32_t* __restrict__ block_idx, uint16_t* __restrict__ out,
+    float* __restrict__ partials, int64_t partial_stride, int64_t kv_stride, int num_q,
+    int num_kv, int block_size, int topk, int decode_slots, int decode_workers, int shift,
+    int row_mask, int num_rows) {
+  __shared__ __align__(16) uint8_t vlds[4][2][kSVBytes];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= num_rows) return;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  // Unit: (token t | worker w, kv head h) and its slot range.
+  const int unit = row / num_kv;
+  const int h = row - unit * num_kv;
+  const int t = kDecode ? 0 : unit;
+  int s_lo = 0, s_hi = topk;
+  if (kDecode) {
+    const int total = num_kv * decode_slots;  // worker_range over (head, slot) units
+    const int per = (total + decode_workers - 1) / decode_workers;
+    const int lo = min(unit * per, total), hi = min(lo + per, total);
+    s_lo = max(lo, h * decode_slots) - h * decode_slots;
+    s_hi = min(hi, (h + 1) * decode_slots) - h * decode_slots;
+  }
+  const TokenPos tp = token_position(image, t);
+  const int64_t cap = static_cast<int64_t>(tp.abs_pos) + 1;
+  const int gh = h * kSG + r16;  // q head of this lane's column
+  const int64_t qrow = static_cast<int64_t>(t) * num_q + gh;
+
+  // B operand of the scores: q codes of head r16, bytes 16g and 64 + 16g;
+  // qsum = sum of the head's 128 codes (exact).
+  const int8_t* qp = q_i8 + qrow * kSD + 16 * g;
+  const uint4 qa = *reinterpret_cast<const uint4*>(qp);
+  const uint4 qb4 = *reinterpret_cast<const uint4*>(qp + 64);
+  int qsum = 0;
+  {
+    const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb4.x, qb4.y, qb4.z, qb4.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      qsum += static_cast<int8_t>(w8[i]) + static_cast<int8_t>(w8[i] >> 8) +
+              static_cast<int8_t>(w8[i] >> 16) + static_cast<int8_t>(w8[i] >> 24);
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+  }
+  const float qbias = qi_bias[qrow];
+  const float fq = f_q[qrow];
+  const float inv127 = 1.0f / 127.0f;
+  const float inv127sq = inv127 * inv127;
+
+  const int8_t* kh = k_base + static_cast<int64_t>(h) * kSD;
+  const int8_t* vh = v_base + static_cast<int64_t>(h) * kSD;
+  const int32_t* brow =
+      block_idx + (kDecode ? static_cast<int64_t>(h) : static_cast<int64_t>(row)) * topk;
+  const int tr_off = (4 * g + (r16 >> 2)) * kSVPitch + 8 * (r16 & 3);
+
+  auto slot_of = [&](int p) {
+    return static_cast<int64_t>(tp.rows[p >> shift]) + (p & row_mask);
+  };
+  // V staging: lane takes 32 bytes (dims 32*(l%4) ..) of row l/4.
+  const int vr_row = lane >> 2;
+  const int vr_col = 32 * (lane & 3);
+  auto load_tile = [&](const TileCursor& c) {
+    BqTileRegs d;
+    const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
+    const int pk = static_cast<int>(c.pos) + (r16 < tl ? r16 : 0);
+    const int8_t* kp = kh + slot_of(pk) * kv_stride + 16 * g;
+    d.k0 = *reinterpret_cast<const uint4*>(kp);
+    d.k1 = *reinterpret_cast<const uint4*>(kp + 64);
+    const int pv = static_cast<int>(c.pos) + (vr_row < tl ? vr_row : 0);
+    const int8_t* vp = vh + slot_of(pv) * kv_stride + vr_col;
+    d.v0 = *reinterpret_cast<const uint2*>(vp);
+    d.v1 = *reinterpret_cast<const uint2*>(vp + 8);
+    d.v2 = *reinterpret_cast<const uint2*>(vp + 16);
+    d.v3 = *reinterpret_cast<const uint2*>(vp + 24);
+    return d;
+  };
+  auto next = [&](TileCursor c) {
+    c.pos += kTile;
+    while (c.pos >= c.phi) {
+      ++c.s;
+      if (c.s >= s_hi) {
+        c.valid = false;
+        return c;
+      }
+      const int b = brow[c.s];
+      if (b < 0) {
+        if (!kDecode) {
+          c.valid = false;
+          return c;
+        }
+        c.pos = 0;
+        c.phi = 0;
+        continue;
+      }
+      c.pos = static_cast<int64_t>(b) * block_size;
+      c.phi = min(c.pos + block_size, cap);
+    }
+    c.valid = true;
+    return c;
+  };
+
+  float m = kNegBig;
+  float lsum = 0.0f;
+  f32x4_t acc[kSD / 16];
+#pragma unroll
+  for (int b = 0; b < kSD / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  TileCursor cur = next(TileCursor{s_lo - 1, 0, 0, false});
+  BqTileRegs rg{};
+  if (cur.valid) rg = load_tile(cur);
+  int buf = 0;
+  while (cur.valid) {
+    const TileCursor nxt = next(cur);
+    const int tl = static_cast<int>(min<int64_t>(kTile, cur.phi - cur.pos));
+    uint8_t* vb = vlds[wave][buf];
+    wave_sync();
+    {
+      // 32 int8 values -> 32 bf16 (exact) at row vr_row, dims vr_col ..
+      const uint32_t w8[8] = {rg.v0.x, rg.v0.y, rg.v1.x, rg.v1.y,
+                              rg.v2.x, rg.v2.y, rg.v3.x, rg.v3.y};
+      uint32_t o16[16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int b = 0; b < 4; b += 2) {
+          const float f0 = static_cast<float>(static_cast<int8_t>(w8[i] >> (8 * b)));
+          const float f1 = static_cast<float>(static_cast<int8_t>(w8[i] >> (8 * b + 8)));
+          o16[2 * i + b / 2] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+        }
+      }
+      uint8_t* dst = vb + vr_row * kSVPitch + 2 * vr_col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4*>(dst + 16 * i) =
+            make_uint4(o16[4 * i], o16[4 * i + 1], o16[4 * i + 2], o16[4 * i + 3]);
+    }
+    BqTileRegs rn{};
+    if (nxt.valid) rn = load_tile(nxt);
+
+    i32x4_t si = {0, 0, 0, 0};
+    si = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+        __builtin_bit_cast(i32x4_t, rg.k0), __builtin_bit_cast(i32x4_t, qa), si, 0, 0, 0);
+    si = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+        __builtin_bit_cast(i32x4_t, rg.k1), __builtin_bit_cast(i32x4_t, qb4), si, 0, 0, 0);
+    // Lane holds positions 4g + j of head r16.
+    float sj[4], vsj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pj = static_cast<int>(cur.pos) + (4 * g + j < tl ? 4 * g + j : 0);
+      const int64_t sl = slot_of(pj) * num_kv + h;
+      const float ks = k_scale[sl];
+      vsj[j] = v_scale[sl];
+      const float raw = static_cast<float>(si[j] + 128 * qsum);
+      float sc = raw - qbias;
+      sc = sc * fq;
+      sc = sc * ks;
+      sc = sc * inv127sq;
+      sj[j] = (4 * g + j < tl) ? sc : kNegBig;
+    }
+    float tmax = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
+    tmax = max_ref(tmax, shfl_xor_f32(tmax, 16));
+    tmax = max_ref(tmax, shfl_xor_f32(tmax, 32));
+    const float m_new = tmax > m ? tmax : m;
+    const float corr = fexp(max_ref(-87.0f, m - m_new));
+    float w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sj[j] - m_new));
+    float ws[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ws[j] = w[j] + shfl_xor_f32(w[j], 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ws[j] = ws[j] + shfl_xor_f32(ws[j], 16);
+    const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
+    lsum = lsum * corr + wsum;
+    m = m_new;
+    s16x4_t phi, plo;
+#pragma unroll
+    for (int j = 0; j < 4; j += 2) {
+      float p0 = w[j] * vsj[j];
+      p0 = p0 * inv127;
+      float p1 = w[j + 1] * vsj[j + 1];
+      p1 = p1 * inv127;
+      p0 = (4 * g + j < tl) ? p0 : 0.0f;
+      p1 = (4 * g + j + 1 < tl) ? p1 : 0.0f;
+      const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
+      const float r0 = p0 - static_cast<float>(hb[0]);
+      const float r1 = p1 - static_cast<float>(hb[1]);
+      const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+      const s16x4_t hs = __builtin_bit_cast(s16x4_t, __builtin_shufflevector(hb, hb, 0, 1, 0, 1));
+      const s16x4_t ls = __builtin_bit_cast(s16x4_t, __builtin_shufflevector(lb, lb, 0, 1, 0, 1));
+      phi[j] = hs[0];
+      phi[j + 1] = hs[1];
+      plo[j] = ls[0];
+      plo[j + 1] = ls[1];
+    }
+    wave_sync();
+#pragma unroll
+    for (int b = 0; b < kSD / 16; ++b) {
+      acc[b] = acc[b] * corr;
+      const s16x4_t va =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + tr_off + 32 * b));
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
+    }
+    rg = rn;
+    cur = nxt;
+    buf ^= 1;
+  }
+
+  if constexpr (kDecode) {
+    // The worker's stripe: acc, m, l of the kv head's 16 q heads (the
+    // identity m = -1e30, l = 0 when its band does not reach the head).
+    float* pw = partials + static_cast<int64_t>(unit) * partial_stride;
+    float* prow = pw + static_cast<int64_t>(gh) * kSD + 4 * g;
+#pragma unroll
+    for (int b = 0; b < kSD / 16; ++b)
+      *reinterpret_cast<float4*>(prow + 16 * b) =
+          make_float4(acc[b][0], acc[b][1], acc[b][2], acc[b][3]);
+    if (g == 0) {
+      pw[num_q * kSD + gh] = m;
+      pw[num_q * kSD + num_q + gh] = lsum;
+    }
+  } else {
+    const float gm = m > kNegBig ? m : kNegBig;
+    float cv = fexp(max_ref(-87.0f, m - gm));
+    cv = lsum > 0.0f ? cv : 0.0f;
+    const float gl = 0.0f + lsum * cv;
+    const float inv = gl > 0.0f ? 1.0f / gl : 0.0f;
+    uint16_t* orow = out + qrow * kSD + 4 * g;
+#pragma unroll
+    for (int b = 0; b < kSD / 16; ++b) {
+      uint32_t lo = 0, hi = 0;
+      if (gl > 0.0f) {
+        lo = f32_to_bf16_bits((acc[b][0] * cv) * inv) |
+             (f32_to_bf16_bits((acc[b][1] * cv) * inv) << 16);
+        hi = f32_to_bf16_bits((acc[b][2] * cv) * inv) |
+             (f32_to_bf16_bits((acc[b][3] * cv) * inv) << 16);
+      }
+      *reinterpret_cast<uint2*>(orow + 16 * b) = make_uint2(lo, hi);
+    }
+  }
+}
+
 }  // namespace
 
 int index_block_stride(int64_t max_pos, int64_t block_size) {
@@ -454,6 +723,37 @@ hipError_t launch_lightning_indexer(const int32_t* image, int seq_len, const voi
   hipLaunchKernelGGL(select_blocks_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, image,
                      scores, block_idx, block_stride, num_heads, block_size, topk,
                      local_blocks, init_blocks, select_bank_cap(topk), rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_bq_block_sparse_attention(
+    const int32_t* image, int seq_len, const void* q_i8, const float* qi_bias,
+    const float* f_q, const void* k_base, const float* k_scale, const void* v_base,
+    const float* v_scale, const int32_t* block_idx, void* output, float* partials,
+    int64_t partial_stride, int64_t kv_stride, int num_q, int num_kv, int block_size,
+    int topk, int decode_slots, int decode_workers, int shift, int row_mask,
+    hipStream_t stream) {
+  if (seq_len <= 0) return hipSuccess;
+  const auto* q = static_cast<const int8_t*>(q_i8);
+  const auto* k = static_cast<const int8_t*>(k_base);
+  const auto* v = static_cast<const int8_t*>(v_base);
+  auto* o = static_cast<uint16_t*>(output);
+  if (seq_len == 1) {
+    const int rows = decode_workers * num_kv;
+    hipLaunchKernelGGL(bq_sparse_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0, stream,
+                       image, q, qi_bias, f_q, k, k_scale, v, v_scale, block_idx, o, partials,
+                       partial_stride, kv_stride, num_q, num_kv, block_size, topk,
+                       decode_slots, decode_workers, shift, row_mask, rows);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_merge_stripes(partials, output, partial_stride, decode_workers, num_q,
+                                stream);
+  }
+  const int rows = seq_len * num_kv;
+  hipLaunchKernelGGL(bq_sparse_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, stream,
+                     image, q, qi_bias, f_q, k, k_scale, v, v_scale, block_idx, o, partials,
+                     partial_stride, kv_stride, num_q, num_kv, block_size, topk, 0, 1, shift,
+                     row_mask, rows);
   return hipGetLastError();
 }
 

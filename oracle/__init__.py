@@ -49,6 +49,9 @@ _SIG = {
     "ifo_absmax_quantize": (F32, [VP, I64, VP, VP]),
     "ifo_bq_block_quant": (None, [VP, VP, VP, I64, I64, I64]),
     "ifo_gemm_cols": (None, [VP, VP, VP, I64, I64, I64]),
+    "ifo_bq_block_sparse_attention": (C.c_int, [VP, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP,
+                                                VP, I64, I64, I64, I64, I64, I64, I64, I64,
+                                                I64]),
     "ifo_index_block_scores": (None, [VP, I64, VP, VP, VP, VP, I64, I64, I64, I64, F32, I64,
                                       I64]),
     "ifo_select_blocks": (None, [VP, I64, I64, I64, I64, VP]),
@@ -266,6 +269,22 @@ def block_sparse_attention(runs, base_rows, q, k, v, block_idx, *, num_q, num_kv
                                           kv_stride, block_size, topk, page_len, seq_len)
     if st != 0:
         raise ValueError(f"oracle sparse attention rejected the arguments ({st})")
+    return out
+
+
+def bq_block_sparse_attention(runs, base_rows, q_i8, qi_bias, f_q, k_cache, k_scale, v_cache,
+                              v_scale, block_idx, *, num_q, num_kv, head_dim, kv_stride,
+                              block_size, topk, page_len, seq_len, cap) -> np.ndarray:
+    runs = np.ascontiguousarray(runs, dtype=np.int32)
+    rows = np.ascontiguousarray(base_rows, dtype=np.int32)
+    bi = np.ascontiguousarray(block_idx, dtype=np.int32)
+    out = np.zeros(seq_len * num_q * head_dim, dtype=np.uint16)
+    st = lib().ifo_bq_block_sparse_attention(
+        _p(runs), runs.shape[0], _p(rows), _p(q_i8), _p(qi_bias), _p(f_q), _p(k_cache),
+        _p(k_scale), _p(v_cache), _p(v_scale), _p(bi), _p(out), num_q, num_kv, head_dim,
+        kv_stride, block_size, topk, page_len, seq_len, cap)
+    if st != 0:
+        raise ValueError(f"oracle bq sparse attention rejected the arguments ({st})")
     return out
 
 

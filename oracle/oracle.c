@@ -1046,6 +1046,155 @@ int ifo_block_sparse_attention(const int32_t* runs, int64_t num_runs,
     return 0;
 }
 
+/* One (kv head h, slots [s0, s1)) pass of the bq block-sparse kernels over
+ * the head's gqa q heads, into acc (gqa x D) and m, l (gqa): tiles of each
+ * block in slot order through bq_process_kv_tile_head
+ * (prototypes/bq_sparse_attention.mojo:23-91, the bq branch of process_tile).
+ * A slot holding -1 ends the list (stop_at_neg) or is skipped. */
+static void bq_sparse_pass(attn_ctx* c, const int32_t* rows, const int8_t* q_i8,
+                           const float* qi_bias, const float* f_q, const int8_t* k_base,
+                           const float* k_scale, const int8_t* v_base,
+                           const float* v_scale, const int32_t* brow, int64_t t,
+                           int64_t h, int64_t num_q, int64_t s0, int64_t s1,
+                           int stop_at_neg, int64_t block_size, int64_t cap,
+                           float* m, float* l, float* acc) {
+    int64_t D = c->head_dim, gqa = c->gqa;
+    int64_t q_off[64];
+    for (int64_t r = 0; r < gqa; r++) {
+        m[r] = NEG_BIG;
+        l[r] = 0.0f;
+        q_off[r] = (t * num_q + h * gqa + r) * D;
+    }
+    memset(acc, 0, sizeof(float) * (size_t)(gqa * D));
+    c->qi = q_i8;
+    c->qi_bias = qi_bias + t * num_q + h * gqa;   /* indexed [0 * gqa + r] */
+    c->f_q = f_q + t * num_q + h * gqa;
+    c->ki = k_base + h * D;
+    c->vi = v_base + h * D;
+    c->k_scale = k_scale + h;                    /* indexed [slot * num_kv + 0] */
+    c->v_scale = v_scale + h;
+    attn_item it = {0, rows, 0, 0, 0, 0};
+    for (int64_t s = s0; s < s1; s++) {
+        int64_t b = brow[s];
+        if (b < 0) {
+            if (stop_at_neg) break;
+            continue;
+        }
+        int64_t plo = b * block_size;
+        int64_t phi = (b + 1) * block_size;
+        if (phi > cap) phi = cap;
+        for (int64_t pos = plo; pos < phi; pos += TILE) {
+            int64_t tl = phi - pos < TILE ? phi - pos : TILE;
+            process_tile(c, &it, q_off, pos, tl, m, l, acc);
+        }
+    }
+}
+
+/* dispatch_bq_block_sparse_attention (prototypes/bq_sparse_attention.mojo:
+ * 351-430) at degree 1.  seq_len > 1: BqBlockSparseFlashKernel (:94-186), one
+ * stripe per token over its blocks in order, finalized by
+ * PrefillMergeKernel.  seq_len == 1: BqBlockSparseFlashDecodeKernel
+ * (:216-310): the num_kv * min(topk, causal blocks) (kv head, slot) units are
+ * banded over min(cap, units) workers by worker_range (tile_dispatch,
+ * kernels/helpers.mojo:264-282, saturate_workers), each worker writing one
+ * stripe (untouched heads keep m = -1e30, l = 0), and the stripes merged per
+ * head by write_finalized_head (dispatch_merge_context_flash_partials,
+ * kernels/logsum_merge.mojo:251-292). */
+int ifo_bq_block_sparse_attention(const int32_t* runs, int64_t num_runs,
+                                  const int32_t* base_rows, const int8_t* q_i8,
+                                  const float* qi_bias, const float* f_q,
+                                  const int8_t* k_base, const float* k_scale,
+                                  const int8_t* v_base, const float* v_scale,
+                                  const int32_t* block_idx, uint16_t* out,
+                                  int64_t num_q, int64_t num_kv, int64_t head_dim,
+                                  int64_t kv_stride, int64_t block_size, int64_t topk,
+                                  int64_t page_len, int64_t seq_len, int64_t cap) {
+    if (num_q <= 0 || num_kv <= 0 || num_q % num_kv != 0 || num_q > 64) return -1;
+    if (head_dim % (2 * W) != 0 || head_dim > 512) return -1;
+    if (page_len <= 0 || (page_len & (page_len - 1)) != 0) return -1;
+    if (seq_len <= 0 || cap < 1) return seq_len <= 0 ? 0 : -1;
+    int64_t D = head_dim, gqa = num_q / num_kv;
+    int64_t stride = ifo_flash_partial_stride(num_q, D);
+    attn_ctx c;
+    memset(&c, 0, sizeof(c));
+    c.is_bq = 1;
+    c.num_q = gqa;
+    c.num_kv = num_kv;
+    c.gqa = gqa;
+    c.head_dim = D;
+    c.kv_stride = kv_stride;
+    c.shift = ifo_pow2_shift(page_len);
+    c.row_mask = page_len - 1;
+    c.page_mask = -1;
+    float* acc = (float*)malloc(sizeof(float) * (size_t)(gqa * D));
+    float m[64], l[64];
+    if (seq_len == 1) {
+        int64_t abs_pos = runs[1];
+        if (abs_pos < 0) {
+            free(acc);
+            return 0;
+        }
+        int64_t causal = abs_pos / block_size + 1;
+        int64_t pqb = topk < causal ? topk : causal;
+        int64_t total = num_kv * pqb;
+        int64_t workers = cap < total ? cap : total;
+        float* part = (float*)calloc((size_t)(workers * stride), sizeof(float));
+        const int32_t* rows = base_rows + runs[2];
+        for (int64_t w = 0; w < workers; w++) {
+            float* pw = part + w * stride;
+            for (int64_t gh = 0; gh < num_q; gh++) {
+                pw[num_q * D + gh] = NEG_BIG;
+                pw[num_q * D + num_q + gh] = 0.0f;
+            }
+            int64_t wr[2];
+            ifo_worker_range(total, workers, w, 0, wr);
+            if (wr[0] >= wr[1]) continue;
+            int64_t h0 = wr[0] / pqb, h1 = (wr[1] - 1) / pqb;
+            for (int64_t h = h0; h <= h1; h++) {
+                int64_t lo = (wr[0] > h * pqb ? wr[0] : h * pqb) - h * pqb;
+                int64_t hi = (wr[1] < (h + 1) * pqb ? wr[1] : (h + 1) * pqb) - h * pqb;
+                bq_sparse_pass(&c, rows, q_i8, qi_bias, f_q, k_base, k_scale, v_base,
+                               v_scale, block_idx + h * topk, 0, h, num_q, lo, hi, 0,
+                               block_size, abs_pos + 1, m, l, acc);
+                for (int64_t r = 0; r < gqa; r++) {
+                    int64_t gh = h * gqa + r;
+                    memcpy(pw + gh * D, acc + r * D, sizeof(float) * (size_t)D);
+                    pw[num_q * D + gh] = m[r];
+                    pw[num_q * D + num_q + gh] = l[r];
+                }
+            }
+        }
+        for (int64_t gh = 0; gh < num_q; gh++)
+            ifo_finalize_head(out + gh * D, part, stride, workers, num_q, D, gh);
+        free(part);
+        free(acc);
+        return 0;
+    }
+    float* part = (float*)calloc((size_t)stride, sizeof(float));
+    int64_t ri = 0;
+    for (int64_t t = 0; t < seq_len; t++) {
+        int64_t abs_pos = token_position(runs, num_runs, t, &ri);
+        if (abs_pos < 0) continue;
+        const int32_t* rows = base_rows + runs[4 * ri + 2];
+        for (int64_t h = 0; h < num_kv; h++) {
+            bq_sparse_pass(&c, rows, q_i8, qi_bias, f_q, k_base, k_scale, v_base, v_scale,
+                           block_idx + (t * num_kv + h) * topk, t, h, num_q, 0, topk, 1,
+                           block_size, abs_pos + 1, m, l, acc);
+            for (int64_t r = 0; r < gqa; r++) {
+                int64_t gh = h * gqa + r;
+                memcpy(part + gh * D, acc + r * D, sizeof(float) * (size_t)D);
+                part[num_q * D + gh] = m[r];
+                part[num_q * D + num_q + gh] = l[r];
+            }
+        }
+        for (int64_t gh = 0; gh < num_q; gh++)
+            ifo_finalize_head(out + (t * num_q + gh) * D, part, stride, 1, num_q, D, gh);
+    }
+    free(part);
+    free(acc);
+    return 0;
+}
+
 /* ------------------------------------------------------------------------ */
 /* KV append: RopeCacheWriteKernel (kernels/rope.mojo:16-125)                */
 /* ------------------------------------------------------------------------ */

@@ -127,6 +127,16 @@ int ifo_block_sparse_attention(const int32_t* runs, int64_t num_runs,
                                int64_t kv_stride, int64_t block_size, int64_t topk,
                                int64_t page_len, int64_t seq_len);
 
+int ifo_bq_block_sparse_attention(const int32_t* runs, int64_t num_runs,
+                                  const int32_t* base_rows, const int8_t* q_i8,
+                                  const float* qi_bias, const float* f_q,
+                                  const int8_t* k_base, const float* k_scale,
+                                  const int8_t* v_base, const float* v_scale,
+                                  const int32_t* block_idx, uint16_t* out,
+                                  int64_t num_q, int64_t num_kv, int64_t head_dim,
+                                  int64_t kv_stride, int64_t block_size, int64_t topk,
+                                  int64_t page_len, int64_t seq_len, int64_t cap);
+
 void ifo_gemm_cols(const uint16_t* x, const uint16_t* w, uint16_t* out,
                    int64_t rows, int64_t cols, int64_t seq_len);
 

@@ -196,3 +196,71 @@ def test_sparse_rejects_unsupported_shapes():
     scores = A.index_scores_buffer(plan, IH, BLOCK)
     with pytest.raises(InfernoHipError):
         A.dispatch_lightning_indexer(plan, q, kv, bi, scores, topk_blocks=33)
+
+
+def _bq_inputs(rng, n_tok, cache_rows):
+    q = rng.integers(-127, 128, n_tok * NUM_Q * HD).astype(np.int8)
+    qb = (q.reshape(-1, HD).astype(np.int64).sum(axis=1) * 128).astype(np.float32)
+    fq = rng.uniform(0.002, 0.02, n_tok * NUM_Q).astype(np.float32)
+    k = rng.integers(-127, 128, cache_rows * KV_STRIDE).astype(np.int8)
+    v = rng.integers(-127, 128, cache_rows * KV_STRIDE).astype(np.int8)
+    ks = rng.uniform(0.5, 4.0, cache_rows * NUM_KV).astype(np.float32)
+    vs = rng.uniform(0.5, 4.0, cache_rows * NUM_KV).astype(np.float32)
+    return q, qb, fq, k, ks, v, vs
+
+
+def _check_bq_sparse(plan, runs, rows, inputs, bi, page_len, cap):
+    q, qb, fq, k, ks, v, vs = inputs
+    seq = plan.seq_len
+    out = empty_dev(seq * NUM_Q * HD, np.uint16)
+    A.dispatch_bq_block_sparse_attention(plan, to_dev(q), to_dev(qb), to_dev(fq), to_dev(k),
+                                         to_dev(ks), to_dev(v), to_dev(vs), to_dev(bi), out,
+                                         cap=cap)
+    got = from_dev(out, np.uint16)
+    want = oracle.bq_block_sparse_attention(runs, rows, q, qb, fq, k, ks, v, vs, bi,
+                                            num_q=NUM_Q, num_kv=NUM_KV, head_dim=HD,
+                                            kv_stride=KV_STRIDE, block_size=BLOCK, topk=TOPK,
+                                            page_len=page_len, seq_len=seq, cap=cap)
+    r = compare_bf16(got, want)
+    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    return r
+
+
+@pytest.mark.parametrize("cap", [1, 7, 64])
+def test_bq_sparse_decode_worker_bands(cap):
+    """seq_len 1: the (kv head, slot) units banded over min(cap, units)
+    workers, selections from the GPU indexer plus a list with -1 holes."""
+    announce(f"bq sparse decode cap={cap}")
+    rng = np.random.default_rng(300 + cap)
+    page_len = 128
+    case = make_decode_case(31, [7000], page_len=page_len)
+    plan = _plan(case.runs, case.base_rows, 1, case.cache_rows, page_len)
+    index_q = _bf(rng.standard_normal(IH * HD))
+    index_k = _bf(rng.standard_normal(case.cache_rows * HD))
+    bi, _ = _run_indexer(plan, index_q, index_k)
+    bi[0, 2, 3] = -1
+    bi[0, 2, 9] = -1
+    inputs = _bq_inputs(rng, 1, case.cache_rows)
+    r = _check_bq_sparse(plan, case.runs, case.base_rows, inputs, bi, page_len, cap)
+    print(f"  bq sparse decode cap={cap}: {r}", flush=True)
+
+
+def test_bq_sparse_prefill_chunk():
+    """seq_len > 1: a 20-token chunk at positions 1000..1019, per-head lists
+    with an early -1, a repeated block and a block past the causal end."""
+    announce("bq sparse prefill chunk")
+    rng = np.random.default_rng(41)
+    page_len = 64
+    n_tok, base = 20, 1000
+    need = (base + n_tok + page_len - 1) // page_len
+    rows = rng.permutation(need + 2).astype(np.int32)[:need] * page_len
+    cache_rows = (need + 2) * page_len
+    runs = np.asarray([[0, base, 0, need]], dtype=np.int32)
+    plan = _plan(runs, rows, n_tok, cache_rows, page_len)
+    bi = np.full((n_tok, NUM_KV, TOPK), -1, np.int32)
+    for t in range(n_tok):
+        bi[t, 0, :3] = [7, 0, 3]
+        bi[t, 1, :2] = [7, 7]
+        bi[t, 2, :4] = [1, 2, -1, 5]
+        bi[t, 3, :3] = [9, 6, 7]
+    _check_bq_sparse(plan, runs, rows, _bq_inputs(rng, n_tok, cache_rows), bi, page_len, cap=8)

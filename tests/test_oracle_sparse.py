@@ -184,3 +184,111 @@ def test_sparse_equals_dense_when_every_block_is_selected():
                                  head_dim=HD, kv_stride=kv_stride, window=0, cache_size=64,
                                  page_len=64, seq_len=1, cap=1)
         assert np.array_equal(sparse, dense), p
+
+
+def _bq_case(rng, positions, num_q, num_kv, kv_stride, page_len=64):
+    D = HD
+    num_rows = (max(positions) // page_len + 2) * page_len
+    rows = rng.permutation(num_rows // page_len).astype(np.int32) * page_len
+    runs = _decode_runs(positions, len(rows))
+    q = rng.integers(-127, 128, len(positions) * num_q * D).astype(np.int8)
+    qb = (q.reshape(-1, D).astype(np.int64).sum(axis=1) * 128).astype(np.float32)
+    fq = rng.uniform(0.5, 2.0, len(positions) * num_q).astype(np.float32)
+    k = rng.integers(-127, 128, num_rows * kv_stride).astype(np.int8)
+    v = rng.integers(-127, 128, num_rows * kv_stride).astype(np.int8)
+    ks = rng.uniform(0.5, 4.0, num_rows * num_kv).astype(np.float32)
+    vs = rng.uniform(0.5, 4.0, num_rows * num_kv).astype(np.float32)
+    return runs, rows, q, qb, fq, k, ks, v, vs
+
+
+@pytest.mark.parametrize("cap,nb", [(1, 5), (32, 16)])
+def test_bq_sparse_decode_equals_dense_decode(cap, nb):
+    """Every block selected: with one worker (cap 1) the decode route is the
+    dense decode's single split; with 16 blocks and one (head, block) unit per
+    worker, each head's stripes are exactly the dense decode's 16 block-aligned
+    splits (16 = one merge batch), so the outputs are bit-equal."""
+    rng = np.random.default_rng(cap + nb)
+    num_q, num_kv, kv_stride = 16, 2, 1024
+    p = nb * BLOCK - 1
+    runs, rows, q, qb, fq, k, ks, v, vs = _bq_case(rng, [p], num_q, num_kv, kv_stride)
+    bi = np.full((1, num_kv, TOPK), -1, np.int32)
+    bi[0, :, :nb] = np.arange(nb)
+    sparse = oracle.bq_block_sparse_attention(runs, rows, q, qb, fq, k, ks, v, vs, bi,
+                                              num_q=num_q, num_kv=num_kv, head_dim=HD,
+                                              kv_stride=kv_stride, block_size=BLOCK, topk=TOPK,
+                                              page_len=64, seq_len=1, cap=cap)
+    dense_cap = 1 if cap == 1 else nb
+    assert oracle.recommended_workers((p + 1) * kv_stride, dense_cap) == dense_cap
+    dense = oracle.bq_attention(1, runs, rows, q, qb, fq, k, ks, v, vs, num_q=num_q,
+                                num_kv=num_kv, head_dim=HD, kv_stride=kv_stride, window=0,
+                                cache_size=64, page_len=64, seq_len=1, cap=dense_cap)
+    assert np.array_equal(sparse, dense)
+
+
+def test_bq_sparse_routes_q0_closed_form():
+    """q = 0 makes every score 0: each stripe weights its tiles by powers of
+    fexp(0) in walk order, so the output pins the decode route's worker bands
+    (cap 3 over 4 kv heads x 5 slots, -1 slots skipped) and the prefill route's
+    stop at -1."""
+    rng = np.random.default_rng(9)
+    num_q, num_kv = 64, 4
+    gqa, kv_stride = num_q // num_kv, num_kv * HD
+    c = float(oracle.fexp(np.zeros(1, np.float32))[0])
+    for positions in ([1000], [1000, 300]):
+        runs, rows, q, qb, fq, k, ks, v, vs = _bq_case(rng, positions, num_q, num_kv,
+                                                       kv_stride)
+        q[:] = 0
+        qb[:] = 0
+        bi = np.full((len(positions), num_kv, TOPK), -1, np.int32)
+        lists = [[7, 0, 3, -1, 5], [1, -1, 2, 2, 6], [7, 6, 5, 4, 3], [-1, -1, 0, 1, 2]]
+        for i in range(len(positions)):
+            for h in range(num_kv):
+                bi[i, h, :5] = lists[h]
+        seq = len(positions)
+        out = oracle.bq_block_sparse_attention(runs, rows, q, qb, fq, k, ks, v, vs, bi,
+                                               num_q=num_q, num_kv=num_kv, head_dim=HD,
+                                               kv_stride=kv_stride, block_size=BLOCK,
+                                               topk=TOPK, page_len=64, seq_len=seq, cap=3)
+        got = oracle.bf16_to_f32(out).astype(np.float64).reshape(seq, num_q, HD)
+        vf = v.astype(np.float64).reshape(-1, num_kv, HD)
+        vsf = vs.astype(np.float64).reshape(-1, num_kv)
+
+        def walk(tok, h, slots, stop):
+            tiles = []
+            for sidx in slots:
+                b = int(bi[tok, h, sidx])
+                if b < 0:
+                    if stop:
+                        break
+                    continue
+                lo, hi = b * BLOCK, min((b + 1) * BLOCK, positions[tok] + 1)
+                tiles += [list(range(s0, min(s0 + 16, hi))) for s0 in range(lo, hi, 16)]
+            n = len(tiles)
+            num, den = np.zeros(HD), 0.0
+            for j, tile in enumerate(tiles):
+                wgt = c ** (n - j)
+                sl = [rows[x // 64] + x % 64 for x in tile]
+                num += wgt * (vf[sl, h] * vsf[sl, h][:, None] / 127.0).sum(axis=0)
+                den += wgt * len(tile)
+            return num, den
+
+        for i, p in enumerate(positions):
+            for h in range(num_kv):
+                if seq == 1:
+                    slots_n = min(TOPK, p // BLOCK + 1)
+                    total, workers = num_kv * slots_n, min(3, num_kv * slots_n)
+                    per = -(-total // workers)
+                    num, den = np.zeros(HD), 0.0
+                    for w in range(workers):
+                        lo, hi = min(w * per, total), min(w * per + per, total)
+                        s_lo = max(lo, h * slots_n) - h * slots_n
+                        s_hi = min(hi, (h + 1) * slots_n) - h * slots_n
+                        if s_lo >= s_hi:
+                            continue
+                        a, d = walk(i, h, range(s_lo, s_hi), stop=False)
+                        num, den = num + c * a, den + c * d
+                else:
+                    num, den = walk(i, h, range(TOPK), stop=True)
+                want = num / den if den > 0 else np.zeros(HD)  # no tiles: zeros
+                for r in range(gqa):
+                    assert np.allclose(got[i, h * gqa + r], want, atol=1e-2, rtol=0), (seq, i, h)
