@@ -429,14 +429,27 @@ class SparseM3:
         kvs = self.NKV * self.HD
         self.index_k = torch.empty(rows * self.HD, dtype=torch.int16, device=dev)
         self.index_q = torch.empty(B * self.IH * self.HD, dtype=torch.int16, device=dev)
-        self.k = torch.empty(rows * kvs, dtype=torch.int16, device=dev)
+        self.kv = a.kv
+        elt = torch.int8 if self.kv == "bq" else torch.int16
+        self.k = torch.empty(rows * kvs, dtype=elt, device=dev)
         self.v = torch.empty_like(self.k)
-        self.q = torch.empty(B * self.NQ * self.HD, dtype=torch.int16, device=dev)
+        self.q = torch.empty(B * self.NQ * self.HD, dtype=elt, device=dev)
         _fill(self.index_k, self.seed * 16 + 1, sid)
         _fill(self.index_q, self.seed * 16 + 2, sid)
         _fill(self.k, self.seed * 16 + 3, sid)
         _fill(self.v, self.seed * 16 + 4, sid)
         _fill(self.q, self.seed * 16 + 5, sid, scale=float(1.0 / np.sqrt(self.HD)))
+        if self.kv == "bq":
+            # int8 codes (random bytes) with f32 scales, as ifr_bq_attn_prep lays them out.
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(self.seed)
+            self.ksc = torch.rand(rows * self.NKV, device=dev, generator=gen) * 4 + 0.5
+            self.vsc = torch.rand(rows * self.NKV, device=dev, generator=gen) * 4 + 0.5
+            self.qb = torch.zeros(B * self.NQ, dtype=torch.float32, device=dev)
+            self.fq = torch.full((B * self.NQ,), 0.01, dtype=torch.float32, device=dev)
+            self.dtype = "int8 KV (f32 scales); indexer bf16"
+            self.name = self.name.replace("sparse attention 64q/4kv hd128 bf16",
+                                          "bq int8 sparse attention 64q/4kv hd128")
         self.plan = AttentionPlan(table, B, kind=1, window=0, cache_size=P, page_len=P,
                                   cache_rows=rows, cap=16, kv_row_bytes=kvs * 2, device=dev)
         self.scores = A.index_scores_buffer(self.plan, self.IH, self.BLOCK, device=dev)
@@ -449,6 +462,10 @@ class SparseM3:
         if phase == "indexer":
             A.dispatch_lightning_indexer(p, self.index_q, self.index_k, self.block_idx,
                                          self.scores)
+        elif self.kv == "bq":
+            A.dispatch_bq_block_sparse_attention(p, self.q, self.qb, self.fq, self.k, self.ksc,
+                                                 self.v, self.vsc, self.block_idx, self.out,
+                                                 cap=128)
         else:
             A.dispatch_block_sparse_attention(p, self.q, self.k, self.v, self.block_idx,
                                               self.out)
@@ -468,8 +485,12 @@ class SparseM3:
 
     def step_bytes(self) -> int:
         B = len(self.pos)
-        attn = (self.attended() * self.NKV * self.HD * 2 * 2 + B * self.NQ * self.HD * 2 * 2
-                + B * self.IH * self.TOPK * 4)
+        if self.kv == "bq":  # int8 codes + two f32 scales per position and kv head
+            attn = (self.attended() * self.NKV * (self.HD * 2 + 8) + B * self.NQ * self.HD * 3
+                    + B * self.NQ * 8 + B * self.IH * self.TOPK * 4)
+        else:
+            attn = (self.attended() * self.NKV * self.HD * 2 * 2
+                    + B * self.NQ * self.HD * 2 * 2 + B * self.IH * self.TOPK * 4)
         return self.dominant_bytes() + attn
 
     def config(self) -> dict:
@@ -478,12 +499,15 @@ class SparseM3:
                 "attended_positions_per_kv_head": self.attended(), "pool_pages": self.pool,
                 "page_len": self.PLEN, "num_q": self.NQ, "num_kv": self.NKV,
                 "head_dim": self.HD, "index_heads": self.IH, "block": self.BLOCK,
-                "topk_blocks": self.TOPK, "seed": self.seed}
+                "topk_blocks": self.TOPK, "kv": self.kv, "seed": self.seed}
 
     def cpu_baseline(self, budget_s):
         """The oracle's indexer + sparse attention on the first sequences of the
-        batch, one thread."""
+        batch, one thread (bf16 KV)."""
         import torch
+
+        if self.kv == "bq":
+            return None
 
         import oracle
 
@@ -713,6 +737,8 @@ def main() -> None:
     ap.add_argument("--norm", choices=("none", "separate", "fused"), default="none",
                     help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
                          "own pass or fused into the append kernel")
+    ap.add_argument("--kv", choices=("bf16", "bq"), default="bf16",
+                    help="config 6: bf16 or butterquant int8 KV for the sparse attention")
     ap.add_argument("--oproj", action="store_true",
                     help="configs 1-3: the bf16 o_proj GEMM after the merge")
     ap.add_argument("--oquant", choices=("none", "separate", "fused"), default="none",

@@ -5,10 +5,10 @@
 // blocks.  The run table, page table and token->run map come from a
 // full-attention plan image (ifr_plan_attention).
 //
-// index_scores_kernel   one wave per (token, block): each lane takes one index
-//                       head and whole positions, and forms the dots in the
-//                       reference's VDPBF16PS order, so block scores, and with
-//                       them the selected blocks, are bit-identical.
+// index_scores_kernel   one wave per (token, block): each lane takes whole
+//                       positions and all index heads, and forms the dots in
+//                       the reference's VDPBF16PS order, so block scores, and
+//                       with them the selected blocks, are bit-identical.
 // select_blocks_kernel  one wave per (token, index head): the reference's
 //                       32-slot streaming bank, each reduction done as a rank
 //                       count under reduce_argmax's order (value, then slot
@@ -25,6 +25,12 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 struct TokenPos {
   int abs_pos;
@@ -49,13 +55,10 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ index_q,
     const uint16_t* __restrict__ index_k, float* __restrict__ scores, int block_stride,
     int block_size, float scale, int shift, int row_mask) {
-  static_assert(64 % H == 0, "heads must divide the wave");
-  constexpr int kP = D / 32;        // port-unroll accumulators, one strip
-  constexpr int kLanes = 64 / H;    // positions a pass
+  constexpr int kP = D / 32;  // port-unroll accumulators, one strip
+  __shared__ __align__(16) float qs[4][H * D];  // the token's queries, unpacked
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int head = lane / kLanes;   // lane = (head, position)
-  const int sub = lane % kLanes;
   const int t = blockIdx.y;
   const int b = blockIdx.x * 4 + wave;
   const TokenPos tp = token_position(image, t);
@@ -63,56 +66,70 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
   if (b >= nb) return;
   const int lo = b * block_size;
   const int hi = min(lo + block_size, tp.abs_pos + 1);
-
-  uint32_t qp[D / 2];  // this lane's head query, bf16 pairs
   {
-    const uint4* qr = reinterpret_cast<const uint4*>(
-        index_q + (static_cast<int64_t>(t) * H + head) * D);
-#pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
-      const uint4 v = qr[c];
-      qp[4 * c] = v.x;
-      qp[4 * c + 1] = v.y;
-      qp[4 * c + 2] = v.z;
-      qp[4 * c + 3] = v.w;
-    }
+    const uint16_t* qt = index_q + static_cast<int64_t>(t) * H * D;
+    for (int i = lane; i < H * D; i += 64) qs[wave][i] = bf16_to_f32(qt[i]);
   }
-  float best = kNegBig;
-  for (int pos = lo + sub; pos < hi; pos += kLanes) {
+  wave_sync();
+  float best[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) best[h] = kNegBig;
+  // A lane takes whole positions and all heads: the key's pairs are unpacked
+  // once, the queries are read from LDS (every lane the same address).
+  for (int p0 = lo; p0 < hi; p0 += 64) {
+    const int pos = p0 + lane;
+    if (pos >= hi) break;
     const int64_t slot = static_cast<int64_t>(tp.rows[pos >> shift]) + (pos & row_mask);
     const uint4* kr = reinterpret_cast<const uint4*>(index_k + slot * D);
-    float s[16];
+    uint4 kv[D / 8];
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) kv[c] = kr[c];
+    float s[H][16];
 #pragma unroll
     for (int p = 0; p < kP; ++p) {
-      uint32_t kp[16];
+      float klo[16], khi[16];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint4 v = kr[4 * p + c];
-        kp[4 * c] = v.x;
-        kp[4 * c + 1] = v.y;
-        kp[4 * c + 2] = v.z;
-        kp[4 * c + 3] = v.w;
+        const uint4 v = kv[4 * p + c];
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          klo[4 * c + e] = bf16_lo(w4[e]);
+          khi[4 * c + e] = bf16_hi(w4[e]);
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t q2 = qp[16 * p + j];
-        // bf16 products are exact in f32, so the fma rounds (odd + even) once.
-        const float odd = bf16_hi(kp[j]) * bf16_hi(q2);
-        const float a = fmaf(bf16_lo(kp[j]), bf16_lo(q2), odd);
-        s[j] = p == 0 ? a : s[j] + a;
+      for (int h = 0; h < H; ++h) {
+        const float4* qh = reinterpret_cast<const float4*>(&qs[wave][h * D + 32 * p]);
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+          const float4 q4 = qh[j / 2];  // even, odd of pair j, then of pair j+1
+          // bf16 products are exact in f32, so the fma rounds (odd + even) once.
+          const float a0 = fmaf(klo[j], q4.x, khi[j] * q4.y);
+          const float a1 = fmaf(klo[j + 1], q4.z, khi[j + 1] * q4.w);
+          s[h][j] = p == 0 ? a0 : s[h][j] + a0;
+          s[h][j + 1] = p == 0 ? a1 : s[h][j + 1] + a1;
+        }
       }
     }
 #pragma unroll
-    for (int w = 8; w >= 1; w >>= 1) {
+    for (int h = 0; h < H; ++h) {
 #pragma unroll
-      for (int j = 0; j < w; ++j) s[j] = s[j] + s[j + w];
+      for (int w = 8; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int jj = 0; jj < w; ++jj) s[h][jj] = s[h][jj] + s[h][jj + w];
+      }
+      const float sh = s[h][0] * scale;
+      best[h] = sh > best[h] ? sh : best[h];
     }
-    const float sh = s[0] * scale;
-    best = sh > best ? sh : best;
   }
 #pragma unroll
-  for (int msk = 1; msk < kLanes; msk <<= 1) best = fmaxf(best, shfl_xor_f32(best, msk));
-  if (sub == 0) scores[(static_cast<int64_t>(t) * H + head) * block_stride + b] = best;
+  for (int h = 0; h < H; ++h) {
+    float v = best[h];
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) v = fmaxf(v, shfl_xor_f32(v, msk));
+    if (lane == 0) scores[(static_cast<int64_t>(t) * H + h) * block_stride + b] = v;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -152,12 +169,27 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
   float v = kNegBig;
   int id = -1;
   int fill = 0;
+  // Scores stream through two 64-block register windows [base, base + 128),
+  // the next one loading while the bank works on the current.
+  int base = 0;
+  float win0 = lane < nb ? sr[lane] : kNegBig;
+  float win1 = 64 + lane < nb ? sr[64 + lane] : kNegBig;
   for (int b = 0; b < nb;) {
     const int n_new = min(cap - fill, nb - b);
-    if (lane >= fill && lane < fill + n_new) {
-      const int blk = b + lane - fill;
-      v = (blk >= local_start || blk < init_blocks) ? 1.0e30f : sr[blk];
-      id = blk;
+    {
+      const int blk = b + lane - fill;  // block this lane would take
+      const int rel = min(max(blk - base, 0), 127);
+      const float x0 = __shfl(win0, rel & 63);
+      const float x1 = __shfl(win1, rel & 63);
+      if (lane >= fill && lane < fill + n_new) {
+        v = (blk >= local_start || blk < init_blocks) ? 1.0e30f : (rel < 64 ? x0 : x1);
+        id = blk;
+      }
+    }
+    if (b + n_new - base >= 64) {
+      base += 64;
+      win0 = win1;
+      win1 = base + 64 + lane < nb ? sr[base + 64 + lane] : kNegBig;
     }
     fill += n_new;
     b += n_new;
@@ -261,12 +293,6 @@ struct TileRegs {
   uint4 k0, k1, k2, k3;  // keys: row r16, dims 32c + 8g .. +8
   uint4 v0, v1, v2, v3;  // values: rows g, g+4, g+8, g+12, 16 bytes at 16*r16
 };
-
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 __global__ __launch_bounds__(256) void sparse_attention_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
