@@ -134,28 +134,54 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
 
 // ---------------------------------------------------------------------------
 // stream_select_blocks (lightning_indexer.mojo:48-126) per (token, head) row.
-// Lane s < cap holds bank slot s.  reduce_top_k's successive argmax passes
+// Lane s < kCap holds bank slot s.  reduce_top_k's successive argmax passes
 // (matrixops.mojo:125-218) pick slots in one total order -- larger value,
-// then smaller lane s % 16, then smaller register s / 16 -- so a slot's
-// selection index is the number of slots ahead of it in that order.
+// then smaller lane s % 16, then smaller register s / 16 -- so a bitonic
+// sort of the bank under that order leaves the kept slots, in selection
+// order, in lanes 0..topk-1: exactly the refilled bank of the reference.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int bank_rank(float v, int slot, int cap) {
-  const int key = (slot & 15) * 64 + (slot >> 4);
-  int rank = 0;
-  for (int s2 = 0; s2 < cap; ++s2) {
-    const float v2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s2));
-    const int key2 = (s2 & 15) * 64 + (s2 >> 4);
-    rank += (v2 > v || (v2 == v && key2 < key)) ? 1 : 0;
+template <int kCap>
+__device__ __forceinline__ void bank_sort(float& v, int& id, int lane) {
+  int key = (lane & 15) * 64 + ((lane & (kCap - 1)) >> 4);  // slot order on ties
+#pragma unroll
+  for (int k = 2; k <= kCap; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const float v2 = shfl_xor_f32(v, j);
+      const int key2 = shfl_xor_i32(key, j);
+      const int id2 = shfl_xor_i32(id, j);
+      const bool other_first = v2 > v || (v2 == v && key2 < key);
+      const bool keep_first = ((lane & j) == 0) == ((lane & k) == 0);
+      if (keep_first ? other_first : !other_first) {
+        v = v2;
+        key = key2;
+        id = id2;
+      }
+    }
   }
-  return rank;
 }
 
+// Ascending sort of ids over kCap lanes (empty lanes carry INT_MAX).
+template <int kCap>
+__device__ __forceinline__ void id_sort(int& id, int lane) {
+#pragma unroll
+  for (int k = 2; k <= kCap; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int id2 = shfl_xor_i32(id, j);
+      const bool keep_low = ((lane & j) == 0) == ((lane & k) == 0);
+      id = keep_low ? min(id, id2) : max(id, id2);
+    }
+  }
+}
+
+constexpr int kFastChunks = 32;  // fast path: rows of up to 64 * 32 blocks
+
+template <int kCap>
 __global__ __launch_bounds__(256) void select_blocks_kernel(
     const int32_t* __restrict__ image, const float* __restrict__ scores,
     int32_t* __restrict__ block_idx, int block_stride, int num_heads, int block_size,
-    int topk, int local_blocks, int init_blocks, int cap, int num_rows) {
-  __shared__ float bank_v[4][64];
-  __shared__ int bank_b[4][64];
+    int topk, int local_blocks, int init_blocks, int num_rows) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
@@ -166,6 +192,62 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
   const float* sr = scores + static_cast<int64_t>(row) * block_stride;
   const int local_start = max(nb - local_blocks, 0);
 
+  int32_t* out = block_idx + static_cast<int64_t>(row) * topk;
+  // Short rows keep every block.
+  if (nb <= topk) {
+    if (lane < topk) out[lane] = lane < nb ? lane : -1;
+    return;
+  }
+  // Fast path.  If exactly topk scores are >= the topk-th largest score T,
+  // every bank reduction keeps them (at most topk - 1 entries can precede
+  // one of them) and the final pass returns them: the result is the set
+  // {score >= T} whatever the tie order.  T comes from a radix select over
+  // the scores held in registers (nb <= 2048); ties straddling T, or longer
+  // rows, take the bank below.
+  if (nb <= 64 * kFastChunks) {
+    float vals[kFastChunks];
+    uint32_t keys[kFastChunks];
+    const int n_chunks = (nb + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < kFastChunks; ++i) {
+      const int blk = 64 * i + lane;
+      float x = -INFINITY;
+      if (i < n_chunks && blk < nb)
+        x = (blk >= local_start || blk < init_blocks) ? 1.0e30f : sr[blk] + 0.0f;  // -0 -> +0
+      vals[i] = x;
+      const uint32_t u = __float_as_uint(x);
+      keys[i] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // order-preserving
+    }
+    uint32_t prefix = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = prefix | (1u << bit);
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < kFastChunks; ++i)
+        if (i < n_chunks) cnt += __popcll(__ballot(keys[i] >= cand));
+      if (cnt >= topk) prefix = cand;
+    }
+    const uint32_t tu = (prefix & 0x80000000u) ? (prefix & 0x7FFFFFFFu) : ~prefix;
+    const float thr = __uint_as_float(tu);
+    int cnt_ge = 0;
+#pragma unroll
+    for (int i = 0; i < kFastChunks; ++i)
+      if (i < n_chunks) cnt_ge += __popcll(__ballot(vals[i] >= thr));
+    if (cnt_ge == topk) {
+      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      int written = 0;
+#pragma unroll
+      for (int i = 0; i < kFastChunks; ++i) {
+        if (i >= n_chunks) break;
+        const bool sel = vals[i] >= thr;
+        const uint64_t mask = __ballot(sel);
+        if (sel) out[written + __popcll(mask & below)] = 64 * i + lane;
+        written += __popcll(mask);
+      }
+      return;
+    }
+  }
+
   float v = kNegBig;
   int id = -1;
   int fill = 0;
@@ -175,7 +257,7 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
   float win0 = lane < nb ? sr[lane] : kNegBig;
   float win1 = 64 + lane < nb ? sr[64 + lane] : kNegBig;
   for (int b = 0; b < nb;) {
-    const int n_new = min(cap - fill, nb - b);
+    const int n_new = min(kCap - fill, nb - b);
     {
       const int blk = b + lane - fill;  // block this lane would take
       const int rel = min(max(blk - base, 0), 127);
@@ -193,45 +275,21 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
     }
     fill += n_new;
     b += n_new;
-    if (fill == cap) {
-      // Keep the top `topk` slots, in selection order, in slots 0..topk-1.
-      const int rank = bank_rank(v, lane, cap);
-      bank_v[wave][lane] = kNegBig;
-      bank_b[wave][lane] = -1;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (lane < cap && rank < topk) {
-        bank_v[wave][rank] = v;
-        bank_b[wave][rank] = id;
+    if (fill == kCap) {
+      bank_sort<kCap>(v, id, lane);
+      if (lane >= topk) {
+        v = kNegBig;
+        id = -1;
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      v = bank_v[wave][lane];
-      id = bank_b[wave][lane];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       fill = topk;
     }
   }
-  const int rank = bank_rank(v, lane, cap);
-  const bool sel = lane < cap && rank < topk && v > kNegBig;
-  const uint64_t mask = __ballot(sel);
-  const int count = __popcll(mask);
-  int32_t* out = block_idx + static_cast<int64_t>(row) * topk;
-  if (sel) {
-    // Ids are distinct: the output slot is the number of selected ids below.
-    int below = 0;
-    for (int s2 = 0; s2 < cap; ++s2) {
-      const int id2 = __builtin_amdgcn_readlane(id, s2);
-      const bool sel2 = (mask >> s2) & 1ull;
-      below += (sel2 && id2 < id) ? 1 : 0;
-    }
-    out[below] = id;
-  }
-  if (lane >= count && lane < topk) out[lane] = -1;
+  bank_sort<kCap>(v, id, lane);
+  const bool sel = lane < kCap && lane < topk && v > kNegBig;
+  const int count = __popcll(__ballot(sel));
+  int sid = sel ? id : INT32_MAX;
+  id_sort<kCap>(sid, lane);
+  if (lane < topk) out[lane] = lane < count ? sid : -1;
 }
 
 // ---------------------------------------------------------------------------
@@ -746,9 +804,23 @@ hipError_t launch_lightning_indexer(const int32_t* image, int seq_len, const voi
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int rows = seq_len * num_heads;
-  hipLaunchKernelGGL(select_blocks_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, image,
-                     scores, block_idx, block_stride, num_heads, block_size, topk,
-                     local_blocks, init_blocks, select_bank_cap(topk), rows);
+  const int cap = select_bank_cap(topk);
+  dim3 sgrid((rows + 3) / 4);
+  if (cap == 16) {
+    hipLaunchKernelGGL(select_blocks_kernel<16>, sgrid, dim3(256), 0, stream, image, scores,
+                       block_idx, block_stride, num_heads, block_size, topk, local_blocks,
+                       init_blocks, rows);
+  } else if (cap == 32) {
+    hipLaunchKernelGGL(select_blocks_kernel<32>, sgrid, dim3(256), 0, stream, image, scores,
+                       block_idx, block_stride, num_heads, block_size, topk, local_blocks,
+                       init_blocks, rows);
+  } else if (cap == 64) {
+    hipLaunchKernelGGL(select_blocks_kernel<64>, sgrid, dim3(256), 0, stream, image, scores,
+                       block_idx, block_stride, num_heads, block_size, topk, local_blocks,
+                       init_blocks, rows);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

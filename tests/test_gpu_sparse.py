@@ -76,6 +76,20 @@ def test_indexer_random_decode_bit_exact(page_len):
         assert np.array_equal(got_sc[i, :, :nb], want_sc[i, :, :nb]), i
 
 
+def test_indexer_long_row_takes_the_bank():
+    """A context past 2048 blocks (270,000 positions) skips the radix-select
+    shortcut and runs the streaming bank on random scores."""
+    announce("indexer long row (bank path)")
+    rng = np.random.default_rng(5)
+    page_len = 128
+    case = make_decode_case(19, [270_000, 5], page_len=page_len)
+    index_q = _bf(rng.standard_normal(2 * IH * HD))
+    index_k = _bf(rng.standard_normal(case.cache_rows * HD))
+    got, _, _ = _check_indexer(case.runs, case.base_rows, index_q, index_k, case.cache_rows,
+                               page_len)
+    assert got[0, 0, -1] == 270_000 // BLOCK
+
+
 def test_indexer_reference_smoke_prefill():
     """prototypes/smoke_lightning_indexer.mojo: one run of 5000 tokens from
     position 0, identity 128-row pages, index_q = 0.01, index_k[g] = (5120 - g)
