@@ -1066,8 +1066,9 @@ int32_t ifr_block_sparse_attention(const void* image_dev, const int64_t* info, c
     return fail(IFR_EUNSUPPORTED, "sparse attention is compiled for head_dim 128, gqa 16");
   if (kv_stride < num_kv * head_dim || kv_stride % 8 != 0)
     return fail(IFR_EINVAL, "kv_stride must cover num_kv heads and keep 16-byte rows");
-  if (block_size <= 0 || block_size > (1 << 20))
-    return fail(IFR_EINVAL, "block_size must be in [1, 2^20]");
+  if (block_size <= 0 || block_size > (1 << 20) || block_size % 16 != 0)
+    return fail(IFR_EINVAL, "block_size must be a multiple of 16 in [16, 2^20]");
+  if (page_len < 16) return fail(IFR_EINVAL, "page_len must be at least 16");
   if (topk_blocks <= 0 || topk_blocks > (1 << 16)) return fail(IFR_EINVAL, "bad topk_blocks");
   if (!image_dev || !q || !k_base || !v_base || !block_idx || !output)
     return fail(IFR_EINVAL, "null pointer");
@@ -1127,8 +1128,9 @@ int32_t ifr_bq_block_sparse_attention(
     return fail(IFR_EUNSUPPORTED, "bq sparse attention is compiled for head_dim 128, gqa 16");
   if (kv_stride < num_kv * head_dim || kv_stride % 16 != 0)
     return fail(IFR_EINVAL, "kv_stride must cover num_kv heads in 16-byte rows");
-  if (block_size <= 0 || block_size > (1 << 20))
-    return fail(IFR_EINVAL, "block_size must be in [1, 2^20]");
+  if (block_size <= 0 || block_size > (1 << 20) || block_size % 16 != 0)
+    return fail(IFR_EINVAL, "block_size must be a multiple of 16 in [16, 2^20]");
+  if (page_len < 16) return fail(IFR_EINVAL, "page_len must be at least 16");
   if (topk_blocks <= 0 || topk_blocks > (1 << 16)) return fail(IFR_EINVAL, "bad topk_blocks");
   if (cap < 1 || cap > (1 << 20)) return fail(IFR_EINVAL, "cap must be in [1, 2^20]");
   if (!image_dev || !q_i8 || !qi_bias || !f_q || !k_base || !k_scale || !v_base || !v_scale ||

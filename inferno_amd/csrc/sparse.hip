@@ -32,15 +32,23 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A wave-uniform read of read-only data through the scalar cache.  A vector
+// load here would be counted with the K/V loads in flight, and waiting for
+// it would wait for all of them.
+__device__ __forceinline__ int32_t sload(const int32_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
 struct TokenPos {
   int abs_pos;
   const int32_t* rows;
 };
 
 __device__ __forceinline__ TokenPos token_position(const int32_t* image, int t) {
-  const int run = image[image[kHdrOffTokRun] + t];
-  const int32_t* rp = image + image[kHdrOffRuns] + run * 4;
-  return TokenPos{rp[1] + (t - rp[0]), image + image[kHdrOffRows] + rp[2]};
+  const int run = sload(image + sload(image + kHdrOffTokRun) + t);
+  const int32_t* rp = image + sload(image + kHdrOffRuns) + run * 4;
+  return TokenPos{sload(rp + 1) + (t - sload(rp)), image + sload(image + kHdrOffRows) + sload(rp + 2)};
 }
 
 // ---------------------------------------------------------------------------
@@ -57,7 +65,7 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
     int block_size, float scale, int shift, int row_mask) {
   constexpr int kP = D / 32;  // port-unroll accumulators, one strip
   __shared__ __align__(16) float qs[4][H * D];  // the token's queries, unpacked
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.y;
   const int b = blockIdx.x * 4 + wave;
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
     const int32_t* __restrict__ image, const float* __restrict__ scores,
     int32_t* __restrict__ block_idx, int block_stride, int num_heads, int block_size,
     int topk, int local_blocks, int init_blocks, int num_rows) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
   if (row >= num_rows) return;
@@ -306,7 +314,8 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
 // itself, so the accumulator C[dim][head] rescales lane-locally.  P enters as
 // bf16 hi + lo parts (about 16 significant bits per weight); pad positions
 // carry their fexp(-87) into l but a zero weight into P.V, as in the
-// reference.  The next tile's keys and values load while a tile computes.
+// reference.  The next two tiles' keys and values load while a tile
+// computes.
 // ---------------------------------------------------------------------------
 constexpr int kSD = 128;                // head_dim
 constexpr int kSG = 16;                 // q heads per kv head
@@ -335,7 +344,7 @@ __device__ __forceinline__ TileCursor next_tile(TileCursor c, const int32_t* bro
       c.valid = false;
       return c;
     }
-    const int b = brow[c.s];
+    const int b = sload(brow + c.s);
     if (b < 0) {
       c.valid = false;
       return c;
@@ -358,7 +367,7 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     const int32_t* __restrict__ block_idx, uint16_t* __restrict__ out, int64_t kv_stride,
     int num_q, int num_kv, int block_size, int topk, int shift, int row_mask, int num_rows) {
   __shared__ __align__(16) uint8_t vlds[4][2][kSVBytes];
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
   if (row >= num_rows) return;
@@ -387,19 +396,22 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
   // 4*(r16%4) .. +3 of a 16-dim block, and receives V[4g + k][16b + r16].
   const int tr_off = (4 * g + (r16 >> 2)) * kSVPitch + 8 * (r16 & 3);
 
+  // A tile never straddles a page (page_len >= 16, tiles 16-aligned), so its
+  // page row is one uniform (scalar) load, not a vector load the K/V loads
+  // would have to wait behind.
   auto load_tile = [&](const TileCursor& c) {
     TileRegs d;
     const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
-    const int pk = static_cast<int>(c.pos) + (r16 < tl ? r16 : 0);
-    const int64_t kslot = static_cast<int64_t>(tp.rows[pk >> shift]) + (pk & row_mask);
+    const int64_t prow = sload(tp.rows + static_cast<int>(c.pos >> shift));
+    const int off0 = static_cast<int>(c.pos) & row_mask;
+    const int64_t kslot = prow + off0 + (r16 < tl ? r16 : 0);
     const uint16_t* kp = kh + kslot * kv_stride + 8 * g;
     d.k0 = *reinterpret_cast<const uint4*>(kp);
     d.k1 = *reinterpret_cast<const uint4*>(kp + 32);
     d.k2 = *reinterpret_cast<const uint4*>(kp + 64);
     d.k3 = *reinterpret_cast<const uint4*>(kp + 96);
     auto vrow = [&](int rr) {
-      const int pv = static_cast<int>(c.pos) + (rr < tl ? rr : 0);
-      const int64_t vslot = static_cast<int64_t>(tp.rows[pv >> shift]) + (pv & row_mask);
+      const int64_t vslot = prow + off0 + (rr < tl ? rr : 0);
       return *reinterpret_cast<const uint4*>(
           reinterpret_cast<const uint8_t*>(vh + vslot * kv_stride) + vcol);
     };
@@ -416,12 +428,19 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
 #pragma unroll
   for (int b = 0; b < kSD / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // Three tiles in flight: the current one (rg), and the next two (r1, then
+  // r2, issued during the current tile).
+  auto advance = [&](const TileCursor& c) {
+    return c.valid ? next_tile(c, brow, topk, block_size, cap) : c;
+  };
   TileCursor cur = next_tile(TileCursor{-1, 0, 0, false}, brow, topk, block_size, cap);
-  TileRegs rg{};
+  TileCursor c1 = advance(cur);
+  TileRegs rg{}, r1{};
   if (cur.valid) rg = load_tile(cur);
+  if (c1.valid) r1 = load_tile(c1);
   int buf = 0;
   while (cur.valid) {
-    const TileCursor nxt = next_tile(cur, brow, topk, block_size, cap);
+    const TileCursor c2 = advance(c1);
     const int tl = static_cast<int>(min<int64_t>(kTile, cur.phi - cur.pos));
     uint8_t* vb = vlds[wave][buf];
     wave_sync();
@@ -429,8 +448,8 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     *reinterpret_cast<uint4*>(vb + (g + 4) * kSVPitch + vcol) = rg.v1;
     *reinterpret_cast<uint4*>(vb + (g + 8) * kSVPitch + vcol) = rg.v2;
     *reinterpret_cast<uint4*>(vb + (g + 12) * kSVPitch + vcol) = rg.v3;
-    TileRegs rn{};
-    if (nxt.valid) rn = load_tile(nxt);
+    TileRegs r2{};
+    if (c2.valid) r2 = load_tile(c2);
 
     f32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
     sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k0), qf[0], sc, 0, 0, 0);
@@ -484,8 +503,10 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
     }
-    rg = rn;
-    cur = nxt;
+    rg = r1;
+    r1 = r2;
+    cur = c1;
+    c1 = c2;
     buf ^= 1;
   }
 
@@ -524,9 +545,9 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 struct BqTileRegs {
-  uint4 k0, k1;  // keys: row r16, bytes 16g and 64 + 16g
-  uint2 v0, v1;  // values: row r16/4 and 4 + r16/4 ... (see load)
-  uint2 v2, v3;
+  uint4 k0, k1;          // keys: row r16, bytes 16g and 64 + 16g
+  uint2 v0, v1, v2, v3;  // values: 32 bytes of row l/4 at 32*(l%4)
+  float ks[4], vs[4];    // scales of positions 4g + j
 };
 
 template <bool kDecode>
@@ -540,7 +561,7 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
     int num_kv, int block_size, int topk, int decode_slots, int decode_workers, int shift,
     int row_mask, int num_rows) {
   __shared__ __align__(16) uint8_t vlds[4][2][kSVBytes];
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
   if (row >= num_rows) return;
@@ -589,21 +610,25 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
       block_idx + (kDecode ? static_cast<int64_t>(h) : static_cast<int64_t>(row)) * topk;
   const int tr_off = (4 * g + (r16 >> 2)) * kSVPitch + 8 * (r16 & 3);
 
-  auto slot_of = [&](int p) {
-    return static_cast<int64_t>(tp.rows[p >> shift]) + (p & row_mask);
-  };
   // V staging: lane takes 32 bytes (dims 32*(l%4) ..) of row l/4.
   const int vr_row = lane >> 2;
   const int vr_col = 32 * (lane & 3);
   auto load_tile = [&](const TileCursor& c) {
     BqTileRegs d;
     const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
-    const int pk = static_cast<int>(c.pos) + (r16 < tl ? r16 : 0);
-    const int8_t* kp = kh + slot_of(pk) * kv_stride + 16 * g;
+    const int64_t prow = sload(tp.rows + static_cast<int>(c.pos >> shift));  // uniform
+    const int off0 = static_cast<int>(c.pos) & row_mask;
+    const int64_t base = prow + off0;
+    const int8_t* kp = kh + (base + (r16 < tl ? r16 : 0)) * kv_stride + 16 * g;
     d.k0 = *reinterpret_cast<const uint4*>(kp);
     d.k1 = *reinterpret_cast<const uint4*>(kp + 64);
-    const int pv = static_cast<int>(c.pos) + (vr_row < tl ? vr_row : 0);
-    const int8_t* vp = vh + slot_of(pv) * kv_stride + vr_col;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t sl = (base + (4 * g + j < tl ? 4 * g + j : 0)) * num_kv + h;
+      d.ks[j] = k_scale[sl];
+      d.vs[j] = v_scale[sl];
+    }
+    const int8_t* vp = vh + (base + (vr_row < tl ? vr_row : 0)) * kv_stride + vr_col;
     d.v0 = *reinterpret_cast<const uint2*>(vp);
     d.v1 = *reinterpret_cast<const uint2*>(vp + 8);
     d.v2 = *reinterpret_cast<const uint2*>(vp + 16);
@@ -618,7 +643,7 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
         c.valid = false;
         return c;
       }
-      const int b = brow[c.s];
+      const int b = sload(brow + c.s);
       if (b < 0) {
         if (!kDecode) {
           c.valid = false;
@@ -641,12 +666,15 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
 #pragma unroll
   for (int b = 0; b < kSD / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  auto advance = [&](const TileCursor& c) { return c.valid ? next(c) : c; };
   TileCursor cur = next(TileCursor{s_lo - 1, 0, 0, false});
-  BqTileRegs rg{};
+  TileCursor c1 = advance(cur);
+  BqTileRegs rg{}, r1{};
   if (cur.valid) rg = load_tile(cur);
+  if (c1.valid) r1 = load_tile(c1);
   int buf = 0;
   while (cur.valid) {
-    const TileCursor nxt = next(cur);
+    const TileCursor c2 = advance(c1);
     const int tl = static_cast<int>(min<int64_t>(kTile, cur.phi - cur.pos));
     uint8_t* vb = vlds[wave][buf];
     wave_sync();
@@ -670,8 +698,8 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
         *reinterpret_cast<uint4*>(dst + 16 * i) =
             make_uint4(o16[4 * i], o16[4 * i + 1], o16[4 * i + 2], o16[4 * i + 3]);
     }
-    BqTileRegs rn{};
-    if (nxt.valid) rn = load_tile(nxt);
+    BqTileRegs r2{};
+    if (c2.valid) r2 = load_tile(c2);
 
     i32x4_t si = {0, 0, 0, 0};
     si = __builtin_amdgcn_mfma_i32_16x16x64_i8(
@@ -682,14 +710,11 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
     float sj[4], vsj[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int pj = static_cast<int>(cur.pos) + (4 * g + j < tl ? 4 * g + j : 0);
-      const int64_t sl = slot_of(pj) * num_kv + h;
-      const float ks = k_scale[sl];
-      vsj[j] = v_scale[sl];
+      vsj[j] = rg.vs[j];
       const float raw = static_cast<float>(si[j] + 128 * qsum);
       float sc = raw - qbias;
       sc = sc * fq;
-      sc = sc * ks;
+      sc = sc * rg.ks[j];
       sc = sc * inv127sq;
       sj[j] = (4 * g + j < tl) ? sc : kNegBig;
     }
@@ -738,8 +763,10 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
     }
-    rg = rn;
-    cur = nxt;
+    rg = r1;
+    r1 = r2;
+    cur = c1;
+    c1 = c2;
     buf ^= 1;
   }
 
