@@ -81,7 +81,7 @@ __device__ __forceinline__ uint2 load_kv(const uint2* p) {
   return make_uint2(v.x, v.y);
 }
 
-template <int D, int G>
+template <int D, int G, bool kTwoPages>
 __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
@@ -136,15 +136,31 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
   // tk and tk + 8) and V for all 16 positions (wave-uniform slots).
   uint4 kbuf[2][NCH];
   VT vbuf[kTile];
+  // kTwoPages (pages of >= 16 positions): a tile spans at most two pages,
+  // whose rows come from two scalar loads, so no K/V load waits behind a
+  // page-table vector load (vmcnt counts in order).
   auto load_tile = [&](int pos0) {
     const int tile_len = min(kTile, end - pos0);
+    const int p0 = start_pos + pos0;
+    const int pg0 = p0 >> shift;
+    int64_t ra = 0, rb = 0;
+    if constexpr (kTwoPages) {
+      const int pg1 = (p0 + tile_len - 1) >> shift;
+      ra = sload(rows + (pg0 & page_mask));
+      rb = pg1 != pg0 ? sload(rows + (pg1 & page_mask)) : ra;
+    }
+    auto slot_of = [&](int p) -> int64_t {
+      if constexpr (kTwoPages) {
+        return ((p >> shift) == pg0 ? ra : rb) + (p & row_mask);
+      } else {
+        return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+      }
+    };
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int t = 8 * b + tk;
       if (t < tile_len) {
-        const int p = start_pos + pos0 + t;
-        const int64_t slot =
-            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+        const int64_t slot = slot_of(p0 + t);
         const uint16_t* kr = kh + slot * kv_stride;
 #pragma unroll
         for (int i = 0; i < NCH; ++i)
@@ -157,9 +173,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
       if (t < tile_len) {
-        const int p = start_pos + pos0 + t;
-        const int64_t slot =
-            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+        const int64_t slot = slot_of(p0 + t);
         vbuf[t] = load_kv(reinterpret_cast<const VT*>(vh + slot * kv_stride));
       }
     }
@@ -526,12 +540,18 @@ hipError_t launch_partials(const int32_t* image, int num_items, const void* q,
                            int64_t ps, int num_q, int num_kv, int64_t kv_stride,
                            PagedGeom geom, hipStream_t stream) {
   dim3 grid(num_items, (num_kv + kDecodeWaves - 1) / kDecodeWaves);
-  hipLaunchKernelGGL((flash_partial_bf16_kernel<D, G>), grid, dim3(64 * kDecodeWaves), 0,
-                     stream, image, static_cast<const uint16_t*>(q),
-                     static_cast<const uint16_t*>(k),
-                     static_cast<const uint16_t*>(v), partials, ps, num_q,
-                     num_kv, kv_stride, geom.shift, geom.row_mask,
-                     geom.page_mask);
+  const auto* qp = static_cast<const uint16_t*>(q);
+  const auto* kp = static_cast<const uint16_t*>(k);
+  const auto* vp = static_cast<const uint16_t*>(v);
+  if (geom.row_mask + 1 >= kTile) {
+    hipLaunchKernelGGL((flash_partial_bf16_kernel<D, G, true>), grid,
+                       dim3(64 * kDecodeWaves), 0, stream, image, qp, kp, vp, partials, ps,
+                       num_q, num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
+  } else {
+    hipLaunchKernelGGL((flash_partial_bf16_kernel<D, G, false>), grid,
+                       dim3(64 * kDecodeWaves), 0, stream, image, qp, kp, vp, partials, ps,
+                       num_q, num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
+  }
   return hipGetLastError();
 }
 

@@ -127,4 +127,12 @@ __device__ __forceinline__ int uniform_i32(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
+// A wave-uniform read of read-only data through the scalar cache.  A vector
+// load would be counted with the K/V loads in flight (vmcnt is in order), and
+// waiting for it would wait for all of them.
+__device__ __forceinline__ int32_t sload(const int32_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
 }  // namespace ifr

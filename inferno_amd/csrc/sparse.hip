@@ -32,14 +32,6 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// A wave-uniform read of read-only data through the scalar cache.  A vector
-// load here would be counted with the K/V loads in flight, and waiting for
-// it would wait for all of them.
-__device__ __forceinline__ int32_t sload(const int32_t* p) {
-  return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
-      reinterpret_cast<uintptr_t>(p));
-}
-
 struct TokenPos {
   int abs_pos;
   const int32_t* rows;
