@@ -92,7 +92,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
   using V = VecOf<DPL>;
   using VT = typename V::T;
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.y * kDecodeWaves + wave;
   if (g >= num_kv) return;
@@ -156,27 +156,25 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
         return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
       }
     };
+    // Branch-free: a position past the tile reloads the tile's first row
+    // (its score is masked and its value skipped), so every load of the tile
+    // issues back to back.
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int t = 8 * b + tk;
-      if (t < tile_len) {
-        const int64_t slot = slot_of(p0 + t);
-        const uint16_t* kr = kh + slot * kv_stride;
+      const int64_t slot = slot_of(p0 + (t < tile_len ? t : 0));
+      const uint16_t* kr = kh + slot * kv_stride;
 #pragma unroll
-        for (int i = 0; i < NCH; ++i)
-          kbuf[b][i] = load_kv(reinterpret_cast<const uint4*>(kr + 64 * i));
-      } else {
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) kbuf[b][i] = make_uint4(0, 0, 0, 0);
-      }
+      for (int i = 0; i < NCH; ++i)
+        kbuf[b][i] = load_kv(reinterpret_cast<const uint4*>(kr + 64 * i));
     }
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      if (t < tile_len) {
-        const int64_t slot = slot_of(p0 + t);
-        vbuf[t] = load_kv(reinterpret_cast<const VT*>(vh + slot * kv_stride));
-      }
+      const int64_t slot = slot_of(p0 + (t < tile_len ? t : 0));
+      vbuf[t] = load_kv(reinterpret_cast<const VT*>(vh + slot * kv_stride));
     }
+    // Keep the V loads ahead of the score math: one memory round trip a tile.
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   for (int pos0 = start; pos0 < end; pos0 += kTile) {
