@@ -464,6 +464,51 @@ __global__ __launch_bounds__(256) void merge_sliced_kernel(
       inv_l = 1.0f / lv;
       acc = base[static_cast<int64_t>(h) * D + dim];
     }
+  } else if (n > 0 && n <= 64) {
+    // One chunk: every load of the unit (m and l of the lane's split, the
+    // lane's dim of all n splits) issues at once, then the same operations as
+    // below in the same order.
+    float mv = kNegBig, lv = 0.0f;
+    if (lane < n) {
+      const float* sp = base + static_cast<int64_t>(lane) * partial_stride;
+      mv = sp[m_off + h];
+      lv = sp[l_off + h];
+    }
+    float src[64];
+    const float* col = base + static_cast<int64_t>(h) * D + dim;
+#pragma unroll
+    for (int u = 0; u < 64; ++u)
+      src[u] = col[static_cast<int64_t>(min(u, n - 1)) * partial_stride];
+    float gm = mv;
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) gm = max_ref(gm, shfl_xor_f32(gm, msk));
+    gm = max_ref(kNegBig, gm);
+    const float delta = lane < n ? mv - gm : kNegBig;
+    float cv = fexp(max_ref(-87.0f, delta));
+    cv = lv > 0.0f ? cv : 0.0f;
+    float prod = lv * cv;
+    prod = prod + shfl_xor_f32(prod, 8);
+    prod = prod + shfl_xor_f32(prod, 4);
+    prod = prod + shfl_xor_f32(prod, 2);
+    prod = prod + shfl_xor_f32(prod, 1);
+    float gl = 0.0f;
+    for (int b = 0; b * 16 < n; ++b) gl = gl + readlane_f32(prod, 16 * b);
+    bool first = true;
+#pragma unroll
+    for (int u = 0; u < 64; ++u) {
+      const float cu = u < n ? readlane_f32(cv, u) : 0.0f;  // cv is 0 past n
+      if (cu <= 0.0f) continue;
+      if (first) {
+        acc = src[u] * cu;
+        first = false;
+      } else {
+        acc = fmaf(src[u], cu, acc);
+      }
+    }
+    if (gl > 0.0f) {
+      live = true;
+      inv_l = 1.0f / gl;
+    }
   } else {
     // Lanes own splits.  Global max: wave max per 64-split chunk (exact in any
     // order).  Corrections and L: the reference sums the splits in batches
