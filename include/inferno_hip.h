@@ -252,15 +252,15 @@ int32_t ifr_dispatch_gather_rows(const void* src, void* dst,
  * Both calls read a full-attention plan image of the step (kind 1,
  * ifr_plan_attention): its run table, page table and token->run map.
  *
- * dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-441):
- * block scores (IndexBlockScoreKernel :129-219: per token and index head, the
+ * dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-443):
+ * block scores (IndexBlockScoreKernel :129-209: per token and index head, the
  * max over each block's causal positions of scale * dot(index_q, index_k)),
- * then top-k block selection (IndexTopkMergeKernel :222-262 over
+ * then top-k block selection (IndexTopkMergeKernel :253-303 over
  * stream_select_blocks :48-126).  index_q [seq][4][128] bf16, index_k
  * [rows][128] bf16 paged like the plan, block_idx [seq][4][topk] int32
  * ascending with -1 padding, scores scratch of ifr_index_scores_bytes.
  * The reference's top-k pass takes positions from the first run only
- * (:244, a one-sequence prototype); here each token's run gives its
+ * (:420 and :278, a one-sequence prototype); here each token's run gives its
  * position, which is the same for one run. */
 int64_t ifr_index_scores_bytes(const int64_t* info, int64_t num_index_heads,
                                int64_t block_size);
@@ -271,8 +271,8 @@ int32_t ifr_lightning_indexer(const void* image_dev, const int64_t* info,
                               int64_t block_size, int64_t topk_blocks,
                               int64_t local_blocks, int64_t init_blocks, float scale,
                               int64_t page_len, uint64_t stream);
-/* dispatch_block_sparse_attention (prototypes/sparse_attention.mojo:164-199):
- * BlockSparseFlashKernel (:41-125) over each (token, kv head)'s block list in
+/* dispatch_block_sparse_attention (prototypes/sparse_attention.mojo:184-222):
+ * BlockSparseFlashKernel (:41-136) over each (token, kv head)'s block list in
  * order, then the one-stripe PrefillMergeKernel finalisation
  * (kernels/flash_attention_prefill.mojo:208-248).  head_dim 128, 16 q heads
  * per kv head; output [seq][num_q][128] bf16. */
@@ -284,10 +284,10 @@ int32_t ifr_block_sparse_attention(const void* image_dev, const int64_t* info,
                                    int64_t page_len, uint64_t stream);
 
 /* dispatch_bq_block_sparse_attention (prototypes/bq_sparse_attention.mojo:
- * 351-430): the int8 KV variant (codes and f32 scales as ifr_bq_attn_prep
+ * 366-451): the int8 KV variant (codes and f32 scales as ifr_bq_attn_prep
  * writes them, q codes with qi_bias and f_q).  seq_len > 1:
- * BqBlockSparseFlashKernel (:94-186) per (token, kv head), blocks in order,
- * -1 ends the list.  seq_len == 1: BqBlockSparseFlashDecodeKernel (:216-310):
+ * BqBlockSparseFlashKernel (:94-200) per (token, kv head), blocks in order,
+ * -1 ends the list.  seq_len == 1: BqBlockSparseFlashDecodeKernel (:254-364):
  * the num_kv * min(topk, causal blocks) (kv head, slot) units are banded over
  * min(cap, units) workers (cap: the reference's worker capacity, which fixes
  * the result as in ifr_plan_attention), -1 slots skipped, and the workers'

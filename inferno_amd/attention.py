@@ -240,8 +240,8 @@ def dispatch_lightning_indexer(plan: AttentionPlan, index_q, index_k, block_idx,
                                block_size: int = 128, topk_blocks: int = 16,
                                local_blocks: int = 1, init_blocks: int = 0,
                                scale: float | None = None) -> None:
-    """dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-441),
-    defaults of dispatch_minimax_m3_indexer (:456-477)."""
+    """dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-443),
+    defaults of dispatch_minimax_m3_indexer (:454-477)."""
     import numpy as np
 
     if scale is None:
@@ -256,8 +256,8 @@ def dispatch_block_sparse_attention(plan: AttentionPlan, q, k_base, v_base, bloc
                                     num_q: int = 64, num_kv: int = 4, head_dim: int = 128,
                                     kv_stride: int = 512, block_size: int = 128,
                                     topk_blocks: int = 16) -> None:
-    """dispatch_block_sparse_attention (prototypes/sparse_attention.mojo:164-199),
-    defaults of dispatch_minimax_m3_sparse_attention (:211-234)."""
+    """dispatch_block_sparse_attention (prototypes/sparse_attention.mojo:184-222),
+    defaults of dispatch_minimax_m3_sparse_attention (:231-253)."""
     check(lib().ifr_block_sparse_attention(
         _ptr(plan.image), plan.info_ptr, _ptr(q), _ptr(k_base), _ptr(v_base), _ptr(block_idx),
         _ptr(output), num_q, num_kv, head_dim, kv_stride, block_size, topk_blocks,
@@ -271,7 +271,7 @@ def dispatch_bq_block_sparse_attention(plan: AttentionPlan, q_i8, qi_bias, f_q, 
                                        block_size: int = 128, topk_blocks: int = 16,
                                        partials=None) -> None:
     """dispatch_bq_block_sparse_attention (prototypes/bq_sparse_attention.mojo:
-    351-430), defaults of dispatch_bq_minimax_m3_sparse_attention (:443-486).
+    366-451), defaults of dispatch_bq_minimax_m3_sparse_attention (:460-486).
     `cap` is the reference's worker capacity (it bands a decode step's blocks)."""
     import torch
 

@@ -44,7 +44,7 @@ __device__ __forceinline__ TokenPos token_position(const int32_t* image, int t) 
 }
 
 // ---------------------------------------------------------------------------
-// IndexBlockScoreKernel (lightning_indexer.mojo:134-202).  Dots of the index
+// IndexBlockScoreKernel (lightning_indexer.mojo:146-204).  Dots of the index
 // key with each head's query follow bf16_panel_dot_to_scalars with
 // port_unroll = D/32 (one strip of D): accumulator (p, j) takes the pair
 // (32p + 2j + 1, 32p + 2j) as odd*odd + even*even, lane j sums its
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// BlockSparseFlashKernel (sparse_attention.mojo:58-125) + the one-stripe
+// BlockSparseFlashKernel (sparse_attention.mojo:59-131) + the one-stripe
 // write_finalized_head of PrefillMergeKernel (flash_attention_prefill.mojo:
 // 221-240), for head_dim 128 and 16 q heads per kv head.
 //
@@ -522,10 +522,10 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// bq_process_kv_tile_head (prototypes/bq_sparse_attention.mojo:23-91) inside
-// BqBlockSparseFlashKernel (:94-186, one (token, kv head) per wave, blocks in
+// bq_process_kv_tile_head (prototypes/bq_sparse_attention.mojo:29-91) inside
+// BqBlockSparseFlashKernel (:94-200, one (token, kv head) per wave, blocks in
 // order, -1 ends the list, one-stripe finalisation) and
-// BqBlockSparseFlashDecodeKernel (:216-310, one (worker, kv head) per wave over
+// BqBlockSparseFlashDecodeKernel (:254-364, one (worker, kv head) per wave over
 // the worker's band of block slots, -1 skipped, a partial stripe per worker).
 //
 // Scores: raw = sum (k ^ 0x80) * q over u8 x i8 equals sum k*q + 128 * sum q,

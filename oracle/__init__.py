@@ -214,7 +214,7 @@ def absmax_quantize(x) -> tuple[np.ndarray, float, int]:
 
 def index_block_stride(runs, seq_len: int, block_size: int) -> int:
     """Blocks per (token, head) score row: the largest position's block count,
-    rounded up to 16 (lightning_indexer.mojo:424-426 for one run)."""
+    rounded up to 16 (lightning_indexer.mojo:420-422 for one run)."""
     runs = np.asarray(runs, dtype=np.int64).reshape(-1, 4)
     last = 0
     for i, r in enumerate(runs):

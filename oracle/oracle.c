@@ -813,14 +813,14 @@ int ifo_bq_attention(int64_t kind, const int32_t* runs, int64_t num_runs,
 /* ------------------------------------------------------------------------ */
 
 /* The run a token belongs to, advancing `ri` as the reference's kernels do
- * (prototypes/lightning_indexer.mojo:158-163); returns the absolute position. */
+ * (prototypes/lightning_indexer.mojo:161-169); returns the absolute position. */
 static int64_t token_position(const int32_t* runs, int64_t num_runs, int64_t t,
                               int64_t* ri) {
     while (*ri + 1 < num_runs && t >= runs[4 * (*ri + 1)]) (*ri)++;
     return (int64_t)runs[4 * *ri + 1] + (t - runs[4 * *ri]);
 }
 
-/* IndexBlockScoreKernel.execute (prototypes/lightning_indexer.mojo:134-202):
+/* IndexBlockScoreKernel.execute (prototypes/lightning_indexer.mojo:146-204):
  * per token, each causal position's index key is scored against every index
  * head's query (bf16_panel_dot_to_scalars, port unroll
  * pick_port_unroll(32, head_dim)), scaled, and max-folded (strict >) into its
@@ -944,10 +944,10 @@ void ifo_select_blocks(const float* row_scores, int64_t num_blocks, int64_t topk
     for (int64_t s = 0; s < topk; s++) out_row[s] = ids[s];
 }
 
-/* dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-441) at
- * degree 1: block scores, then IndexTopkMergeKernel (:222-262) per (token,
+/* dispatch_lightning_indexer (prototypes/lightning_indexer.mojo:399-443) at
+ * degree 1: block scores, then IndexTopkMergeKernel (:253-303) per (token,
  * head) row.  The reference's merge takes every token's position from the
- * first run (base_pos + t, :244, a one-sequence prototype); here each token's
+ * first run (base_pos + t, :420 and :278, a one-sequence prototype); here each token's
  * own run gives it, which is the same for one run. */
 void ifo_lightning_indexer(const int32_t* runs, int64_t num_runs,
                            const int32_t* base_rows, const uint16_t* index_q,
@@ -971,7 +971,7 @@ void ifo_lightning_indexer(const int32_t* runs, int64_t num_runs,
     }
 }
 
-/* BlockSparseFlashKernel.execute (prototypes/sparse_attention.mojo:58-125) at
+/* BlockSparseFlashKernel.execute (prototypes/sparse_attention.mojo:59-131) at
  * degree 1: per token and kv head, the selected blocks in order (stopping at
  * the first -1), each clipped to the causal count and walked in 16-position
  * process_kv_tile steps from its first position over the head's gqa q heads;
@@ -1049,7 +1049,7 @@ int ifo_block_sparse_attention(const int32_t* runs, int64_t num_runs,
 /* One (kv head h, slots [s0, s1)) pass of the bq block-sparse kernels over
  * the head's gqa q heads, into acc (gqa x D) and m, l (gqa): tiles of each
  * block in slot order through bq_process_kv_tile_head
- * (prototypes/bq_sparse_attention.mojo:23-91, the bq branch of process_tile).
+ * (prototypes/bq_sparse_attention.mojo:29-91, the bq branch of process_tile).
  * A slot holding -1 ends the list (stop_at_neg) or is skipped. */
 static void bq_sparse_pass(attn_ctx* c, const int32_t* rows, const int8_t* q_i8,
                            const float* qi_bias, const float* f_q, const int8_t* k_base,
@@ -1091,10 +1091,10 @@ static void bq_sparse_pass(attn_ctx* c, const int32_t* rows, const int8_t* q_i8,
 }
 
 /* dispatch_bq_block_sparse_attention (prototypes/bq_sparse_attention.mojo:
- * 351-430) at degree 1.  seq_len > 1: BqBlockSparseFlashKernel (:94-186), one
+ * 366-451) at degree 1.  seq_len > 1: BqBlockSparseFlashKernel (:94-200), one
  * stripe per token over its blocks in order, finalized by
  * PrefillMergeKernel.  seq_len == 1: BqBlockSparseFlashDecodeKernel
- * (:216-310): the num_kv * min(topk, causal blocks) (kv head, slot) units are
+ * (:254-364): the num_kv * min(topk, causal blocks) (kv head, slot) units are
  * banded over min(cap, units) workers by worker_range (tile_dispatch,
  * kernels/helpers.mojo:264-282, saturate_workers), each worker writing one
  * stripe (untouched heads keep m = -1e30, l = 0), and the stripes merged per
