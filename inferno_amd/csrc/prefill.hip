@@ -7,15 +7,19 @@
 // Because all queries start at key 0 the tiles line up across queries, so a
 // block of query tokens shares every K/V tile of its kv head.
 //
-// A row is one (query token, q head); a wave owns 16 rows = 8 tokens x the
-// 2 q heads of one kv head; a block of 8 waves owns 64 tokens.  Each
-// iteration stages 64 keys (4 tiles) in LDS and computes, per wave:
+// A row is one (query token, q head); a wave owns 32 rows = 16 tokens x the
+// 2 q heads of one kv head; a block of 4 waves (one per SIMD) owns 64
+// tokens.  Each iteration stages 64 keys (4 tiles) in LDS and computes, per
+// wave:
 //
-//   S^T (16 keys x 16 rows) = K_tile . Q^T, per tile     v_mfma_f32_16x16x32_bf16
-//   O^T (16 dims x 16 rows) += V^T . P'^T, 32 keys/MFMA  v_mfma_f32_16x16x32_bf16
+//   S^T (32 keys x 32 rows) = K . Q^T, per pair of tiles     v_mfma_f32_32x32x16_bf16
+//   O^T (32 dims x 32 rows) += V^T . P'^T, 16 keys/MFMA       v_mfma_f32_32x32x16_bf16
 //
-// In the MFMA C layout lane l holds keys 4*(l/16)..+3 of row l%16, and O^T
-// keeps row l%16 in lane l, so the per-row softmax state stays lane-local.
+// In the 32x32 C layout lane l holds row l%32 and keys 8j + 4*(l/32) + i
+// (j, i < 4) of a 32-key block, so a 16-key tile is 8 keys in lane l and 8 in
+// lane l^32: the per-row softmax state stays in the lane pair.  Each K / V
+// fragment read from LDS feeds 32 rows (the transposing V reads are the
+// costliest LDS operation on gfx950).
 // The reference's per-tile steps are kept in tile order: a row skips tiles
 // past its position (the reference never visits them), pads of its last
 // tile score -1e30 (their fexp(-87) enters l, not PV), and m, corr, w use
@@ -23,14 +27,20 @@
 // a pair of tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 equals the
 // reference's nested (acc*c0 + w0 V0)*c1 + w1 V1 up to f32 rounding, and
 // the product of the rescales is carried as a per-row scale S (acc =
-// acc_stored * S) that divides the weights instead of multiplying the 64
+// acc_stored * S) that divides the weights instead of multiplying the 128
 // accumulators.  P' enters the bf16 MFMA as hi + lo bf16 parts (~16
-// significant bits per weight); QK^T products are exact in f32.
+// significant bits per weight); QK^T products are exact in f32.  The biased
+// exp is evaluated with fused multiply-adds (fexp_fused): its value differs
+// from the reference's separately rounded steps by about 2e-5 relative,
+// far inside the bf16 output tolerance, and it saves a third of the
+// softmax's VALU work, which bounds this kernel together with the MFMAs.
 //
-// K and V tiles are staged row-major in LDS; V^T operands come from
-// ds_read_b64_tr_b16 (a 16-lane transposing read).  The next iteration's
-// keys are loaded into registers while the current one is computed; the
-// run's page table is staged in LDS first.
+// K and V reach LDS straight from global memory (global_load_lds_dwordx4,
+// no registers) one iteration ahead.  K rows are stored XOR-swizzled (16-byte
+// chunk c of key k at position c ^ (k & 15)) so the 16 keys a QK operand read
+// touches fall in distinct banks; V rows are stored plainly and read with
+// ds_read_b64_tr_b16 (a 16-lane transposing read).  The run's page table is
+// staged in LDS first.
 // Blocks are numbered kv-head-fastest so every block of a kv head lands on
 // one XCD (block id mod 8) and shares that XCD's L2.
 #include "common.hpp"
@@ -41,79 +51,87 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef short s16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPD = 256;             // head_dim
-constexpr int kPWaves = 8;           // waves per block (one block per CU)
-constexpr int kPTokensPerWave = 8;   // x 2 q heads = 16 rows
+constexpr int kPWaves = 4;           // waves per block (one per SIMD, one block per CU)
+constexpr int kPThreads = 64 * kPWaves;
+constexpr int kPTokensPerWave = 16;  // x 2 q heads = 32 rows
 constexpr int kPTokens = kPWaves * kPTokensPerWave;  // tokens per block
 static_assert(kPTokens == kPrefillTokens, "plan query blocks must match the kernel");
 constexpr int kKeys = 64;                // keys per iteration
-constexpr int kTiles = kKeys / 16;       // 16-key tiles per iteration
-constexpr int kHalves = kTiles / 2;      // 32-key MFMA operands per iteration
-static_assert(kTiles % 2 == 0, "tiles pair up into 32-key MFMA operands");
-constexpr int kKPitch = kPD * 2 + 16;    // bytes per K row in LDS: 132 dwords
-constexpr int kVPitch = kPD * 2 + 32;    // bytes per V row in LDS: 136 dwords
-constexpr int kKBytes = kKeys * kKPitch;
-constexpr int kVBytes = kKeys * kVPitch;
-constexpr int kBufBytes = kKBytes + kVBytes;
-constexpr int kChunksPerThread = kKeys * kPD * 2 / 16 / (64 * kPWaves);  // of K and of V
-static_assert(kChunksPerThread == 4, "staging layout");
-constexpr int kKeyStep = kKeys / kChunksPerThread;  // keys between a thread's chunks
+constexpr int kBlocks = kKeys / 32;      // 32-key S blocks (tile pairs) per iteration
+constexpr int kDimBlocks = kPD / 32;     // 32-dim blocks of O^T
+constexpr int kRowBytes = kPD * 2;       // one key row of K or V in LDS
+constexpr int kTileBytes = kKeys * kRowBytes;  // 32 KiB: one iteration of K (or V)
+constexpr int kStageRows = kKeys / kPWaves;  // key rows each wave stages per iteration
+static_assert(kStageRows % 2 == 0, "two rows per 64-lane load");
+static_assert(4 * kTileBytes + 4 * kPrefillLdsPages <= 160 * 1024, "LDS budget");
 
-static_assert(kKeyStep * 32 == 64 * kPWaves, "32 lanes per key row");
-
-// x + x[lane ^ 16] and x + x[lane ^ 32] through the gfx950 lane swaps: with
-// both operands x, the two results hold the low and high member of each
-// pair, so their sum (low + high) is the same in both lanes.
-__device__ __forceinline__ float sum_xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
-                                                  false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
+// x + x[lane ^ 32] and max(x, x[lane ^ 32]) through the gfx950 lane swap:
+// with both operands x, the two results hold the low and high member of
+// each pair, so their sum (low + high) is the same in both lanes.
 __device__ __forceinline__ float sum_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
                                                   false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-__device__ __forceinline__ float max_xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
-                                                  false, false);
-  return max_ref(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
 __device__ __forceinline__ float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
                                                   false, false);
-  return max_ref(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// The reference's biased exp (the steps of fexp) with fused multiply-adds.
+// The argument arrives pre-scaled: t = a_magic * x + bias_f, clamped below
+// at x = -87 by the caller.
+constexpr float kExpA = 12102203.16156148f;
+constexpr float kExpBias = 1059208216.0f;
+__device__ __forceinline__ float fexp_fused_t(float t) {
+  const int32_t i = static_cast<int32_t>(t);
+  const float f = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u) - 1.0f;
+  float p = __builtin_fmaf(f, 0.38696467876434326f, -0.37554836273193359f);
+  p = __builtin_fmaf(f, p, 1.6501418352127075f);
+  return __int_as_float(i) * p;
+}
+__device__ __forceinline__ float fexp_fused(float x) {
+  return fexp_fused_t(__builtin_fmaf(kExpA, fmaxf(x, -87.0f), kExpBias));
 }
 
 // One tile's online-softmax step for this lane's row (process_kv_tile's
-// m / corr / w / l updates, attention_ops.mojo:165-180).  Masked: the tile
-// reaches past some row's last key (or the row is empty); a row with no key
-// in the tile is left untouched (corr 1, weights 0), pads score -1e30 and
-// enter l only.  The in-lane sum of the 4 weights comes first, then the
-// lanes ^16 and ^32 (the same 16 weights as the reference's halving tree,
-// added in another order).
+// m / corr / w / l updates, attention_ops.mojo:165-180).  sv[0..7] are the
+// lane's 8 keys of the tile, key 8*(i/4) + 4*half + i%4 for value i.
+// Masked: the tile reaches past some row's last key (or the row is empty);
+// a row with no key in the tile is left untouched (corr 1, weights 0), pads
+// score -1e30 and enter l only.  The in-lane sum of the 8 weights comes
+// first, then lane ^32's (the same 16 weights as the reference's halving
+// tree, added in another order).  Maxima use v_max_f32 (the scores are
+// finite for finite inputs).
 template <bool kMasked>
-__device__ __forceinline__ void softmax_tile(const f32x4_t s, int valid, int key0, float& m,
-                                             float& l, float& corr, float (&w)[4]) {
-  float sc[4];
+__device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, int half,
+                                             float& m, float& l, float& corr, float (&w)[8]) {
+  float sc[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sc[j] = (!kMasked || key0 + j < valid) ? s[j] : kNegBig;
-  float mx = max_ref(max_ref(sc[0], sc[1]), max_ref(sc[2], sc[3]));
-  mx = max_xor16(mx);
+  for (int i = 0; i < 8; ++i) {
+    const int key = 8 * (i >> 2) + 4 * half + (i & 3);
+    sc[i] = (!kMasked || key < valid) ? sv[i] : kNegBig;
+  }
+  float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                   fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
   mx = max_xor32(mx);
-  const float m_new = mx > m ? mx : m;
-  const float c = fexp(max_ref(-87.0f, m - m_new));
-  float e[4];
+  const float m_new = fmaxf(mx, m);
+  const float c = fexp_fused(m - m_new);
+  // a*(s - m_new) + bias as one fma per key, clamped at s - m_new = -87.
+  const float t0 = __builtin_fmaf(-kExpA, m_new, kExpBias);
+  const float t_min = __builtin_fmaf(kExpA, -87.0f, kExpBias);
+  float e[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) e[j] = fexp(max_ref(-87.0f, sc[j] - m_new));
-  float ts = (e[0] + e[1]) + (e[2] + e[3]);
-  ts = sum_xor16(ts);
+  for (int i = 0; i < 8; ++i) e[i] = fexp_fused_t(fmaxf(__builtin_fmaf(kExpA, sc[i], t0), t_min));
+  float ts = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
   ts = sum_xor32(ts);
   if (kMasked) {
     const bool any = valid > 0;
@@ -121,29 +139,39 @@ __device__ __forceinline__ void softmax_tile(const f32x4_t s, int valid, int key
     m = any ? m_new : m;
     corr = any ? c : 1.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = key0 + j < valid ? e[j] : 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      const int key = 8 * (i >> 2) + 4 * half + (i & 3);
+      w[i] = key < valid ? e[i] : 0.0f;
+    }
   } else {
     l = l * c + ts;
     m = m_new;
     corr = c;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = e[j];
+    for (int i = 0; i < 8; ++i) w[i] = e[i];
   }
 }
 
-// Two waves per SIMD (<= 256 VGPR + AGPR per lane); one block per CU.
-__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2)))
+// One wave per SIMD (up to 512 VGPR + AGPR per lane); one block per CU.
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_full_mfma_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride,
     int shift, int row_mask) {
-  __shared__ __align__(16) uint8_t lds[2 * kBufBytes];
+  // Two K and two V buffers as separate LDS objects: the LDS reads of one
+  // buffer then provably do not alias the loads landing in the other, and
+  // no wait for those loads is inserted before the reads.
+  __shared__ __align__(16) uint8_t kbuf0[kTileBytes];
+  __shared__ __align__(16) uint8_t kbuf1[kTileBytes];
+  __shared__ __align__(16) uint8_t vbuf0[kTileBytes];
+  __shared__ __align__(16) uint8_t vbuf1[kTileBytes];
   __shared__ int32_t page_rows[kPrefillLdsPages];
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int grp = lane >> 4;   // key group within a tile / k group of the MFMA
+  const int half = lane >> 5;  // key half of the C layout / k half of the operands
+  const int row = lane & 31;
   const int g = blockIdx.x % num_kv;
   const int qb = blockIdx.x / num_kv;
 
@@ -160,8 +188,7 @@ void prefill_full_mfma_kernel(
   const int count_max = base_pos + (t0 + ntok - 1 - buf_start) + 1;
   const int n_iters = (count_max + kKeys - 1) / kKeys;
 
-  // This lane's row: token wave*8 + (l%16)/2, q head 2g + (l%16)%2.
-  const int row = lane & 15;
+  // This lane's row: token wave*16 + (l%32)/2, q head 2g + (l%32)%2.
   const int tok_local = wave * kPTokensPerWave + (row >> 1);
   const int head = g * 2 + (row & 1);
   const bool row_live = tok_local < ntok;
@@ -176,211 +203,284 @@ void prefill_full_mfma_kernel(
                            ? base_pos + (t0 + wave_first - buf_start) + 1
                            : 0;
 
-  // Q^T fragments: lane holds Q[row][32c + 8*(l/16) .. +7] for chunks c.
-  bf16x8_t qf[8];
+  // Q^T fragments: lane holds Q[row][16*d + 8*half .. +7] for 16-dim steps d.
+  bf16x8_t qf[kPD / 16];
   {
     const uint16_t* qr =
-        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * grp;
+        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * half;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * c);
-      qf[c] = __builtin_bit_cast(bf16x8_t, v);
+    for (int d = 0; d < kPD / 16; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
+      qf[d] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
 
   // The O^T accumulator is kept as acc_stored with acc = acc_stored * S: a
   // tile's rescale multiplies S, and the weights entering the MFMA are
-  // divided by the new S, so the 64 accumulators are not rescaled per
+  // divided by the new S, so the 128 accumulators are not rescaled per
   // iteration.  When S would fall below 2^-64 the accumulators take it over
   // (acc_stored *= S, S = 1) for the whole wave.
-  f32x4_t acc[16];
+  f32x16_t acc[kDimBlocks];
 #pragma unroll
-  for (int b = 0; b < 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b = 0; b < kDimBlocks; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
   float m = kNegBig, l = 0.0f, S = 1.0f;
 
   // The run's page table, staged once (the host routes runs with more than
-  // kPrefillLdsPages pages elsewhere): the K/V loads of an iteration then
-  // wait on an LDS read rather than on a global load.
+  // kPrefillLdsPages pages elsewhere): the staging addresses of an iteration
+  // then wait on an LDS read rather than on a global load.
   const int n_pages = count_max > 0 ? ((count_max - 1) >> shift) + 1 : 0;
-  for (int i = tid; i < n_pages; i += 64 * kPWaves) page_rows[i] = rows[i];
+  for (int i = tid; i < n_pages; i += kPThreads) page_rows[i] = rows[i];
   __syncthreads();
 
-  // Staging of one iteration: kKeys keys x 512 B of K and of V, 16-byte
-  // chunks; thread tid takes dims 8*(tid%32) of keys tid/32 + kKeyStep*r
-  // (32 consecutive lanes read one key's 512 contiguous bytes).  Keys past
-  // count_max read the last key (in bounds) and are stored as zeros.
+  // Staging of one iteration: wave w moves key rows kStageRows*w .. +15 of
+  // K and of V, two rows per load (lanes 0-31 the first, 32-63 the second,
+  // 16 bytes each).  Lane p of a row writes LDS chunk p; for K that chunk
+  // holds global chunk p ^ (key & 15), for V chunk p ^ 2*(key & 3).  Keys past count_max read the last
+  // key (in bounds); their V rows are zeroed once the last iteration's
+  // loads have landed.
   const uint16_t* kbase = kc + static_cast<int64_t>(g) * kPD;
   const uint16_t* vbase = vc + static_cast<int64_t>(g) * kPD;
-  const int ckey = tid >> 5, cd0 = 8 * (tid & 31);
-  uint4 kreg[kChunksPerThread], vreg[kChunksPerThread];
-  uint32_t in_range = 0;  // bit r: chunk r holds a key below count_max
-  // All page-table reads first, then all K/V loads: no load waits on
-  // another, and the zero fill of keys past count_max happens at the LDS
-  // store, when the loaded data is needed anyway.
-  auto gload = [&](int it) {
-    int32_t page_row[kChunksPerThread];
-    in_range = 0;
+  const int stage_row0 = wave * kStageRows + half;
+  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst) {
 #pragma unroll
-    for (int r = 0; r < kChunksPerThread; ++r) {
-      const int key = it * kKeys + ckey + kKeyStep * r;
-      in_range |= (key < count_max ? 1u : 0u) << r;
-      const int kk = min(key, count_max - 1);
-      page_row[r] = kk;
-    }
-#pragma unroll
-    for (int r = 0; r < kChunksPerThread; ++r) page_row[r] = page_rows[page_row[r] >> shift];
-#pragma unroll
-    for (int r = 0; r < kChunksPerThread; ++r) {
-      const int kk = min(it * kKeys + ckey + kKeyStep * r, count_max - 1);
-      const int64_t slot = static_cast<int64_t>(page_row[r]) + (kk & row_mask);
-      const int64_t off = slot * kv_stride + cd0;
-      kreg[r] = *reinterpret_cast<const uint4*>(kbase + off);
-      vreg[r] = *reinterpret_cast<const uint4*>(vbase + off);
+    for (int i = 0; i < kStageRows / 2; ++i) {
+      const int r = stage_row0 + 2 * i;  // key row within the iteration
+      const int key = min(it * kKeys + r, count_max - 1);
+      const int64_t slot = static_cast<int64_t>(page_rows[key >> shift]) + (key & row_mask);
+      const int64_t off = slot * kv_stride;
+      const int kchunk = row ^ (r & 15);
+      const int lds_row = wave * kStageRows + 2 * i;  // wave-uniform
+      __builtin_amdgcn_global_load_lds(
+          kbase + off + 8 * kchunk,
+          (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          vbase + off + 8 * (row ^ (2 * (r & 3))),
+          (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
     }
   };
-  auto lstore = [&](int buf) {
-    uint8_t* kl = lds + buf * kBufBytes;
-    uint8_t* vl = kl + kKBytes;
+  // V rows of keys >= count_max in this wave's staged rows become zeros
+  // (after the wave's own loads into them have landed).
+  auto zero_tail = [&](int it, uint8_t* vdst) {
+    if ((it + 1) * kKeys <= count_max) return;  // block-uniform
 #pragma unroll
-    for (int r = 0; r < kChunksPerThread; ++r) {
-      const uint32_t keep = ((in_range >> r) & 1u) ? 0xFFFFFFFFu : 0u;
-      const uint4 kv = make_uint4(kreg[r].x & keep, kreg[r].y & keep, kreg[r].z & keep,
-                                  kreg[r].w & keep);
-      const uint4 vv = make_uint4(vreg[r].x & keep, vreg[r].y & keep, vreg[r].z & keep,
-                                  vreg[r].w & keep);
-      *reinterpret_cast<uint4*>(kl + (ckey + kKeyStep * r) * kKPitch + 2 * cd0) = kv;
-      *reinterpret_cast<uint4*>(vl + (ckey + kKeyStep * r) * kVPitch + 2 * cd0) = vv;
+    for (int i = 0; i < kStageRows / 2; ++i) {
+      const int r = stage_row0 + 2 * i;
+      if (it * kKeys + r >= count_max)
+        *reinterpret_cast<uint4*>(vdst + r * kRowBytes + 16 * row) =
+            make_uint4(0u, 0u, 0u, 0u);
     }
   };
 
-  if (n_iters > 0) {
-    gload(0);
-    lstore(0);
-  }
-  if (n_iters > 1) gload(1);
+  if (n_iters > 0) stage(0, kbuf0, vbuf0);
+  __builtin_amdgcn_s_waitcnt(0);  // the Q fragments and iteration 0's rows
+  if (n_iters > 0) zero_tail(0, vbuf0);
   __syncthreads();
 
+  // QK operand reads: lane reads chunk 2d + half of key 32*sb + row, found
+  // at position (2d + half) ^ (row & 15) = 2d ^ kx with kx = (row & 15) ^ half;
+  // the byte address is therefore k_lane ^ 32d.
+  const int k_lane = row * kRowBytes + 16 * ((row & 15) ^ half);
   // Transposing-read address of this lane inside a 16-key tile of V: lane
-  // R = l%16 of group grp addresses key 4*grp + R/4, dims 4*(R%4) .. +3;
-  // the read returns, in lane R, keys 4*grp .. +3 of dim R (per 16 dims).
-  const int tr_off = (4 * grp + (row >> 2)) * kVPitch + 8 * (row & 3);
-  const int key0 = 4 * grp;
-  // Settle every load issued so far (the Q fragments among them) before the
-  // loop, so that the loop's own waits track only the K/V prefetch and the
-  // prefetch stays in flight across a whole iteration.
-  __builtin_amdgcn_s_waitcnt(0);
+  // j of 16-lane group q addresses key 4*(q/2) + j/4 (+8 for the second
+  // read), dims 16*(q%2) + 4*(j%4) .. +3 of 32-dim block b; the read
+  // returns, in lane j, 4 keys of dim 16*(q%2) + j.  Lane l thus gets the
+  // keys 4*half + 0..3 and 8 + 4*half + 0..3 of dim l%32, the k order of its
+  // P values.  Unswizzled, that is chunk c = 4b + 2*(q%2) + (j%4)/2 of the
+  // row, stored at c ^ 2*(j/4) (key & 3 = j/4): position
+  // 4*(b ^ (j/8)) + 2*((q%2) ^ ((j/4)%2)) + (j%4)/2.  b ^ (j/8) is b + j/8
+  // for even b and b - j/8 for odd b, so the per-block addresses are
+  // immediate offsets from two lane bases.  The 4 rows a 16-lane group reads
+  // then cover 8 distinct 16-byte chunks (32 banks).
+  const int vj = lane & 15;
+  const int v_row = (4 * half + (vj >> 2)) * kRowBytes +
+                    32 * (((lane >> 4) & 1) ^ ((vj >> 2) & 1)) + 8 * (vj & 3);
+  const int v_even = v_row + 64 * (vj >> 3);
+  const int v_odd = v_row - 64 * (vj >> 3);
 
-  for (int it = 0; it < n_iters; ++it) {
-    const int buf = it & 1;
-    const uint8_t* kl = lds + buf * kBufBytes;
-    const uint8_t* vl = kl + kKBytes;
-    const int key_base = it * kKeys;
-
-    if (key_base < wave_count) {
-      // ---- S^T for the 4 tiles ----
-      f32x4_t s[kTiles];
+  // S^T of tile pair h (32 keys) of the staged iteration.
+  auto qk = [&](const uint8_t* kl, int h) {
+    f32x16_t sblk;
 #pragma unroll
-      for (int t = 0; t < kTiles; ++t) {
-        s[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        if (key_base + 16 * t < wave_count) {
+    for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
 #pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            const uint4 kv = *reinterpret_cast<const uint4*>(
-                kl + (16 * t + row) * kKPitch + 64 * c + 16 * grp);
-            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv),
-                                                           qf[c], s[t], 0, 0, 0);
+    for (int d = 0; d < kPD / 16; ++d) {
+      const uint4 kv =
+          *reinterpret_cast<const uint4*>(kl + 32 * h * kRowBytes + (k_lane ^ (32 * d)));
+      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kv), qf[d],
+                                                     sblk, 0, 0, 0);
+    }
+    return sblk;
+  };
+  // Online softmax of the pair's two tiles; tile_key0 is the first key of
+  // tile a.  Tiles past the wave's last row are skipped (corr 1, weights 0).
+  auto softmax_pair = [&](const f32x16_t& sblk, int tile_key0, bool masked, float (&w)[2][8],
+                          float (&corr)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = sblk[8 * u + i];
+      if (!masked) {
+        softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u]);
+      } else {
+        corr[u] = 1.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[u][i] = 0.0f;
+        const int tk = tile_key0 + 16 * u;
+        if (tk < wave_count) {  // wave-uniform
+          if (tk + 16 <= wave_min) {
+            softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u]);
+          } else {
+            const int valid = min(16, max(0, count - tk));
+            softmax_tile<true>(sv, valid, half, m, l, corr[u], w[u]);
           }
         }
       }
-      // ---- per pair of tiles: online softmax, fold, acc_stored += V^T P''^T ----
-      // The pair's MFMAs depend only on its own tiles, so they run while
-      // the next pair's softmax is computed.
+    }
+  };
+  // Fold of the pair and acc_stored += V^T P''^T:
+  // acc*c_a*c_b + w_a*c_b V_a + w_b V_b = S' (acc_stored + (w_a*c_b V_a +
+  // w_b V_b) / S'),  S' = S*c_a*c_b.
+  auto fold_pv = [&](const uint8_t* vl, int h, const float (&w)[2][8], const float (&corr)[2]) {
+    float S_new = S * (corr[0] * corr[1]);
+    if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
+      // The accumulators are copied to VGPRs here, inside the rare branch
+      // (the asm keeps the copy from being hoisted to the loop).
 #pragma unroll
-      for (int h = 0; h < kHalves; ++h) {
-        if (key_base + 32 * h >= wave_count) continue;  // wave-uniform
-        float w[2][4];
-        float corr[2];
+      for (int b = 0; b < kDimBlocks; ++b) {
+        f32x16_t t = acc[b];
+        asm volatile("" : "+v"(t));
+        acc[b] = t * S_new;
+      }
+      S_new = 1.0f;
+    }
+    S = S_new;
+    const float inv_s = __builtin_amdgcn_rcpf(S_new);
+    const float fs[2] = {corr[1] * inv_s, inv_s};
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int t = 2 * h + u;
-          const int tile_key0 = key_base + 16 * t;
-          corr[u] = 1.0f;
+    for (int u = 0; u < 2; ++u) {
+      // P''^T as bf16 hi + lo: k index 8*half + i holds the lane's value i.
+      bf16x8_t phi, plo;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) w[u][j] = 0.0f;
-          if (tile_key0 < wave_count) {  // wave-uniform
-            if (tile_key0 + 16 <= wave_min) {
-              softmax_tile<false>(s[t], 16, key0, m, l, corr[u], w[u]);
-            } else {
-              const int valid = min(16, max(0, count - tile_key0));
-              softmax_tile<true>(s[t], valid, key0, m, l, corr[u], w[u]);
-            }
-          }
-        }
-        // acc*c_a*c_b + w_a*c_b V_a + w_b V_b = S' (acc_stored + (w_a*c_b V_a +
-        // w_b V_b) / S'),  S' = S*c_a*c_b.
-        float S_new = S * (corr[0] * corr[1]);
-        if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
+      for (int i = 0; i < 8; i += 2) {
+        const float p0 = w[u][i] * fs[u];
+        const float p1 = w[u][i + 1] * fs[u];
+        const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
+        const float r0 = p0 - static_cast<float>(hb[0]);
+        const float r1 = p1 - static_cast<float>(hb[1]);
+        const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+        phi[i] = hb[0];
+        phi[i + 1] = hb[1];
+        plo[i] = lb[0];
+        plo[i + 1] = lb[1];
+      }
+      const uint8_t* vt = vl + (32 * h + 16 * u) * kRowBytes;
+      // Four 32-dim blocks at a time: 16 VGPRs of V^T operands in flight.
 #pragma unroll
-          for (int b = 0; b < 16; ++b) acc[b] = acc[b] * S_new;
-          S_new = 1.0f;
-        }
-        S = S_new;
-        const float inv_s = 1.0f / S_new;
-        const float fs[2] = {corr[1] * inv_s, inv_s};
-        // P''^T as bf16 hi + lo: k index 8*grp + i holds tile a key 4*grp + i
-        // (i < 4), tile b key 4*grp + i - 4 (i >= 4), the order the V^T
-        // reads below produce.
-        bf16x8_t phi, plo;
+      for (int b0 = 0; b0 < kDimBlocks; b0 += 4) {
+        bf16x8_t av[4];
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-          const int u = i >> 2;
-          const float p0 = w[u][i & 3] * fs[u];
-          const float p1 = w[u][(i & 3) + 1] * fs[u];
-          const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
-          const float r0 = p0 - static_cast<float>(hb[0]);
-          const float r1 = p1 - static_cast<float>(hb[1]);
-          const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
-          phi[i] = hb[0];
-          phi[i + 1] = hb[1];
-          plo[i] = lb[0];
-          plo[i + 1] = lb[1];
-        }
-#pragma unroll
-        for (int b = 0; b < 16; ++b) {
-          const uint8_t* va = vl + (32 * h) * kVPitch + tr_off + 32 * b;
-          const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(va));
+        for (int b = 0; b < 4; ++b) {
+          const uint8_t* vb = vt + (((b0 + b) & 1) ? v_odd : v_even) + 64 * (b0 + b);
+          const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
           const s16x4_t v1 =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(va + 16 * kVPitch));
-          const s16x8_t a8 = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-          const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a8);
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, phi, acc[b], 0, 0, 0);
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, plo, acc[b], 0, 0, 0);
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kRowBytes));
+          av[b] = __builtin_bit_cast(bf16x8_t,
+                                     __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
         }
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], phi, acc[b0 + b], 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], plo, acc[b0 + b], 0, 0, 0);
       }
     }
-    if (it + 1 < n_iters) {
-      lstore(buf ^ 1);
-      if (it + 2 < n_iters) gload(it + 2);
-    }
+  };
+
+  // End of one iteration: the accumulators stay in AGPRs across iterations
+  // (the MFMAs read and write them there; only the rare rescale moves them
+  // through VGPRs); the next iteration's rows have landed (each wave waits
+  // for its own loads; the barrier publishes them to the block).
+  auto iteration_end = [&](int it, uint8_t* vnext) {
+#pragma unroll
+    for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
+    __builtin_amdgcn_s_waitcnt(0);
+    if (it + 1 < n_iters) zero_tail(it + 1, vnext);
     __syncthreads();
+  };
+  // An iteration whose keys are valid for every row: straight-line code.
+  auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
+                            uint8_t* vnext) {
+    if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+    float w0[2][8], c0[2], w1[2][8], c1[2];
+    const f32x16_t s0 = qk(kl, 0);
+    softmax_pair(s0, 0, false, w0, c0);
+    fold_pv(vl, 0, w0, c0);
+    const f32x16_t s1 = qk(kl, 1);
+    softmax_pair(s1, 0, false, w1, c1);
+    fold_pv(vl, 1, w1, c1);
+    iteration_end(it, vnext);
+  };
+  // An iteration on the causal diagonal: per-tile masks.
+  auto masked_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
+                              uint8_t* vnext) {
+    const int key_base = it * kKeys;
+    if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+#pragma unroll 1
+    for (int h = 0; h < kBlocks; ++h) {
+      if (key_base + 32 * h >= wave_count) break;  // wave-uniform
+      float w[2][8], corr[2];
+      const f32x16_t sb = qk(kl, h);
+      softmax_pair(sb, key_base + 32 * h, true, w, corr);
+      fold_pv(vl, h, w, corr);
+    }
+    iteration_end(it, vnext);
+  };
+
+  // Iterations whose keys are valid for every row of the block (the first
+  // row's count bounds them; a partial block has none) run unmasked
+  // straight-line code, in pairs so that each buffer is a fixed LDS object;
+  // the remaining ones (the causal diagonal, and an odd one left over) the
+  // masked per-tile code.  All waves of the block run the same iterations
+  // and barriers.  Iteration it reads buffer it % 2.
+  const int block_min = ntok == kPTokens ? base_pos + (t0 - buf_start) + 1 : 0;
+  const int it_full = min(n_iters, block_min / kKeys) & ~1;
+  int it = 0;
+  for (; it < it_full; it += 2) {
+    full_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
+    full_iteration(it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
+  }
+  for (; it < n_iters; ++it) {
+    if (it & 1)
+      masked_iteration(it, kbuf1, vbuf1, kbuf0, vbuf0);
+    else
+      masked_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
   }
 
   // ---- one-segment merge and bf16 store (PrefillMergeKernel) ----
+  // Lane l holds dims 32*b + 8*j + 4*half + i (value 4*j + i of block b).
   if (row_live) {
     const float c0 = l > 0.0f ? fexp(max_ref(-87.0f, m - m)) : 0.0f;
     const float gl = l * c0;
     const bool live = gl > 0.0f;
     const float inv_l = live ? 1.0f / gl : 0.0f;
-    uint16_t* dst = out + (static_cast<int64_t>(tok) * num_q + head) * kPD + 4 * grp;
+    uint16_t* dst = out + (static_cast<int64_t>(tok) * num_q + head) * kPD + 4 * half;
 #pragma unroll
-    for (int b = 0; b < 16; ++b) {
-      uint32_t e[4];
+    for (int b = 0; b < kDimBlocks; ++b) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float av = (acc[b][j] * S) * c0;
-        e[j] = live ? f32_to_bf16_bits(av * inv_l) : 0u;
+        uint32_t e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float av = (acc[b][4 * j + i] * S) * c0;
+          e[i] = live ? f32_to_bf16_bits(av * inv_l) : 0u;
+        }
+        *reinterpret_cast<uint2*>(dst + 32 * b + 8 * j) =
+            make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
       }
-      *reinterpret_cast<uint2*>(dst + 16 * b) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
     }
   }
 }
@@ -392,7 +492,7 @@ hipError_t launch_prefill_full_mfma(const int32_t* image, int num_qblocks, const
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(prefill_full_mfma_kernel, dim3(num_qblocks * num_kv), dim3(64 * kPWaves),
+  hipLaunchKernelGGL(prefill_full_mfma_kernel, dim3(num_qblocks * num_kv), dim3(kPThreads),
                      0, stream, image, static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
