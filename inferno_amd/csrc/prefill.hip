@@ -300,17 +300,33 @@ void prefill_full_mfma_kernel(
   const int v_odd = v_row - 64 * (vj >> 3);
 
   // S^T of tile pair h (32 keys) of the staged iteration.
+  // The K operand reads run kKAhead steps ahead of their MFMAs.
+  constexpr int kKAhead = 6;
   auto qk = [&](const uint8_t* kl, int h) {
     f32x16_t sblk;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
+    const uint8_t* kh = kl + 32 * h * kRowBytes;
+    uint4 kf[kPD / 16];
+#pragma unroll
+    for (int d = 0; d < kKAhead; ++d)
+      kf[d] = *reinterpret_cast<const uint4*>(kh + (k_lane ^ (32 * d)));
 #pragma unroll
     for (int d = 0; d < kPD / 16; ++d) {
-      const uint4 kv =
-          *reinterpret_cast<const uint4*>(kl + 32 * h * kRowBytes + (k_lane ^ (32 * d)));
-      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kv), qf[d],
+      if (d + kKAhead < kPD / 16)
+        kf[d + kKAhead] = *reinterpret_cast<const uint4*>(kh + (k_lane ^ (32 * (d + kKAhead))));
+      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]), qf[d],
                                                      sblk, 0, 0, 0);
     }
+    // Keep that order: kKAhead reads, then each MFMA followed by the read
+    // kKAhead steps ahead of it.
+    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+    for (int d = 0; d < kPD / 16 - kKAhead; ++d) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
     return sblk;
   };
   // Online softmax of the pair's two tiles; tile_key0 is the first key of
@@ -359,10 +375,11 @@ void prefill_full_mfma_kernel(
     S = S_new;
     const float inv_s = __builtin_amdgcn_rcpf(S_new);
     const float fs[2] = {corr[1] * inv_s, inv_s};
+    // P''^T of both tiles as bf16 hi + lo: k index 8*half + i holds the
+    // lane's value i.
+    bf16x8_t phi[2], plo[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      // P''^T as bf16 hi + lo: k index 8*half + i holds the lane's value i.
-      bf16x8_t phi, plo;
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
         const float p0 = w[u][i] * fs[u];
@@ -371,33 +388,50 @@ void prefill_full_mfma_kernel(
         const float r0 = p0 - static_cast<float>(hb[0]);
         const float r1 = p1 - static_cast<float>(hb[1]);
         const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
-        phi[i] = hb[0];
-        phi[i + 1] = hb[1];
-        plo[i] = lb[0];
-        plo[i + 1] = lb[1];
-      }
-      const uint8_t* vt = vl + (32 * h + 16 * u) * kRowBytes;
-      // Four 32-dim blocks at a time: 16 VGPRs of V^T operands in flight.
-#pragma unroll
-      for (int b0 = 0; b0 < kDimBlocks; b0 += 4) {
-        bf16x8_t av[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint8_t* vb = vt + (((b0 + b) & 1) ? v_odd : v_even) + 64 * (b0 + b);
-          const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
-          const s16x4_t v1 =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kRowBytes));
-          av[b] = __builtin_bit_cast(bf16x8_t,
-                                     __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], phi, acc[b0 + b], 0, 0, 0);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], plo, acc[b0 + b], 0, 0, 0);
+        phi[u][i] = hb[0];
+        phi[u][i + 1] = hb[1];
+        plo[u][i] = lb[0];
+        plo[u][i + 1] = lb[1];
       }
     }
+    // V^T operands in groups of four 32-dim blocks (8 transposing reads);
+    // two groups are in flight, so each group's reads are issued a group of
+    // MFMAs ahead of their use.
+    auto read_group = [&](int u, int b0, bf16x8_t (&av)[4]) {
+      const uint8_t* vt = vl + (32 * h + 16 * u) * kRowBytes;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint8_t* vb = vt + (((b0 + b) & 1) ? v_odd : v_even) + 64 * (b0 + b);
+        const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
+        const s16x4_t v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kRowBytes));
+        av[b] = __builtin_bit_cast(bf16x8_t,
+                                   __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    auto mfma_group = [&](int u, int b0, const bf16x8_t (&av)[4]) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], phi[u], acc[b0 + b], 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], plo[u], acc[b0 + b], 0, 0, 0);
+    };
+    bf16x8_t ga[4], gb[4];
+    read_group(0, 0, ga);
+    read_group(0, 4, gb);
+    mfma_group(0, 0, ga);
+    read_group(1, 0, ga);
+    mfma_group(0, 4, gb);
+    read_group(1, 4, gb);
+    mfma_group(1, 0, ga);
+    mfma_group(1, 4, gb);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   };
 
   // End of one iteration: the accumulators stay in AGPRs across iterations
@@ -415,11 +449,14 @@ void prefill_full_mfma_kernel(
   auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                             uint8_t* vnext) {
     if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+    // Straight-line order that lets the pair-1 scores (MFMA) run under the
+    // pair-0 softmax (VALU), and the pair-0 PV (MFMA) under the pair-1
+    // softmax.
     float w0[2][8], c0[2], w1[2][8], c1[2];
     const f32x16_t s0 = qk(kl, 0);
+    const f32x16_t s1 = qk(kl, 1);
     softmax_pair(s0, 0, false, w0, c0);
     fold_pv(vl, 0, w0, c0);
-    const f32x16_t s1 = qk(kl, 1);
     softmax_pair(s1, 0, false, w1, c1);
     fold_pv(vl, 1, w1, c1);
     iteration_end(it, vnext);
