@@ -43,6 +43,8 @@
 // staged in LDS first.
 // Blocks are numbered kv-head-fastest so every block of a kv head lands on
 // one XCD (block id mod 8) and shares that XCD's L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -91,11 +93,16 @@ __device__ __forceinline__ float max_xor32(float x) {
 // at x = -87 by the caller.
 constexpr float kExpA = 12102203.16156148f;
 constexpr float kExpBias = 1059208216.0f;
+// The quadratic a + f*(b + c*f) in the mantissa fraction f = F - 1 is
+// evaluated in F = 1 + f itself, F taken straight from the bits:
+// (a - b + c) + F*((b - 2c) + c*F).
+constexpr double kExpQa = 1.6501418352127075, kExpQb = -0.37554836273193359,
+                 kExpQc = 0.38696467876434326;
 __device__ __forceinline__ float fexp_fused_t(float t) {
   const int32_t i = static_cast<int32_t>(t);
-  const float f = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u) - 1.0f;
-  float p = __builtin_fmaf(f, 0.38696467876434326f, -0.37554836273193359f);
-  p = __builtin_fmaf(f, p, 1.6501418352127075f);
+  const float F = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u);
+  float p = __builtin_fmaf(F, static_cast<float>(kExpQc), static_cast<float>(kExpQb - 2 * kExpQc));
+  p = __builtin_fmaf(F, p, static_cast<float>(kExpQa - kExpQb + kExpQc));
   return __int_as_float(i) * p;
 }
 __device__ __forceinline__ float fexp_fused(float x) {
@@ -257,6 +264,29 @@ void prefill_full_mfma_kernel(
           (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(
           vbase + off + 8 * (row ^ (2 * (r & 3))),
+          (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+    }
+  };
+  // The same for an iteration whose kStageRows rows per wave all lie below
+  // count_max and inside one page (pages of >= 16 rows): one page lookup, a
+  // wave-uniform 64-bit base and 32-bit row offsets.
+  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+    const int key0 = it * kKeys + wave * kStageRows;  // wave-uniform
+    const int prow = __builtin_amdgcn_readfirstlane(page_rows[key0 >> shift]);
+    const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+    const uint16_t* kb = kbase + slot0 * kv_stride;
+    const uint16_t* vb = vbase + slot0 * kv_stride;
+    const int stride = static_cast<int>(kv_stride);
+#pragma unroll
+    for (int i = 0; i < kStageRows / 2; ++i) {
+      const int rr = 2 * i + half;  // row within the wave's rows (r & 15 == rr)
+      const int roff = rr * stride;
+      const int lds_row = wave * kStageRows + 2 * i;  // wave-uniform
+      __builtin_amdgcn_global_load_lds(
+          kb + roff + 8 * (row ^ rr),
+          (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          vb + roff + 8 * (row ^ (2 * (rr & 3))),
           (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
     }
   };
@@ -446,9 +476,15 @@ void prefill_full_mfma_kernel(
     __syncthreads();
   };
   // An iteration whose keys are valid for every row: straight-line code.
-  auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
-                            uint8_t* vnext) {
-    if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+  // The next iteration's rows are staged unconditionally (past the last
+  // iteration they are clamped, in-bounds rows of an unused buffer), so the
+  // staging shares a block with the score MFMAs.
+  auto full_iteration = [&](auto page_stage, int it, const uint8_t* kl, const uint8_t* vl,
+                            uint8_t* knext, uint8_t* vnext) {
+    if (decltype(page_stage)::value)
+      stage_page(it + 1, knext, vnext);
+    else
+      stage(it + 1, knext, vnext);
     // Straight-line order that lets the pair-1 scores (MFMA) run under the
     // pair-0 softmax (VALU), and the pair-0 PV (MFMA) under the pair-1
     // softmax.
@@ -486,9 +522,18 @@ void prefill_full_mfma_kernel(
   const int block_min = ntok == kPTokens ? base_pos + (t0 - buf_start) + 1 : 0;
   const int it_full = min(n_iters, block_min / kKeys) & ~1;
   int it = 0;
-  for (; it < it_full; it += 2) {
-    full_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
-    full_iteration(it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
+  // Iteration it + 1 < it_full has every row below count_max, so with pages
+  // of >= 16 rows the first of a pair stages through stage_page.
+  if (shift >= 4) {
+    for (; it < it_full; it += 2) {
+      full_iteration(std::true_type{}, it, kbuf0, vbuf0, kbuf1, vbuf1);
+      full_iteration(std::false_type{}, it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
+    }
+  } else {
+    for (; it < it_full; it += 2) {
+      full_iteration(std::false_type{}, it, kbuf0, vbuf0, kbuf1, vbuf1);
+      full_iteration(std::false_type{}, it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
+    }
   }
   for (; it < n_iters; ++it) {
     if (it & 1)
