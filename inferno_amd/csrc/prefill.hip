@@ -221,6 +221,10 @@ void prefill_full_mfma_kernel(
       qf[d] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
+  // The Q^T fragments live in AGPRs (MFMA operands may come from there),
+  // which leaves the VGPRs to the softmax and the operand reads.
+#pragma unroll
+  for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
 
   // The O^T accumulator is kept as acc_stored with acc = acc_stored * S: a
   // tile's rescale multiplies S, and the weights entering the MFMA are
@@ -399,6 +403,8 @@ void prefill_full_mfma_kernel(
         f32x16_t t = acc[b];
         asm volatile("" : "+v"(t));
         acc[b] = t * S_new;
+        asm volatile("" : "+a"(acc[b]));
+        __builtin_amdgcn_sched_barrier(0);  // one block of 16 at a time in VGPRs
       }
       S_new = 1.0f;
     }
@@ -464,13 +470,15 @@ void prefill_full_mfma_kernel(
     __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   };
 
-  // End of one iteration: the accumulators stay in AGPRs across iterations
-  // (the MFMAs read and write them there; only the rare rescale moves them
-  // through VGPRs); the next iteration's rows have landed (each wave waits
+  // End of one iteration: the accumulators and the Q^T fragments stay in
+  // AGPRs across iterations (the MFMAs read and write them there; only the
+  // rare rescale moves the accumulators through VGPRs); the next iteration's rows have landed (each wave waits
   // for its own loads; the barrier publishes them to the block).
   auto iteration_end = [&](int it, uint8_t* vnext) {
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
+#pragma unroll
+    for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
     __builtin_amdgcn_s_waitcnt(0);
     if (it + 1 < n_iters) zero_tail(it + 1, vnext);
     __syncthreads();
