@@ -428,6 +428,73 @@ __global__ __launch_bounds__(256) void merge_kernel(
   }
 }
 
+// The sliced merge of one (head, dim) over n <= 64 * kChunks splits with
+// every load of the unit issued at once (m and l of the lane's splits, the
+// lane's dim of all n splits), then the operations of the chunked path in
+// merge_sliced_kernel in the same order: global max, per 64-split chunk the
+// corrections and the halving-tree sums of L in batches of 16, and the acc
+// chain over the splits in order.
+template <int kChunks>
+__device__ __forceinline__ void merge_sliced_direct(const float* base, int64_t partial_stride,
+                                                    int m_off, int l_off, int h, int D, int dim,
+                                                    int lane, int n, float& acc, float& inv_l,
+                                                    bool& live) {
+  float mv[kChunks], lv[kChunks];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    mv[c] = kNegBig;
+    lv[c] = 0.0f;
+    if (64 * c + lane < n) {
+      const float* sp = base + static_cast<int64_t>(64 * c + lane) * partial_stride;
+      mv[c] = sp[m_off + h];
+      lv[c] = sp[l_off + h];
+    }
+  }
+  float src[64 * kChunks];
+  const float* col = base + static_cast<int64_t>(h) * D + dim;
+#pragma unroll
+  for (int u = 0; u < 64 * kChunks; ++u)
+    src[u] = col[static_cast<int64_t>(min(u, n - 1)) * partial_stride];
+  float gm = kNegBig;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    float sm = mv[c];
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) sm = max_ref(sm, shfl_xor_f32(sm, msk));
+    gm = max_ref(gm, sm);
+  }
+  float gl = 0.0f;
+  bool first = true;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const float delta = 64 * c + lane < n ? mv[c] - gm : kNegBig;
+    float cv = fexp(max_ref(-87.0f, delta));
+    cv = lv[c] > 0.0f ? cv : 0.0f;
+    float prod = lv[c] * cv;
+    prod = prod + shfl_xor_f32(prod, 8);
+    prod = prod + shfl_xor_f32(prod, 4);
+    prod = prod + shfl_xor_f32(prod, 2);
+    prod = prod + shfl_xor_f32(prod, 1);
+    const int cnt = min(64, n - 64 * c);
+    for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
+#pragma unroll
+    for (int u = 0; u < 64; ++u) {
+      const float cu = u < cnt ? readlane_f32(cv, u) : 0.0f;  // cv is 0 past n
+      if (cu <= 0.0f) continue;
+      if (first) {
+        acc = src[64 * c + u] * cu;
+        first = false;
+      } else {
+        acc = fmaf(src[64 * c + u], cu, acc);
+      }
+    }
+  }
+  if (gl > 0.0f) {
+    live = true;
+    inv_l = 1.0f / gl;
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void merge_sliced_kernel(
     const int32_t* __restrict__ image, const float* __restrict__ partials,
@@ -465,50 +532,11 @@ __global__ __launch_bounds__(256) void merge_sliced_kernel(
       acc = base[static_cast<int64_t>(h) * D + dim];
     }
   } else if (n > 0 && n <= 64) {
-    // One chunk: every load of the unit (m and l of the lane's split, the
-    // lane's dim of all n splits) issues at once, then the same operations as
-    // below in the same order.
-    float mv = kNegBig, lv = 0.0f;
-    if (lane < n) {
-      const float* sp = base + static_cast<int64_t>(lane) * partial_stride;
-      mv = sp[m_off + h];
-      lv = sp[l_off + h];
-    }
-    float src[64];
-    const float* col = base + static_cast<int64_t>(h) * D + dim;
-#pragma unroll
-    for (int u = 0; u < 64; ++u)
-      src[u] = col[static_cast<int64_t>(min(u, n - 1)) * partial_stride];
-    float gm = mv;
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) gm = max_ref(gm, shfl_xor_f32(gm, msk));
-    gm = max_ref(kNegBig, gm);
-    const float delta = lane < n ? mv - gm : kNegBig;
-    float cv = fexp(max_ref(-87.0f, delta));
-    cv = lv > 0.0f ? cv : 0.0f;
-    float prod = lv * cv;
-    prod = prod + shfl_xor_f32(prod, 8);
-    prod = prod + shfl_xor_f32(prod, 4);
-    prod = prod + shfl_xor_f32(prod, 2);
-    prod = prod + shfl_xor_f32(prod, 1);
-    float gl = 0.0f;
-    for (int b = 0; b * 16 < n; ++b) gl = gl + readlane_f32(prod, 16 * b);
-    bool first = true;
-#pragma unroll
-    for (int u = 0; u < 64; ++u) {
-      const float cu = u < n ? readlane_f32(cv, u) : 0.0f;  // cv is 0 past n
-      if (cu <= 0.0f) continue;
-      if (first) {
-        acc = src[u] * cu;
-        first = false;
-      } else {
-        acc = fmaf(src[u], cu, acc);
-      }
-    }
-    if (gl > 0.0f) {
-      live = true;
-      inv_l = 1.0f / gl;
-    }
+    merge_sliced_direct<1>(base, partial_stride, m_off, l_off, h, D, dim, lane, n, acc, inv_l,
+                           live);
+  } else if (n > 0 && n <= 128) {
+    merge_sliced_direct<2>(base, partial_stride, m_off, l_off, h, D, dim, lane, n, acc, inv_l,
+                           live);
   } else {
     // Lanes own splits.  Global max: wave max per 64-split chunk (exact in any
     // order).  Corrections and L: the reference sums the splits in batches

@@ -51,7 +51,7 @@ def _assert_close(got, ref, what):
     assert r["n_nan"] == 0 and r["n_fail"] == 0, (what, r)
 
 
-@pytest.mark.parametrize("cap", [1, 3, 128, 512])
+@pytest.mark.parametrize("cap", [1, 3, 64, 96, 128, 512])
 def test_config1_append_then_decode(cap):
     """Config 1: B=1, ctx 4096 in 64-token pages drawn from a seeded permutation
     of a 128-page pool; append one token (RoPE + cache write), then decode."""
