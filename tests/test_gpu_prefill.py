@@ -24,9 +24,9 @@ def _table(runs, rows) -> KVRunTable:
     return t
 
 
-def _prefill(case, n, q, k, v, cap=16):
+def _prefill(case, n, q, k, v, cap=16, page_len=PAGE_LEN):
     plan = AttentionPlan(_table(case.runs, case.base_rows), n, kind=FULL, window=0,
-                         cache_size=PAGE_LEN, page_len=PAGE_LEN, cache_rows=case.cache_rows,
+                         cache_size=page_len, page_len=page_len, cache_rows=case.cache_rows,
                          cap=cap, kv_row_bytes=KV_STRIDE * 2)
     assert plan.summary.mode == 2 and int(plan.info[14]) > 0
     out = empty_dev(n * NUM_Q * HEAD_DIM, np.uint16)
@@ -51,6 +51,28 @@ def test_prefill_small_all_tokens():
                            threads=8)
     r = compare_bf16(got, ref)
     print(f"  prefill small: {r}", flush=True)
+    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+
+
+@pytest.mark.parametrize("page_len", [8, 128])
+def test_prefill_page_sizes(page_len):
+    """Pages of 8 rows (the kernel's per-row staging path) and of 128 rows
+    (a staged iteration inside one page), with full and partial query blocks
+    and prefixes that are not page multiples."""
+    announce(f"prefill page_len={page_len}")
+    prefix, new = [0, 70, 1500, 333], [64, 200, 129, 7]
+    case = make_prefill_case(11 + page_len, prefix, new, page_len=page_len)
+    n = sum(new)
+    q = seeded_bf16(n * NUM_Q * HEAD_DIM, 21)
+    k = seeded_bf16(case.cache_rows * KV_STRIDE, 22)
+    v = seeded_bf16(case.cache_rows * KV_STRIDE, 23)
+    got = _prefill(case, n, to_dev(q), to_dev(k), to_dev(v), page_len=page_len)
+    ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=NUM_Q,
+                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
+                           cache_size=page_len, page_len=page_len, seq_len=n, cap=16,
+                           threads=8)
+    r = compare_bf16(got, ref)
+    print(f"  prefill page_len={page_len}: {r}", flush=True)
     assert r["n_fail"] == 0 and r["n_nan"] == 0, r
 
 
