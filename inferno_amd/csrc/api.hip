@@ -320,6 +320,18 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
       unit_buf.insert(unit_buf.end(), {runs[4 * i], sb[i], ns[i]});
       n_stripes += ns[i];
     }
+    // Longest items first: workgroups are dispatched in item order as
+    // earlier ones finish, so this is a longest-processing-time schedule
+    // over the CUs (each item names its own stripe; the order changes no
+    // result).
+    std::vector<std::array<int32_t, kItemWords>> recs(n_items);
+    for (int64_t i = 0; i < n_items; ++i)
+      std::copy(items + i * kItemWords, items + (i + 1) * kItemWords, recs[i].begin());
+    std::stable_sort(recs.begin(), recs.end(), [](const auto& x, const auto& y) {
+      return x[4] - x[3] > y[4] - y[3];
+    });
+    for (int64_t i = 0; i < n_items; ++i)
+      std::copy(recs[i].begin(), recs[i].end(), items + i * kItemWords);
   } else {
     // Token-partitioned prefill kernels (kernels/flash_attention_prefill.mojo).
     mode = sliding ? IFR_PLAN_TOKEN_DIRECT : IFR_PLAN_TOKEN_MERGE;
