@@ -13,9 +13,10 @@
 //                       32-slot streaming bank, each reduction done as a rank
 //                       count under reduce_argmax's order (value, then slot
 //                       lane, then slot register).
-// sparse_attention_kernel  one wave per (token, kv head): S = K.Q^T and P.V for
-//                       the 16 q heads of the kv head on MFMA around the
-//                       reference's per-tile online softmax, then the
+// sparse_attention_kernel  four waves per (token, kv head): S = K.Q^T and P.V
+//                       for the 16 q heads of the kv head on MFMA around the
+//                       reference's per-tile online softmax (each wave forms
+//                       the same scores and owns 32 output dims), then the
 //                       one-stripe finalisation.
 #include "common.hpp"
 #include "launch.hpp"
@@ -350,19 +351,28 @@ __device__ __forceinline__ TileCursor next_tile(TileCursor c, const int32_t* bro
 
 struct TileRegs {
   uint4 k0, k1, k2, k3;  // keys: row r16, dims 32c + 8g .. +8
-  uint4 v0, v1, v2, v3;  // values: rows g, g+4, g+8, g+12, 16 bytes at 16*r16
+  uint4 v0;              // values: row lane/4, 16 bytes of the wave's 32 dims
 };
+// The four waves of a workgroup share one (token, kv head): each forms the
+// same scores and softmax (identical arithmetic) and owns 32 of the 128
+// output dims in P.V, so a decode step has four times as many waves on its
+// block lists.  V rows of the wave's dims are staged at a 96-byte pitch
+// (4 rows x 32 bytes of a transposing read fall on distinct banks).
+constexpr int kSDW = kSD / 4;                 // output dims per wave
+constexpr int kSVPitchW = kSDW * 2 + 32;      // bytes per V row in LDS
+constexpr int kSVBytesW = kTile * kSVPitchW;
 
 __global__ __launch_bounds__(256) void sparse_attention_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k_base, const uint16_t* __restrict__ v_base,
     const int32_t* __restrict__ block_idx, uint16_t* __restrict__ out, int64_t kv_stride,
     int num_q, int num_kv, int block_size, int topk, int shift, int row_mask, int num_rows) {
-  __shared__ __align__(16) uint8_t vlds[4][2][kSVBytes];
+  __shared__ __align__(16) uint8_t vlds[4][2][kSVBytesW];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + wave;
+  const int row = blockIdx.x;
   if (row >= num_rows) return;
+  const int dq = wave;  // the wave's quarter of the output dims
   const int t = row / num_kv;
   const int h = row - t * num_kv;
   const TokenPos tp = token_position(image, t);
@@ -382,11 +392,13 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
   const uint16_t* kh = k_base + static_cast<int64_t>(h) * kSD;
   const uint16_t* vh = v_base + static_cast<int64_t>(h) * kSD;
   const int32_t* brow = block_idx + static_cast<int64_t>(row) * topk;
-  // V staging: lane takes 16 bytes of rows g, g+4, g+8, g+12.
-  const int vcol = 16 * r16;
+  // V staging: lane takes 16 bytes (chunk lane%4) of row lane/4 of the
+  // wave's 32 dims.
+  const int vrow_l = lane >> 2;
+  const int vcol = 16 * (lane & 3);
   // Transposing read: lane r16 of group g addresses row 4g + r16/4, dims
   // 4*(r16%4) .. +3 of a 16-dim block, and receives V[4g + k][16b + r16].
-  const int tr_off = (4 * g + (r16 >> 2)) * kSVPitch + 8 * (r16 & 3);
+  const int tr_off = (4 * g + (r16 >> 2)) * kSVPitchW + 8 * (r16 & 3);
 
   // A tile never straddles a page (page_len >= 16, tiles 16-aligned), so its
   // page row is one uniform (scalar) load, not a vector load the K/V loads
@@ -402,23 +414,17 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     d.k1 = *reinterpret_cast<const uint4*>(kp + 32);
     d.k2 = *reinterpret_cast<const uint4*>(kp + 64);
     d.k3 = *reinterpret_cast<const uint4*>(kp + 96);
-    auto vrow = [&](int rr) {
-      const int64_t vslot = prow + off0 + (rr < tl ? rr : 0);
-      return *reinterpret_cast<const uint4*>(
-          reinterpret_cast<const uint8_t*>(vh + vslot * kv_stride) + vcol);
-    };
-    d.v0 = vrow(g);
-    d.v1 = vrow(g + 4);
-    d.v2 = vrow(g + 8);
-    d.v3 = vrow(g + 12);
+    const int64_t vslot = prow + off0 + (vrow_l < tl ? vrow_l : 0);
+    d.v0 = *reinterpret_cast<const uint4*>(
+        reinterpret_cast<const uint8_t*>(vh + vslot * kv_stride + kSDW * dq) + vcol);
     return d;
   };
 
   float m = kNegBig;  // state of head r16 (the same in its four lanes)
   float lsum = 0.0f;
-  f32x4_t acc[kSD / 16];  // acc[b][j] = O[dim 16b + 4g + j][head r16]
+  f32x4_t acc[kSDW / 16];  // acc[b][j] = O[dim 32dq + 16b + 4g + j][head r16]
 #pragma unroll
-  for (int b = 0; b < kSD / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b = 0; b < kSDW / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // Three tiles in flight: the current one (rg), and the next two (r1, then
   // r2, issued during the current tile).
@@ -436,10 +442,7 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     const int tl = static_cast<int>(min<int64_t>(kTile, cur.phi - cur.pos));
     uint8_t* vb = vlds[wave][buf];
     wave_sync();
-    *reinterpret_cast<uint4*>(vb + g * kSVPitch + vcol) = rg.v0;
-    *reinterpret_cast<uint4*>(vb + (g + 4) * kSVPitch + vcol) = rg.v1;
-    *reinterpret_cast<uint4*>(vb + (g + 8) * kSVPitch + vcol) = rg.v2;
-    *reinterpret_cast<uint4*>(vb + (g + 12) * kSVPitch + vcol) = rg.v3;
+    *reinterpret_cast<uint4*>(vb + vrow_l * kSVPitchW + vcol) = rg.v0;
     TileRegs r2{};
     if (c2.valid) r2 = load_tile(c2);
 
@@ -488,7 +491,7 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     }
     wave_sync();
 #pragma unroll
-    for (int b = 0; b < kSD / 16; ++b) {
+    for (int b = 0; b < kSDW / 16; ++b) {
       acc[b] = acc[b] * corr;  // scale_unrolled for head r16
       const s16x4_t va =
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + tr_off + 32 * b));
@@ -509,9 +512,10 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
   cv = lsum > 0.0f ? cv : 0.0f;
   const float gl = 0.0f + lsum * cv;
   const float inv = gl > 0.0f ? 1.0f / gl : 0.0f;
-  uint16_t* orow = out + (static_cast<int64_t>(t) * num_q + h * kSG + r16) * kSD + 4 * g;
+  uint16_t* orow =
+      out + (static_cast<int64_t>(t) * num_q + h * kSG + r16) * kSD + kSDW * dq + 4 * g;
 #pragma unroll
-  for (int b = 0; b < kSD / 16; ++b) {
+  for (int b = 0; b < kSDW / 16; ++b) {
     uint32_t lo = 0, hi = 0;
     if (gl > 0.0f) {
       lo = f32_to_bf16_bits((acc[b][0] * cv) * inv) | (f32_to_bf16_bits((acc[b][1] * cv) * inv) << 16);
@@ -882,7 +886,7 @@ hipError_t launch_block_sparse_attention(const int32_t* image, int seq_len, cons
                                          hipStream_t stream) {
   if (seq_len <= 0) return hipSuccess;
   const int rows = seq_len * num_kv;
-  hipLaunchKernelGGL(sparse_attention_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream,
+  hipLaunchKernelGGL(sparse_attention_kernel, dim3(rows), dim3(256), 0, stream,
                      image, static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k_base), static_cast<const uint16_t*>(v_base),
                      block_idx, static_cast<uint16_t*>(output), kv_stride, num_q, num_kv,
