@@ -213,7 +213,7 @@ __device__ __forceinline__ void unpack_i8x4(uint32_t w, float* f) {
   f[3] = static_cast<float>(static_cast<int8_t>(w >> 24));
 }
 
-template <int G>
+template <int G, bool kTwoPages>
 __global__ __launch_bounds__(256) void bq_partial_kernel(
     const int32_t* __restrict__ image, const int8_t* __restrict__ q_i8,
     const float* __restrict__ qi_bias, const float* __restrict__ f_q,
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
     int64_t partial_stride, int num_q, int num_kv, int64_t kv_stride,
     int shift, int row_mask, int page_mask) {
   constexpr int D = kBqD;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.y * 4 + wave;
   if (g >= num_kv) return;
@@ -277,34 +277,74 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
     for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
   }
 
+  // One tile's loads: the lane's 64 key bytes of position tk and its scale,
+  // then the 4 value bytes (dims 4*lane..) of every position and the
+  // positions' value scales.  Positions past the tile's end load the tile's
+  // last position (in bounds) and are masked below.  kTwoPages (pages of
+  // >= 16 positions): a tile spans at most two pages, whose rows come from
+  // two scalar loads, and the value scales are scalar loads too, so no
+  // vector load waits on another.
+  struct BqDecodeTile {
+    uint4 k[4];
+    float ks;
+    uint32_t v[kTile];
+    float vs[kTile];
+  };
+  auto load_tile = [&](int pos0) {
+    BqDecodeTile d;
+    const int tile_len = min(kTile, end - pos0);
+    const int p0 = start_pos + pos0;
+    const int pg0 = p0 >> shift;
+    int64_t ra = 0, rb = 0;
+    if constexpr (kTwoPages) {
+      const int pg1 = (p0 + tile_len - 1) >> shift;
+      ra = sload(rows + (pg0 & page_mask));
+      rb = pg1 != pg0 ? sload(rows + (pg1 & page_mask)) : ra;
+    }
+    auto slot_of = [&](int p) -> int64_t {
+      if constexpr (kTwoPages) {
+        return ((p >> shift) == pg0 ? ra : rb) + (p & row_mask);
+      } else {
+        return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+      }
+    };
+    const int64_t kslot = slot_of(p0 + min(tk, tile_len - 1));
+    const int8_t* kr = kh + kslot * kv_stride;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d.k[i] = *reinterpret_cast<const uint4*>(kr + 64 * i);
+    d.ks = k_scale[kslot * num_kv + g];
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      const int64_t vslot = slot_of(p0 + min(t, tile_len - 1));
+      d.v[t] = *reinterpret_cast<const uint32_t*>(vh + vslot * kv_stride);
+      if constexpr (kTwoPages) {
+        d.vs[t] = __int_as_float(sload(reinterpret_cast<const int32_t*>(v_scale) +
+                                       vslot * num_kv + g));
+      } else {
+        d.vs[t] = v_scale[vslot * num_kv + g];
+      }
+    }
+    return d;
+  };
+
+  BqDecodeTile cur = load_tile(start);
   for (int pos0 = start; pos0 < end; pos0 += kTile) {
     const int tile_len = min(kTile, end - pos0);
     const bool valid = tk < tile_len;
+    BqDecodeTile nxt;
+    if (pos0 + kTile < end) nxt = load_tile(pos0 + kTile);  // wave-uniform
     float s[G];
     {
-      uint4 kv4[4];
-      float ks = 0.0f;
-      if (valid) {
-        const int p = start_pos + pos0 + tk;
-        const int64_t slot =
-            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
-        const int8_t* kr = kh + slot * kv_stride;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kv4[i] = *reinterpret_cast<const uint4*>(kr + 64 * i);
-        ks = k_scale[slot * num_kv + g];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kv4[i] = make_uint4(0, 0, 0, 0);
-      }
+      const float ks = cur.ks;
 #pragma unroll
       for (int r = 0; r < G; ++r) {
         int a = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].x), static_cast<int>(qv[r][i].x), a, false);
-          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].y), static_cast<int>(qv[r][i].y), a, false);
-          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].z), static_cast<int>(qv[r][i].z), a, false);
-          a = __builtin_amdgcn_sdot4(static_cast<int>(kv4[i].w), static_cast<int>(qv[r][i].w), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(cur.k[i].x), static_cast<int>(qv[r][i].x), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(cur.k[i].y), static_cast<int>(qv[r][i].y), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(cur.k[i].z), static_cast<int>(qv[r][i].z), a, false);
+          a = __builtin_amdgcn_sdot4(static_cast<int>(cur.k[i].w), static_cast<int>(qv[r][i].w), a, false);
         }
         a = a + dpp_i32<kDppXor1>(a);
         a = a + dpp_i32<kDppXor2>(a);
@@ -313,19 +353,6 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
         sc = sc * ks;
         sc = sc * inv127sq;
         s[r] = valid ? sc : kNegBig;
-      }
-    }
-
-    uint32_t vv[kTile];
-    float vs[kTile];
-#pragma unroll
-    for (int t = 0; t < kTile; ++t) {
-      if (t < tile_len) {
-        const int p = start_pos + pos0 + t;
-        const int64_t slot =
-            static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
-        vv[t] = *reinterpret_cast<const uint32_t*>(vh + slot * kv_stride);
-        vs[t] = v_scale[slot * num_kv + g];
       }
     }
 
@@ -355,19 +382,20 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
 
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      if (t < tile_len) {
+      if (t < tile_len) {  // wave-uniform
         float vf[4];
-        unpack_i8x4(vv[t], vf);
+        unpack_i8x4(cur.v[t], vf);
 #pragma unroll
         for (int r = 0; r < G; ++r) {
           const float wt = readlane_f32(w[r], 4 * t);
-          const float a = wt * vs[t];
+          const float a = wt * cur.vs[t];
           const float wts = a * inv127;
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[r][e] = fmaf(vf[e], wts, acc[r][e]);
         }
       }
     }
+    cur = nxt;
   }
 
   float* part = partials + static_cast<int64_t>(stripe) * partial_stride;
@@ -418,11 +446,18 @@ hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_unit
                                hipStream_t stream, int8_t* q_out, float* q_scale) {
   if (num_items > 0) {
     dim3 grid(num_items, (num_kv + 3) / 4);
-    hipLaunchKernelGGL(bq_partial_kernel<2>, grid, dim3(256), 0, stream, image,
-                       static_cast<const int8_t*>(q_i8), qi_bias, f_q,
-                       static_cast<const int8_t*>(k_base), k_scale,
-                       static_cast<const int8_t*>(v_base), v_scale, partials, ps, num_q,
-                       num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
+    if (geom.row_mask + 1 >= kTile)
+      hipLaunchKernelGGL((bq_partial_kernel<2, true>), grid, dim3(256), 0, stream, image,
+                         static_cast<const int8_t*>(q_i8), qi_bias, f_q,
+                         static_cast<const int8_t*>(k_base), k_scale,
+                         static_cast<const int8_t*>(v_base), v_scale, partials, ps, num_q,
+                         num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
+    else
+      hipLaunchKernelGGL((bq_partial_kernel<2, false>), grid, dim3(256), 0, stream, image,
+                         static_cast<const int8_t*>(q_i8), qi_bias, f_q,
+                         static_cast<const int8_t*>(k_base), k_scale,
+                         static_cast<const int8_t*>(v_base), v_scale, partials, ps, num_q,
+                         num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
