@@ -51,12 +51,13 @@ __device__ __forceinline__ TokenPos token_position(const int32_t* image, int t) 
 // (32p + 2j + 1, 32p + 2j) as odd*odd + even*even, lane j sums its
 // accumulators p = 0.. in order, then the 16-lane halving tree.
 // ---------------------------------------------------------------------------
-template <int D, int H>
+template <int D, int H, bool kPageRows>
 __global__ __launch_bounds__(256) void index_scores_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ index_q,
     const uint16_t* __restrict__ index_k, float* __restrict__ scores, int block_stride,
     int block_size, float scale, int shift, int row_mask) {
   constexpr int kP = D / 32;  // port-unroll accumulators, one strip
+  static_assert(H * D == 64 * 8, "one 16-byte query load per lane");
   __shared__ __align__(16) float qs[4][H * D];  // the token's queries, unpacked
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
@@ -67,9 +68,34 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
   if (b >= nb) return;
   const int lo = b * block_size;
   const int hi = min(lo + block_size, tp.abs_pos + 1);
+
+  // One round = 64 positions, one per lane.  A lane past the block rereads
+  // the block's last position (in bounds) and is left out of the maxima.
+  // kPageRows (pages of >= 64 rows): a round spans at most two pages, whose
+  // rows come from scalar loads.
+  auto load_round = [&](int p0, uint4 (&kv)[D / 8]) {
+    const int pos = min(p0 + lane, hi - 1);
+    int64_t slot;
+    if constexpr (kPageRows) {
+      const int pg0 = p0 >> shift;
+      const int pg1 = min(p0 + 63, hi - 1) >> shift;
+      const int64_t ra = sload(tp.rows + pg0);
+      const int64_t rb = pg1 != pg0 ? sload(tp.rows + pg1) : ra;
+      slot = ((pos >> shift) == pg0 ? ra : rb) + (pos & row_mask);
+    } else {
+      slot = static_cast<int64_t>(tp.rows[pos >> shift]) + (pos & row_mask);
+    }
+    const uint4* kr = reinterpret_cast<const uint4*>(index_k + slot * D);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) kv[c] = kr[c];
+  };
+  uint4 kv[D / 8];
+  load_round(lo, kv);  // in flight while the queries are staged
   {
-    const uint16_t* qt = index_q + static_cast<int64_t>(t) * H * D;
-    for (int i = lane; i < H * D; i += 64) qs[wave][i] = bf16_to_f32(qt[i]);
+    const uint4 q8 = reinterpret_cast<const uint4*>(index_q + static_cast<int64_t>(t) * H * D)[lane];
+    float4* qd = reinterpret_cast<float4*>(&qs[wave][8 * lane]);
+    qd[0] = make_float4(bf16_lo(q8.x), bf16_hi(q8.x), bf16_lo(q8.y), bf16_hi(q8.y));
+    qd[1] = make_float4(bf16_lo(q8.z), bf16_hi(q8.z), bf16_lo(q8.w), bf16_hi(q8.w));
   }
   wave_sync();
   float best[H];
@@ -78,13 +104,11 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
   // A lane takes whole positions and all heads: the key's pairs are unpacked
   // once, the queries are read from LDS (every lane the same address).
   for (int p0 = lo; p0 < hi; p0 += 64) {
-    const int pos = p0 + lane;
-    if (pos >= hi) break;
-    const int64_t slot = static_cast<int64_t>(tp.rows[pos >> shift]) + (pos & row_mask);
-    const uint4* kr = reinterpret_cast<const uint4*>(index_k + slot * D);
-    uint4 kv[D / 8];
-#pragma unroll
-    for (int c = 0; c < D / 8; ++c) kv[c] = kr[c];
+    const bool valid = p0 + lane < hi;
+    // The query reads stay inside the loop (hoisted, 512 floats would not
+    // fit in registers).
+    int qoff = wave * H * D;
+    asm volatile("" : "+v"(qoff));
     float s[H][16];
 #pragma unroll
     for (int p = 0; p < kP; ++p) {
@@ -101,7 +125,7 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
       }
 #pragma unroll
       for (int h = 0; h < H; ++h) {
-        const float4* qh = reinterpret_cast<const float4*>(&qs[wave][h * D + 32 * p]);
+        const float4* qh = reinterpret_cast<const float4*>(&qs[0][qoff + h * D + 32 * p]);
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
           const float4 q4 = qh[j / 2];  // even, odd of pair j, then of pair j+1
@@ -121,8 +145,12 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
         for (int jj = 0; jj < w; ++jj) s[h][jj] = s[h][jj] + s[h][jj + w];
       }
       const float sh = s[h][0] * scale;
-      best[h] = sh > best[h] ? sh : best[h];
+      best[h] = valid && sh > best[h] ? sh : best[h];
     }
+    // The next round's loads are issued after this round's math (with its
+    // registers, 3 waves fit per SIMD; a prefetch into a second set, at 2
+    // waves per SIMD, measured slower).
+    if (p0 + 64 < hi) load_round(p0 + 64, kv);  // wave-uniform
   }
 #pragma unroll
   for (int h = 0; h < H; ++h) {
@@ -821,9 +849,16 @@ hipError_t launch_lightning_indexer(const int32_t* image, int seq_len, const voi
   if (seq_len <= 0) return hipSuccess;
   if (head_dim != 128 || num_heads != 4) return hipErrorInvalidValue;
   dim3 grid((block_stride + 3) / 4, seq_len);
-  hipLaunchKernelGGL((index_scores_kernel<128, 4>), grid, dim3(256), 0, stream, image,
-                     static_cast<const uint16_t*>(index_q), static_cast<const uint16_t*>(index_k),
-                     scores, block_stride, block_size, scale, shift, row_mask);
+  const auto* iq = static_cast<const uint16_t*>(index_q);
+  const auto* ik = static_cast<const uint16_t*>(index_k);
+  if (row_mask + 1 >= 64)
+    hipLaunchKernelGGL((index_scores_kernel<128, 4, true>), grid, dim3(256), 0,
+                       stream, image, iq, ik, scores, block_stride, block_size, scale, shift,
+                       row_mask);
+  else
+    hipLaunchKernelGGL((index_scores_kernel<128, 4, false>), grid, dim3(256), 0,
+                       stream, image, iq, ik, scores, block_stride, block_size, scale, shift,
+                       row_mask);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int rows = seq_len * num_heads;

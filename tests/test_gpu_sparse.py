@@ -61,8 +61,10 @@ def _check_indexer(runs, rows, index_q, index_k, cache_rows, page_len):
     return got, got_sc, want_sc
 
 
-@pytest.mark.parametrize("page_len", [64, 128])
+@pytest.mark.parametrize("page_len", [16, 64, 128])
 def test_indexer_random_decode_bit_exact(page_len):
+    """Pages of 16 rows take the per-lane page-table reads; pages of >= 64
+    rows the scalar page-row reads (a 64-position round spans <= 2 pages)."""
     announce(f"indexer random decode page_len={page_len}")
     rng = np.random.default_rng(page_len)
     ctx = [0, 5, 127, 128, 2047, 2048, 5000, 9999]
