@@ -98,6 +98,14 @@ constexpr float kExpBias = 1059208216.0f;
 // (a - b + c) + F*((b - 2c) + c*F).
 constexpr double kExpQa = 1.6501418352127075, kExpQb = -0.37554836273193359,
                  kExpQc = 0.38696467876434326;
+// P.V takes P as bf16 hi parts; a tile whose weight sum exceeds this share
+// of the row's running l (l after the tile) also takes the lo parts
+// p - bf16(p).  The row's final share of a tile can only be smaller (later
+// tiles rescale the tile and l alike and add to l), so leaving the lo parts
+// out of a tile below the share moves the output by at most
+// 2^-9 * kLoShare * max|v|.
+constexpr float kLoShare = 0x1p-7f;
+
 __device__ __forceinline__ float fexp_fused_t(float t) {
   const int32_t i = static_cast<int32_t>(t);
   const float F = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u);
@@ -117,10 +125,12 @@ __device__ __forceinline__ float fexp_fused(float x) {
 // score -1e30 and enter l only.  The in-lane sum of the 8 weights comes
 // first, then lane ^32's (the same 16 weights as the reference's halving
 // tree, added in another order).  Maxima use v_max_f32 (the scores are
-// finite for finite inputs).
+// finite for finite inputs).  big: the tile's weight sum exceeds kLoShare of
+// the updated l.
 template <bool kMasked>
 __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, int half,
-                                             float& m, float& l, float& corr, float (&w)[8]) {
+                                             float& m, float& l, float& corr, float (&w)[8],
+                                             bool& big) {
   float sc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -145,6 +155,7 @@ __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, in
     l = any ? l * c + ts : l;
     m = any ? m_new : m;
     corr = any ? c : 1.0f;
+    big = any && ts > kLoShare * l;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int key = 8 * (i >> 2) + 4 * half + (i & 3);
@@ -154,6 +165,7 @@ __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, in
     l = l * c + ts;
     m = m_new;
     corr = c;
+    big = ts > kLoShare * l;
 #pragma unroll
     for (int i = 0; i < 8; ++i) w[i] = e[i];
   }
@@ -366,25 +378,26 @@ void prefill_full_mfma_kernel(
   // Online softmax of the pair's two tiles; tile_key0 is the first key of
   // tile a.  Tiles past the wave's last row are skipped (corr 1, weights 0).
   auto softmax_pair = [&](const f32x16_t& sblk, int tile_key0, bool masked, float (&w)[2][8],
-                          float (&corr)[2]) {
+                          float (&corr)[2], bool (&big)[2]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       float sv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) sv[i] = sblk[8 * u + i];
       if (!masked) {
-        softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u]);
+        softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u], big[u]);
       } else {
         corr[u] = 1.0f;
+        big[u] = false;
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[u][i] = 0.0f;
         const int tk = tile_key0 + 16 * u;
         if (tk < wave_count) {  // wave-uniform
           if (tk + 16 <= wave_min) {
-            softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u]);
+            softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u], big[u]);
           } else {
             const int valid = min(16, max(0, count - tk));
-            softmax_tile<true>(sv, valid, half, m, l, corr[u], w[u]);
+            softmax_tile<true>(sv, valid, half, m, l, corr[u], w[u], big[u]);
           }
         }
       }
@@ -393,7 +406,8 @@ void prefill_full_mfma_kernel(
   // Fold of the pair and acc_stored += V^T P''^T:
   // acc*c_a*c_b + w_a*c_b V_a + w_b V_b = S' (acc_stored + (w_a*c_b V_a +
   // w_b V_b) / S'),  S' = S*c_a*c_b.
-  auto fold_pv = [&](const uint8_t* vl, int h, const float (&w)[2][8], const float (&corr)[2]) {
+  auto fold_pv = [&](const uint8_t* vl, int h, const float (&w)[2][8], const float (&corr)[2],
+                     const bool (&big)[2]) {
     float S_new = S * (corr[0] * corr[1]);
     if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
       // The accumulators are copied to VGPRs here, inside the rare branch
@@ -411,23 +425,19 @@ void prefill_full_mfma_kernel(
     S = S_new;
     const float inv_s = __builtin_amdgcn_rcpf(S_new);
     const float fs[2] = {corr[1] * inv_s, inv_s};
-    // P''^T of both tiles as bf16 hi + lo: k index 8*half + i holds the
-    // lane's value i.
-    bf16x8_t phi[2], plo[2];
+    // P''^T of both tiles in bf16 (hi): k index 8*half + i holds the lane's
+    // value i.  A tile's lo parts (p - bf16(p), about 8 more bits) follow in
+    // a pass of their own when some row of the wave has the tile's big flag
+    // (more than kLoShare of its running l).
+    bf16x8_t phi[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
-        const float p0 = w[u][i] * fs[u];
-        const float p1 = w[u][i + 1] * fs[u];
-        const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
-        const float r0 = p0 - static_cast<float>(hb[0]);
-        const float r1 = p1 - static_cast<float>(hb[1]);
-        const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+        const bf16x2_t hb =
+            __builtin_convertvector(f32x2_t{w[u][i] * fs[u], w[u][i + 1] * fs[u]}, bf16x2_t);
         phi[u][i] = hb[0];
         phi[u][i + 1] = hb[1];
-        plo[u][i] = lb[0];
-        plo[u][i + 1] = lb[1];
       }
     }
     // V^T operands in groups of four 32-dim blocks (8 transposing reads);
@@ -445,29 +455,50 @@ void prefill_full_mfma_kernel(
                                    __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     };
-    auto mfma_group = [&](int u, int b0, const bf16x8_t (&av)[4]) {
+    auto pass = [&](const bf16x8_t (&pp)[2]) {
+      auto mfma_group = [&](int u, int b0, const bf16x8_t (&av)[4]) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], phi[u], acc[b0 + b], 0, 0, 0);
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], plo[u], acc[b0 + b], 0, 0, 0);
+        for (int b = 0; b < 4; ++b)
+          acc[b0 + b] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], pp[u], acc[b0 + b], 0, 0, 0);
+      };
+      bf16x8_t ga[4], gb[4];
+      read_group(0, 0, ga);
+      read_group(0, 4, gb);
+      mfma_group(0, 0, ga);
+      read_group(1, 0, ga);
+      mfma_group(0, 4, gb);
+      read_group(1, 4, gb);
+      mfma_group(1, 0, ga);
+      mfma_group(1, 4, gb);
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     };
-    bf16x8_t ga[4], gb[4];
-    read_group(0, 0, ga);
-    read_group(0, 4, gb);
-    mfma_group(0, 0, ga);
-    read_group(1, 0, ga);
-    mfma_group(0, 4, gb);
-    read_group(1, 4, gb);
-    mfma_group(1, 0, ga);
-    mfma_group(1, 4, gb);
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    pass(phi);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (__builtin_amdgcn_ballot_w64(big[u]) != 0) {  // wave-uniform
+        bf16x8_t plo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
+        bf16x8_t ga[4], gb[4];
+        read_group(u, 0, ga);
+        read_group(u, 4, gb);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[b], plo, acc[b], 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[4 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[b], plo, acc[4 + b], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
+    }
   };
 
   // End of one iteration: the accumulators and the Q^T fragments stay in
@@ -497,12 +528,13 @@ void prefill_full_mfma_kernel(
     // pair-0 softmax (VALU), and the pair-0 PV (MFMA) under the pair-1
     // softmax.
     float w0[2][8], c0[2], w1[2][8], c1[2];
+    bool g0[2], g1[2];
     const f32x16_t s0 = qk(kl, 0);
     const f32x16_t s1 = qk(kl, 1);
-    softmax_pair(s0, 0, false, w0, c0);
-    fold_pv(vl, 0, w0, c0);
-    softmax_pair(s1, 0, false, w1, c1);
-    fold_pv(vl, 1, w1, c1);
+    softmax_pair(s0, 0, false, w0, c0, g0);
+    fold_pv(vl, 0, w0, c0, g0);
+    softmax_pair(s1, 0, false, w1, c1, g1);
+    fold_pv(vl, 1, w1, c1, g1);
     iteration_end(it, vnext);
   };
   // An iteration on the causal diagonal: per-tile masks.
@@ -514,9 +546,10 @@ void prefill_full_mfma_kernel(
     for (int h = 0; h < kBlocks; ++h) {
       if (key_base + 32 * h >= wave_count) break;  // wave-uniform
       float w[2][8], corr[2];
+      bool big[2];
       const f32x16_t sb = qk(kl, h);
-      softmax_pair(sb, key_base + 32 * h, true, w, corr);
-      fold_pv(vl, h, w, corr);
+      softmax_pair(sb, key_base + 32 * h, true, w, corr, big);
+      fold_pv(vl, h, w, corr, big);
     }
     iteration_end(it, vnext);
   };

@@ -54,6 +54,30 @@ def test_prefill_small_all_tokens():
     assert r["n_fail"] == 0 and r["n_nan"] == 0, r
 
 
+def test_prefill_diffuse_scores():
+    """Queries scaled by 1/16 (scores ~ N(0,1) instead of N(0,256)): attention
+    spreads over many keys, so most tiles stay under the lo-part share and
+    take only the bf16 hi parts of P."""
+    announce("prefill diffuse")
+    prefix, new = [0, 700, 3000, 4095], [64, 130, 200, 1]
+    case = make_prefill_case(5, prefix, new)
+    n = sum(new)
+    rng = np.random.default_rng(11)
+    qf = (rng.standard_normal(n * NUM_Q * HEAD_DIM) / 16.0).astype(np.float32)
+    u = qf.view(np.uint32).astype(np.uint64)
+    q = ((u + ((u >> 16) & 1) + 0x7FFF) >> 16).astype(np.uint16)
+    k = seeded_bf16(case.cache_rows * KV_STRIDE, 12)
+    v = seeded_bf16(case.cache_rows * KV_STRIDE, 13)
+    got = _prefill(case, n, to_dev(q), to_dev(k), to_dev(v))
+    ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=NUM_Q,
+                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
+                           cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n, cap=16,
+                           threads=8)
+    r = compare_bf16(got, ref)
+    print(f"  prefill diffuse: {r}", flush=True)
+    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+
+
 @pytest.mark.parametrize("page_len", [8, 128])
 def test_prefill_page_sizes(page_len):
     """Pages of 8 rows (the kernel's per-row staging path) and of 128 rows
