@@ -206,6 +206,19 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
   }
 }
 
+typedef unsigned int bq_u32x4_t __attribute__((ext_vector_type(4)));
+
+// Codes are streamed once per step: non-temporal loads, as for the bf16
+// cache, keep them from displacing the reused plan image, queries and scales.
+__device__ __forceinline__ uint4 load_codes16(const int8_t* p) {
+  const bq_u32x4_t v =
+      __builtin_nontemporal_load(reinterpret_cast<const bq_u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t load_codes4(const int8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
 __device__ __forceinline__ void unpack_i8x4(uint32_t w, float* f) {
   f[0] = static_cast<float>(static_cast<int8_t>(w & 0xFFu));
   f[1] = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xFFu));
@@ -311,12 +324,12 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
     const int64_t kslot = slot_of(p0 + min(tk, tile_len - 1));
     const int8_t* kr = kh + kslot * kv_stride;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d.k[i] = *reinterpret_cast<const uint4*>(kr + 64 * i);
+    for (int i = 0; i < 4; ++i) d.k[i] = load_codes16(kr + 64 * i);
     d.ks = k_scale[kslot * num_kv + g];
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
       const int64_t vslot = slot_of(p0 + min(t, tile_len - 1));
-      d.v[t] = *reinterpret_cast<const uint32_t*>(vh + vslot * kv_stride);
+      d.v[t] = load_codes4(vh + vslot * kv_stride);
       if constexpr (kTwoPages) {
         d.vs[t] = __int_as_float(sload(reinterpret_cast<const int32_t*>(v_scale) +
                                        vslot * num_kv + g));
