@@ -51,8 +51,6 @@ __device__ __forceinline__ TokenPos token_position(const int32_t* image, int t) 
 // (32p + 2j + 1, 32p + 2j) as odd*odd + even*even, lane j sums its
 // accumulators p = 0.. in order, then the 16-lane halving tree.
 // ---------------------------------------------------------------------------
-typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
-
 template <int D, int H, bool kPageRows>
 __global__ __launch_bounds__(256) void index_scores_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ index_q,
@@ -87,9 +85,6 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
     } else {
       slot = static_cast<int64_t>(tp.rows[pos >> shift]) + (pos & row_mask);
     }
-    // Plain loads: a 128-byte line of the key feeds eight consecutive load
-    // instructions of one lane, and with non-temporal loads it is fetched
-    // again for each of them (measured: the scores took twice as long).
     const uint4* kr = reinterpret_cast<const uint4*>(index_k + slot * D);
 #pragma unroll
     for (int c = 0; c < D / 8; ++c) kv[c] = kr[c];
@@ -448,11 +443,8 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     d.k2 = *reinterpret_cast<const uint4*>(kp + 64);
     d.k3 = *reinterpret_cast<const uint4*>(kp + 96);
     const int64_t vslot = prow + off0 + (vrow_l < tl ? vrow_l : 0);
-    {  // each wave reads only its own dims of V: streamed once, non-temporal
-      const u32x4_nt w = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(
-          reinterpret_cast<const uint8_t*>(vh + vslot * kv_stride + kSDW * dq) + vcol));
-      d.v0 = make_uint4(w.x, w.y, w.z, w.w);
-    }
+    d.v0 = *reinterpret_cast<const uint4*>(
+        reinterpret_cast<const uint8_t*>(vh + vslot * kv_stride + kSDW * dq) + vcol);
     return d;
   };
 
