@@ -55,6 +55,12 @@ def rope_tables(max_pos: int, half: int = 128, theta: float = 10000.0):
     return np.cos(ang).astype(np.float32).reshape(-1), np.sin(ang).astype(np.float32).reshape(-1)
 
 
+def layer_count(step_kv_bytes: int, limit: int = 64) -> int:
+    """Layer caches to rotate through so that consecutive steps touch at least
+    2 GiB of distinct K/V (8x the MI355X's 256 MB last-level cache)."""
+    return max(1, min(limit, -(-(2 << 30) // max(1, step_kv_bytes))))
+
+
 def _fill(t, seed, sid, outlier_every=0, scale=1.0):
     from inferno_amd._lib import check, lib
 
@@ -137,6 +143,18 @@ class DecodeBf16:
         self.vs = torch.empty_like(self.ks)
         for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
             _fill(t, self.seed * 16 + i, sid)
+        # Consecutive steps run on different layers' caches, as a model's
+        # decode step walks every layer before it returns to this one: a
+        # configuration whose step touches less than 2 GiB of K/V would
+        # otherwise find it in the 256 MB last-level cache (MALL) again.
+        self.layers = layer_count(self.kv_positions() * KV_STRIDE * 4)
+        self.kl = [(self.k, self.v)]
+        for j in range(1, self.layers):
+            kj, vj = torch.empty_like(self.k), torch.empty_like(self.v)
+            _fill(kj, self.seed * 16 + 32 * j, sid)
+            _fill(vj, self.seed * 16 + 32 * j + 1, sid)
+            self.kl.append((kj, vj))
+        self.layer = 0
         cos, sin = rope_tables(max(self.pos) + 2)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.plan = AttentionPlan(table, B, kind=self.kind, window=self.window,
@@ -171,6 +189,9 @@ class DecodeBf16:
 
     def launch(self, phase):
         A, p = self.A, self.plan
+        if phase == self.phases[0]:
+            self.layer = (self.layer + 1) % self.layers
+        kc, vc = self.kl[self.layer]
         if phase == "oproj":
             A.dispatch_gemm_cols(self.out, self.o_w, self.o_out, rows=HIDDEN,
                                  cols=NUM_Q * HEAD_DIM, seq_len=len(self.pos),
@@ -181,15 +202,15 @@ class DecodeBf16:
                                           head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
         elif phase == "append" and self.norm == "fused":
             A.dispatch_rms_norm_rope_cache_write(
-                p, self.q, self.ks, self.vs, self.k, self.v, self.qw, self.kw, self.cos,
+                p, self.q, self.ks, self.vs, kc, vc, self.qw, self.kw, self.cos,
                 self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128, pair_stride=128,
                 head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
         elif phase == "append":
-            A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
+            A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, kc, vc, self.cos,
                                         self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
                                         pair_stride=128, head_dim=HEAD_DIM)
         elif phase == "partials":
-            A.flash_partials_bf16(p, self.q, self.k, self.v, self.partials, self.ps,
+            A.flash_partials_bf16(p, self.q, kc, vc, self.partials, self.ps,
                                   num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
                                   kv_stride=KV_STRIDE)
         else:
@@ -222,7 +243,7 @@ class DecodeBf16:
                 "attended_positions": self.kv_positions(), "pool_pages": self.pool,
                 "page_len": PAGE_LEN, "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM,
                 "window": self.window or None, "cap": self.cap, "seed": self.seed,
-                "plan_items": self.plan.summary.num_items}
+                "plan_items": self.plan.summary.num_items, "layer_caches": self.layers}
 
     def cpu_baseline(self, budget_s):
         import torch
@@ -456,19 +477,37 @@ class SparseM3:
         self.block_idx = torch.empty(B * self.IH * self.TOPK, dtype=torch.int32, device=dev)
         self.out = torch.empty(B * self.NQ * self.HD, dtype=torch.int16, device=dev)
         self.cap = 0
+        # Layer caches rotated per step, as in the dense decode: the selected
+        # blocks are the same every step, and a model would read every other
+        # layer's index keys and K/V before this layer's again.
+        self.layers = layer_count(self.step_bytes(), limit=4)
+        bq = self.kv == "bq"
+        self.kl = [(self.index_k, self.k, self.v, self.ksc if bq else None,
+                    self.vsc if bq else None)]
+        for j in range(1, self.layers):
+            ik, kj, vj = (torch.empty_like(self.index_k), torch.empty_like(self.k),
+                          torch.empty_like(self.v))
+            for i, t in enumerate((ik, kj, vj)):
+                _fill(t, self.seed * 16 + 32 * j + i, sid)
+            ks = vs = None
+            if bq:
+                ks = torch.rand(rows * self.NKV, device=dev, generator=gen) * 4 + 0.5
+                vs = torch.rand(rows * self.NKV, device=dev, generator=gen) * 4 + 0.5
+            self.kl.append((ik, kj, vj, ks, vs))
+        self.layer = 0
 
     def launch(self, phase):
         A, p = self.A, self.plan
+        if phase == self.phases[0]:
+            self.layer = (self.layer + 1) % self.layers
+        ik, kc, vc, ks, vs = self.kl[self.layer]
         if phase == "indexer":
-            A.dispatch_lightning_indexer(p, self.index_q, self.index_k, self.block_idx,
-                                         self.scores)
+            A.dispatch_lightning_indexer(p, self.index_q, ik, self.block_idx, self.scores)
         elif self.kv == "bq":
-            A.dispatch_bq_block_sparse_attention(p, self.q, self.qb, self.fq, self.k, self.ksc,
-                                                 self.v, self.vsc, self.block_idx, self.out,
-                                                 cap=128)
+            A.dispatch_bq_block_sparse_attention(p, self.q, self.qb, self.fq, kc, ks, vc, vs,
+                                                 self.block_idx, self.out, cap=128)
         else:
-            A.dispatch_block_sparse_attention(p, self.q, self.k, self.v, self.block_idx,
-                                              self.out)
+            A.dispatch_block_sparse_attention(p, self.q, kc, vc, self.block_idx, self.out)
 
     def dominant_bytes(self) -> int:
         """Indexer: every cached position's index key, the queries, the score
@@ -499,7 +538,8 @@ class SparseM3:
                 "attended_positions_per_kv_head": self.attended(), "pool_pages": self.pool,
                 "page_len": self.PLEN, "num_q": self.NQ, "num_kv": self.NKV,
                 "head_dim": self.HD, "index_heads": self.IH, "block": self.BLOCK,
-                "topk_blocks": self.TOPK, "kv": self.kv, "seed": self.seed}
+                "topk_blocks": self.TOPK, "kv": self.kv, "seed": self.seed,
+                "layer_caches": self.layers}
 
     def cpu_baseline(self, budget_s):
         """The oracle's indexer + sparse attention on the first sequences of the
