@@ -211,8 +211,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
     for (int r = 0; r < G; ++r) {
       float mx = max_ref(s[0][r], s[1][r]);
       mx = max_ref(mx, dpp_f32<kDppRowRor8>(mx));
-      mx = max_ref(mx, shfl_xor_f32(mx, 16));
-      mx = max_ref(mx, shfl_xor_f32(mx, 32));
+      mx = pair_max32(pair_max16(mx));
       const float m_new = mx > m[r] ? mx : m[r];
       const float corr = fexp(max_ref(-87.0f, m[r] - m_new));
       w[0][r] = fexp(max_ref(-87.0f, s[0][r] - m_new));
@@ -220,8 +219,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
       // Halving tree over positions t = 8b + tk: (t, t+8) in-lane, then
       // tk ^ 4, tk ^ 2, tk ^ 1 = lane ^ 32, ^ 16, ^ 8.
       float ts = w[0][r] + w[1][r];
-      ts = ts + shfl_xor_f32(ts, 32);
-      ts = ts + shfl_xor_f32(ts, 16);
+      ts = pair_sum16(pair_sum32(ts));
       ts = ts + dpp_f32<kDppRowRor8>(ts);
       const float lc = l[r] * corr;
       l[r] = lc + ts;
@@ -315,8 +313,7 @@ __global__ __launch_bounds__(256) void merge_kernel(
       float sm = kNegBig;
       if (s0 + lane < n)
         sm = base[static_cast<int64_t>(s0 + lane) * partial_stride + m_off + h];
-#pragma unroll
-      for (int msk = 1; msk < 64; msk <<= 1) sm = max_ref(sm, shfl_xor_f32(sm, msk));
+      sm = wave_max_ref(sm);
       gm = max_ref(gm, sm);
     }
     float gl = 0.0f;
@@ -331,10 +328,7 @@ __global__ __launch_bounds__(256) void merge_kernel(
       float cv = fexp(max_ref(-87.0f, delta));
       cv = ls > 0.0f ? cv : 0.0f;
       float prod = ls * cv;
-      prod = prod + shfl_xor_f32(prod, 8);
-      prod = prod + shfl_xor_f32(prod, 4);
-      prod = prod + shfl_xor_f32(prod, 2);
-      prod = prod + shfl_xor_f32(prod, 1);
+      prod = tree16_sum(prod);
       const int cnt = min(64, n - s0);
       for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
       for (int j = 0; j < cnt; j += 8) {
@@ -458,9 +452,7 @@ __device__ __forceinline__ void merge_sliced_direct(const float* base, int64_t p
   float gm = kNegBig;
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
-    float sm = mv[c];
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) sm = max_ref(sm, shfl_xor_f32(sm, msk));
+    const float sm = wave_max_ref(mv[c]);
     gm = max_ref(gm, sm);
   }
   float gl = 0.0f;
@@ -471,10 +463,7 @@ __device__ __forceinline__ void merge_sliced_direct(const float* base, int64_t p
     float cv = fexp(max_ref(-87.0f, delta));
     cv = lv[c] > 0.0f ? cv : 0.0f;
     float prod = lv[c] * cv;
-    prod = prod + shfl_xor_f32(prod, 8);
-    prod = prod + shfl_xor_f32(prod, 4);
-    prod = prod + shfl_xor_f32(prod, 2);
-    prod = prod + shfl_xor_f32(prod, 1);
+    prod = tree16_sum(prod);
     const int cnt = min(64, n - 64 * c);
     for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
 #pragma unroll
@@ -548,8 +537,7 @@ __global__ __launch_bounds__(256) void merge_sliced_kernel(
       float sm = kNegBig;
       if (s0 + lane < n)
         sm = base[static_cast<int64_t>(s0 + lane) * partial_stride + m_off + h];
-#pragma unroll
-      for (int msk = 1; msk < 64; msk <<= 1) sm = max_ref(sm, shfl_xor_f32(sm, msk));
+      sm = wave_max_ref(sm);
       gm = max_ref(gm, sm);
     }
     float gl = 0.0f;
@@ -564,10 +552,7 @@ __global__ __launch_bounds__(256) void merge_sliced_kernel(
       float cv = fexp(max_ref(-87.0f, delta));
       cv = ls > 0.0f ? cv : 0.0f;
       float prod = ls * cv;
-      prod = prod + shfl_xor_f32(prod, 8);
-      prod = prod + shfl_xor_f32(prod, 4);
-      prod = prod + shfl_xor_f32(prod, 2);
-      prod = prod + shfl_xor_f32(prod, 1);
+      prod = tree16_sum(prod);
       const int cnt = min(64, n - s0);
       for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
       for (int j = 0; j < cnt; j += kAhead) {

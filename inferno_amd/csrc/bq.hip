@@ -375,15 +375,13 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
       float mx = s[r];
       mx = max_ref(mx, dpp_f32<kDppHalfMirror>(mx));  // position ^ 1
       mx = max_ref(mx, dpp_f32<kDppRowRor8>(mx));     // position ^ 2
-      mx = max_ref(mx, shfl_xor_f32(mx, 16));         // position ^ 4
-      mx = max_ref(mx, shfl_xor_f32(mx, 32));         // position ^ 8
+      mx = pair_max32(pair_max16(mx));                // position ^ 4, ^ 8
       const float m_new = mx > m[r] ? mx : m[r];
       const float corr = fexp(max_ref(-87.0f, m[r] - m_new));
       w[r] = fexp(max_ref(-87.0f, s[r] - m_new));
       // Halving tree over positions: ^8, ^4, ^2, ^1 = lane ^32, ^16, ^8, ^4.
       float ts = w[r];
-      ts = ts + shfl_xor_f32(ts, 32);
-      ts = ts + shfl_xor_f32(ts, 16);
+      ts = pair_sum16(pair_sum32(ts));
       ts = ts + dpp_f32<kDppRowRor8>(ts);
       ts = ts + dpp_f32<kDppHalfMirror>(ts);
       const float lc = l[r] * corr;
@@ -493,7 +491,6 @@ __global__ __launch_bounds__(256) void bq_block_quant_kernel(
   const uint16_t* s = src + base;
   float amax = 0.0f;
   for (int i = lane; i < block; i += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(s[i])));
-#pragma unroll
   for (int msk = 1; msk < 64; msk <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, msk));
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int8_t* d = x_i8 + base;

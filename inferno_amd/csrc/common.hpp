@@ -123,6 +123,55 @@ __device__ __forceinline__ int shfl_xor_i32(int v, int mask) {
 __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
+
+// gfx950 lane swaps.  v_permlane32_swap exchanges the upper 32 lanes of its
+// first operand with the lower 32 lanes of its second; v_permlane16_swap the
+// odd 16-lane rows of the first with the even rows of the second.  With x as
+// both operands the two results hold the two members of each (lane,
+// lane ^ 32) or (lane, lane ^ 16) pair, lower lane first, in both lanes of
+// the pair.  A commutative op on them therefore gives, bit for bit, what
+// x op shfl_xor(x, 32 | 16) gives, as one VALU operation instead of an LDS
+// permute round trip.
+constexpr int kDppRowRor4 = 0x124;  // lane i <- (i+4)%16 within 16 lanes
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_sum16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return max_ref(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_max16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return max_ref(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Max over the 64 lanes (exact in any pairing order): quad swaps, the
+// 8-lane mirror, the 16-lane rotate by 8, then the two lane swaps.
+__device__ __forceinline__ float wave_max_ref(float x) {
+  x = max_ref(x, dpp_f32<kDppXor1>(x));
+  x = max_ref(x, dpp_f32<kDppXor2>(x));
+  x = max_ref(x, dpp_f32<kDppHalfMirror>(x));
+  x = max_ref(x, dpp_f32<kDppRowRor8>(x));
+  return pair_max32(pair_max16(x));
+}
+// x + x[lane ^ 8], then ^ 4, ^ 2, ^ 1 inside each 16-lane row (the halving
+// tree of a 16-wide SIMD reduce_add), on DPP.  After the ^ 8 step lanes i and
+// i ^ 8 hold the same bits, so the rotate by 4 reads a lane equal to i ^ 4;
+// the quad swaps are exact.  Same operands, same order as the shuffles.
+__device__ __forceinline__ float tree16_sum(float x) {
+  x = x + dpp_f32<kDppRowRor8>(x);
+  x = x + dpp_f32<kDppRowRor4>(x);
+  x = x + dpp_f32<kDppXor2>(x);
+  return x + dpp_f32<kDppXor1>(x);
+}
 __device__ __forceinline__ int uniform_i32(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
