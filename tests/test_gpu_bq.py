@@ -120,6 +120,7 @@ def test_reference_parity_schedule():
             pair_stride=bq.PAIR_STRIDE)
         r = compare_bf16(got, ref)
         assert r["n_fail"] == 0 and r["n_nan"] == 0, (step, r)
+        assert np.array_equal(got, ref), (step, r)  # bit-exact, as in the batched test
         worst_or = max(worst_or, r["max_abs"])
         worst_ref = max(worst_ref, bq.check_step(tok_seq, tok_pos, spec, q_i8, fq, state.k,
                                                  state.ks, state.v, state.vs, got))
@@ -199,6 +200,9 @@ def test_bq_batched_decode_with_outliers(cap):
     r = compare_bf16(got, ref)
     print(f"  bq decode cap={cap}: {r}", flush=True)
     assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    # Integer scores, the reference's softmax steps and summation orders, and
+    # the merge's batch-of-16 halving tree: the outputs are the oracle's bits.
+    assert np.array_equal(got, ref), r
 
 
 @pytest.mark.parametrize("cols,block,rows", [(8 * 256, 256, 37), (4 * 512, 512, 5),
