@@ -926,10 +926,13 @@ int32_t ifr_bq_attn_prep(const void* image_dev, const int64_t* info,
   if (!image_dev || !q_src || !k_src || !v_src || !q_norm || !k_norm || !q_i8 || !qi_bias ||
       !f_q || !k_cache || !k_scale || !v_cache || !v_scale || !cos_table || !sin_table)
     return fail(IFR_EINVAL, "null pointer");
-  if (head_dim != 256) return fail(IFR_EUNSUPPORTED, "bq prep is compiled for head_dim 256");
-  if (rope_half <= 0 || rope_half % 4 != 0 || rope_half > pair_stride ||
-      pair_stride + rope_half > head_dim || pair_stride % 4 != 0)
-    return fail(IFR_EINVAL, "bad rope geometry");
+  if (head_dim != 256 && head_dim != 512)
+    return fail(IFR_EUNSUPPORTED, "bq prep is compiled for head_dim 256 and 512");
+  const int64_t epl = head_dim / 64;  // elements per lane of the prep kernel
+  if (rope_half <= 0 || rope_half % epl != 0 || rope_half > pair_stride ||
+      pair_stride + rope_half > head_dim || pair_stride % epl != 0)
+    return fail(IFR_EINVAL, "bad rope geometry (rope_half and pair_stride must be multiples "
+                "of head_dim/64)");
   if (num_q <= 0 || num_kv <= 0) return fail(IFR_EINVAL, "bad head counts");
   st = check_geometry(info, page_shift, row_mask, page_mask);
   if (st) return st;
@@ -961,8 +964,9 @@ int32_t bq_attention(const void* image_dev, const int64_t* info, const void* q_i
   if (st) return st;
   st = check_attention_shapes(num_q, num_kv, head_dim, partial_stride, kv_stride, 1);
   if (st) return st;
-  if (head_dim != 256 || num_q / num_kv != 2)
-    return fail(IFR_EUNSUPPORTED, "bq attention is compiled for head_dim 256, gqa 2");
+  if (!((head_dim == 256 && num_q / num_kv == 2) || (head_dim == 512 && num_q / num_kv == 8)))
+    return fail(IFR_EUNSUPPORTED,
+                "bq attention is compiled for head_dim 256 with gqa 2 and head_dim 512 with gqa 8");
   if (!image_dev || !q_i8 || !qi_bias || !f_q || !k_base || !k_scale || !v_base ||
       !v_scale || !output || !partials)
     return fail(IFR_EINVAL, "null pointer");

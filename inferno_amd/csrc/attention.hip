@@ -614,7 +614,8 @@ hipError_t launch_partials(const int32_t* image, int num_items, const void* q,
 }  // namespace
 
 bool attention_shape_supported(int head_dim, int gqa) {
-  return (head_dim == 256 || head_dim == 512) && (gqa == 1 || gqa == 2);
+  return ((head_dim == 256 || head_dim == 512) && (gqa == 1 || gqa == 2)) ||
+         (head_dim == 512 && gqa == 8);
 }
 
 hipError_t launch_merge_stripes(const float* partials, void* output, int64_t ps,
@@ -663,6 +664,9 @@ hipError_t launch_partials_bf16(const int32_t* image, int num_items,
                                 PagedGeom geom, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   const int gqa = num_q / num_kv;
+  if (head_dim == 512 && gqa == 8)
+    return launch_partials_wide_bf16(image, num_items, q, k, v, partials, ps, num_q, num_kv,
+                                     kv_stride, geom, stream);
   if (head_dim == 256 && gqa == 2)
     return launch_partials<256, 2>(image, num_items, q, k, v, partials, ps,
                                    num_q, num_kv, kv_stride, geom, stream);

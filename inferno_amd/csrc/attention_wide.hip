@@ -1,0 +1,354 @@
+// Split-KV partials for Gemma-4's full-attention layers: head_dim 512 with 8 q
+// heads per kv head (16 q / 2 kv heads, modeling/gemma4_common.mojo:14-20,
+// called through dispatch_full_attention and dispatch_bq_full_attention at
+// modeling/gemma_4_moe.mojo:470-476 and modeling/gemma_4_moe_bq.mojo:593-601),
+// for bf16 and butterquant int8 KV.
+//
+// One wave owns one (work item, kv head) and walks the item in the
+// reference's 16-position tiles from its first position (FlashAttentionKernel,
+// kernels/flash_attention.mojo:44-54; BqFlashAttentionKernel,
+// butterquant_kernels/attention.mojo:128-161), one online-softmax update per
+// tile per q head (process_kv_tile, kernels/attention_ops.mojo:193-253;
+// bq_process_kv_tile, butterquant_kernels/attention.mojo:27-102).
+//
+// Eight q heads share every K and V load:
+//   Scores  S (16 positions x 16 columns) = K . Q^T on MFMA, columns 8..15
+//           repeating heads 0..7.  bf16: v_mfma_f32_16x16x32_bf16, 16 steps
+//           over the 512 dims (products exact in f32).  int8:
+//           v_mfma_i32_16x16x64_i8, 8 steps; sum k*q is exact, and with
+//           128 * sum q it is the reference's VNNI raw dot, so the bq scores
+//           are the reference's bit for bit.  Lane l holds S[position
+//           4*(l/16) + j][head l%16], j = 0..3; the A operand of step s is
+//           16 bytes of the key row of position l%16 at byte 64*s + 16*(l/16),
+//           so one load instruction reads 64 contiguous bytes of 16 rows.
+//   Softmax per head in that layout: the tile max over the lane's 4 values
+//           and the lane ^ 16 / ^ 32 swaps; the weight sum in the halving tree
+//           of SIMD.reduce_add over positions (t, t+8) = lane ^ 32, (t, t+4) =
+//           lane ^ 16, then (j, j+2), (j, j+1) in the lane.
+//   P.V     on VALU: lane L owns output dims 8L..8L+7 of all 8 heads (64
+//           accumulators) and adds fma(v, w, acc) in position order, the
+//           reference's per-element order; each weight reaches every lane with
+//           v_readlane.  The V row of a position (1 KiB bf16 or 512 B int8) is
+//           one load instruction.
+#include <type_traits>
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ifr {
+namespace {
+
+constexpr int kWD = 512;                // head_dim
+constexpr int kWG = 8;                  // q heads per kv head
+constexpr int kWQPitch = 2 * kWD + 16;  // bytes per staged bf16 q row in LDS
+
+typedef __bf16 wbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float wf32x4_t __attribute__((ext_vector_type(4)));
+typedef int wi32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int wu32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int wu32x2_t __attribute__((ext_vector_type(2)));
+
+// K/V are streamed once per step (non-temporal, as in the other decode
+// kernels).
+__device__ __forceinline__ uint4 wide_load16(const uint8_t* p) {
+  const wu32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const wu32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 wide_load8(const uint8_t* p) {
+  const wu32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const wu32x2_t*>(p));
+  return make_uint2(v.x, v.y);
+}
+
+template <bool kBq>
+struct WideTile {
+  static constexpr int kRow = kBq ? kWD : 2 * kWD;  // bytes of one head's row
+  static constexpr int kSteps = kRow / 64;          // MFMA k-steps, 16 B per lane
+  using VT = typename std::conditional<kBq, uint2, uint4>::type;
+  uint4 k[kSteps];
+  VT v[kTile];
+  float ks[4], vs[4];  // bq: scales of positions 4*(l/16) + j
+};
+
+__device__ __forceinline__ void unpack8(const uint4& w, float* f) {
+  f[0] = bf16_lo(w.x);
+  f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y);
+  f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z);
+  f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w);
+  f[7] = bf16_hi(w.w);
+}
+__device__ __forceinline__ void unpack8(const uint2& w, float* f) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    f[b] = static_cast<float>(static_cast<int8_t>(w.x >> (8 * b)));
+    f[4 + b] = static_cast<float>(static_cast<int8_t>(w.y >> (8 * b)));
+  }
+}
+
+template <bool kBq, bool kTwoPages>
+__global__ __launch_bounds__(64) void flash_partial_wide_kernel(
+    const int32_t* __restrict__ image, const uint8_t* __restrict__ q,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const uint8_t* __restrict__ kc, const float* __restrict__ k_scale,
+    const uint8_t* __restrict__ vc, const float* __restrict__ v_scale,
+    float* __restrict__ partials, int64_t partial_stride, int num_q, int num_kv,
+    int64_t row_bytes, int shift, int row_mask, int page_mask) {
+  using Tile = WideTile<kBq>;
+  constexpr int kRow = Tile::kRow;
+  constexpr int kSteps = Tile::kSteps;
+  constexpr int kVB = kRow / 64;  // value bytes per lane per position
+  using VT = typename Tile::VT;
+  __shared__ __align__(16) uint8_t qs[kBq ? 16 : kWG * kWQPitch];
+
+  const int lane = threadIdx.x;
+  const int g = blockIdx.y;
+  const int32_t* item = image + sload(image + kHdrOffItems) + blockIdx.x * kItemWords;
+  const int q_row = sload(item);
+  const int run = sload(item + 1);
+  const int start_pos = sload(item + 2);
+  const int start = sload(item + 3);
+  const int end = sload(item + 4);
+  const int stripe = sload(item + 5);
+  const int32_t* rows = image + sload(image + kHdrOffRows) +
+                        sload(image + sload(image + kHdrOffRuns) + run * 4 + 2);
+
+  const int r16 = lane & 15;
+  const int qd = lane >> 4;
+  const int hq = r16 & (kWG - 1);  // q head of the lane's score column
+  const int64_t qh = static_cast<int64_t>(q_row) * num_q + g * kWG + hq;
+
+  // ---- the B operand of the scores ----
+  uint4 qv[kBq ? kSteps : 1];
+  int qsum128 = 0;
+  float qbias = 0.0f, fq = 0.0f;
+  if constexpr (kBq) {
+    const uint8_t* qp = q + qh * kWD + 16 * qd;
+    int qs4 = 0;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      qv[s] = *reinterpret_cast<const uint4*>(qp + 64 * s);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].x), 0x01010101, qs4, false);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].y), 0x01010101, qs4, false);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].z), 0x01010101, qs4, false);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].w), 0x01010101, qs4, false);
+    }
+    // The four lane groups hold disjoint quarters of the head's codes.
+    qs4 = qs4 + __shfl_xor(qs4, 16);
+    qs4 = qs4 + __shfl_xor(qs4, 32);
+    qsum128 = 128 * qs4;
+    qbias = qi_bias[qh];
+    fq = f_q[qh];
+  } else {
+    // Stage the group's 8 q rows in LDS; lane (head lane/8, chunks lane%8 +
+    // 8i) copies 16 bytes at a time.
+    const uint8_t* qg = q + (static_cast<int64_t>(q_row) * num_q + g * kWG) * (2 * kWD);
+    const int sh = lane >> 3;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = (lane & 7) + 8 * i;
+      *reinterpret_cast<uint4*>(qs + sh * kWQPitch + 16 * c) =
+          *reinterpret_cast<const uint4*>(qg + sh * (2 * kWD) + 16 * c);
+    }
+    __syncthreads();
+  }
+  const float inv127 = 1.0f / 127.0f;
+  const float inv127sq = inv127 * inv127;
+
+  const uint8_t* kh = kc + static_cast<int64_t>(g) * kRow + 16 * qd;
+  const uint8_t* vh = vc + static_cast<int64_t>(g) * kRow + kVB * lane;
+
+  float m = kNegBig;  // state of head hq (the same in the lanes of a column)
+  float lsum = 0.0f;
+  float acc[kWG][8];
+#pragma unroll
+  for (int h = 0; h < kWG; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+
+  // One tile's loads, branch-free: a position past the tile reloads the
+  // tile's first row (its score is masked, its value skipped).  kTwoPages
+  // (pages of >= 16 positions): a tile spans at most two pages, whose rows
+  // come from two scalar loads.
+  auto load_tile = [&](int pos0, int tile_len) {
+    Tile d;
+    const int p0 = start_pos + pos0;
+    const int pg0 = p0 >> shift;
+    int64_t ra = 0, rb = 0;
+    if constexpr (kTwoPages) {
+      const int pg1 = (p0 + tile_len - 1) >> shift;
+      ra = sload(rows + (pg0 & page_mask));
+      rb = pg1 != pg0 ? sload(rows + (pg1 & page_mask)) : ra;
+    }
+    auto slot_of = [&](int t) -> int64_t {
+      const int p = p0 + (t < tile_len ? t : 0);
+      if constexpr (kTwoPages) {
+        return ((p >> shift) == pg0 ? ra : rb) + (p & row_mask);
+      } else {
+        return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+      }
+    };
+    const uint8_t* kr = kh + slot_of(r16) * row_bytes;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) d.k[s] = wide_load16(kr + 64 * s);
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      const uint8_t* vr = vh + slot_of(t) * row_bytes;
+      if constexpr (kBq) {
+        d.v[t] = wide_load8(vr);
+      } else {
+        d.v[t] = wide_load16(vr);
+      }
+    }
+    if constexpr (kBq) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t sl = slot_of(4 * qd + j) * num_kv + g;
+        d.ks[j] = k_scale[sl];
+        d.vs[j] = v_scale[sl];
+      }
+    }
+    // Keep every load of the tile ahead of the math: one round trip a tile.
+    __builtin_amdgcn_sched_barrier(0);
+    return d;
+  };
+
+  for (int pos0 = start; pos0 < end; pos0 += kTile) {
+    const int tile_len = min(kTile, end - pos0);
+    const Tile d = load_tile(pos0, tile_len);
+
+    // ---- scores: lane holds positions 4*qd + j of head hq ----
+    float sj[4];
+    if constexpr (kBq) {
+      wi32x4_t si = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s)
+        si = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(wi32x4_t, d.k[s]),
+                                                    __builtin_bit_cast(wi32x4_t, qv[s]), si,
+                                                    0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float sc = static_cast<float>(si[j] + qsum128) - qbias;
+        sc = sc * fq;
+        sc = sc * d.ks[j];
+        sc = sc * inv127sq;
+        sj[j] = 4 * qd + j < tile_len ? sc : kNegBig;
+      }
+    } else {
+      wf32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const uint4 qf = *reinterpret_cast<const uint4*>(qs + hq * kWQPitch + 64 * s + 16 * qd);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(wbf16x8_t, d.k[s]),
+                                                     __builtin_bit_cast(wbf16x8_t, qf), sc, 0,
+                                                     0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sj[j] = 4 * qd + j < tile_len ? sc[j] : kNegBig;
+    }
+
+    // ---- online softmax of head hq (online_softmax_tile) ----
+    float mx = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
+    mx = pair_max32(pair_max16(mx));
+    const float m_new = mx > m ? mx : m;
+    const float corr = fexp(max_ref(-87.0f, m - m_new));
+    float w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sj[j] - m_new));
+    float ws[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ws[j] = pair_sum16(pair_sum32(w[j]));
+    const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
+    const float lc = lsum * corr;
+    lsum = lc + wsum;
+    m = m_new;
+    if constexpr (kBq) {
+      // bq_process_kv_tile's value weights: (w * v_scale) / 127.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = w[j] * d.vs[j];
+        w[j] = a * inv127;
+      }
+    }
+
+    // ---- scale_unrolled, then P.V in position order ----
+#pragma unroll
+    for (int h = 0; h < kWG; ++h) {
+      const float ch = readlane_f32(corr, h);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] * ch;
+    }
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) {
+      if (t < tile_len) {  // wave-uniform
+        float vf[8];
+        unpack8(d.v[t], vf);
+#pragma unroll
+        for (int h = 0; h < kWG; ++h) {
+          const float wt = readlane_f32(w[t & 3], h + 16 * (t >> 2));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(vf[e], wt, acc[h][e]);
+        }
+      }
+    }
+  }
+
+  float* part = partials + static_cast<int64_t>(stripe) * partial_stride;
+#pragma unroll
+  for (int h = 0; h < kWG; ++h) {
+    float* dst = part + static_cast<int64_t>(g * kWG + h) * kWD + 8 * lane;
+    *reinterpret_cast<float4*>(dst) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    *reinterpret_cast<float4*>(dst + 4) =
+        make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+  }
+  if (lane < kWG) {
+    part[num_q * kWD + g * kWG + lane] = m;
+    part[num_q * kWD + num_q + g * kWG + lane] = lsum;
+  }
+}
+
+template <bool kBq>
+hipError_t launch_wide(const int32_t* image, int num_items, const void* q,
+                       const float* qi_bias, const float* f_q, const void* k,
+                       const float* k_scale, const void* v, const float* v_scale,
+                       float* partials, int64_t ps, int num_q, int num_kv,
+                       int64_t kv_stride, PagedGeom geom, hipStream_t stream) {
+  if (num_items <= 0) return hipSuccess;
+  const int64_t row_bytes = kv_stride * (kBq ? 1 : 2);
+  dim3 grid(num_items, num_kv);
+  const auto* qp = static_cast<const uint8_t*>(q);
+  const auto* kp = static_cast<const uint8_t*>(k);
+  const auto* vp = static_cast<const uint8_t*>(v);
+  if (geom.row_mask + 1 >= kTile) {
+    hipLaunchKernelGGL((flash_partial_wide_kernel<kBq, true>), grid, dim3(64), 0, stream,
+                       image, qp, qi_bias, f_q, kp, k_scale, vp, v_scale, partials, ps,
+                       num_q, num_kv, row_bytes, geom.shift, geom.row_mask, geom.page_mask);
+  } else {
+    hipLaunchKernelGGL((flash_partial_wide_kernel<kBq, false>), grid, dim3(64), 0, stream,
+                       image, qp, qi_bias, f_q, kp, k_scale, vp, v_scale, partials, ps,
+                       num_q, num_kv, row_bytes, geom.shift, geom.row_mask, geom.page_mask);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_partials_wide_bf16(const int32_t* image, int num_items, const void* q,
+                                     const void* k, const void* v, float* partials,
+                                     int64_t ps, int num_q, int num_kv, int64_t kv_stride,
+                                     PagedGeom geom, hipStream_t stream) {
+  return launch_wide<false>(image, num_items, q, nullptr, nullptr, k, nullptr, v, nullptr,
+                            partials, ps, num_q, num_kv, kv_stride, geom, stream);
+}
+
+hipError_t launch_partials_wide_bq(const int32_t* image, int num_items, const void* q_i8,
+                                   const float* qi_bias, const float* f_q, const void* k,
+                                   const float* k_scale, const void* v, const float* v_scale,
+                                   float* partials, int64_t ps, int num_q, int num_kv,
+                                   int64_t kv_stride, PagedGeom geom, hipStream_t stream) {
+  return launch_wide<true>(image, num_items, q_i8, qi_bias, f_q, k, k_scale, v, v_scale,
+                           partials, ps, num_q, num_kv, kv_stride, geom, stream);
+}
+
+}  // namespace ifr

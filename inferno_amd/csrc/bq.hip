@@ -3,41 +3,47 @@
 // attention (bq_process_kv_tile / BqFlashAttentionKernel, :27-167), whose
 // partials feed the shared log-sum-exp merge.
 //
-// Prep, one wave per head (D = 256, lane L owns elements 4L..4L+3):
+// Prep, one wave per head (D = 256 or 512, lane L owns elements EPL*L ..
+// EPL*L + EPL - 1, EPL = D/64):
 //   RMS     the reference's lane-wise chain over 16 AVX-512 lanes
 //           (butterquant/head_prep.mojo:9-16) is replayed exactly: lane
 //           j < 16 runs ssq_j = x_j^2, then fma(x_{16ri+j}, x_{16ri+j}, ssq_j)
-//           for ri = 1..15, and the 16 partial sums are tree-reduced.
+//           for ri = 1 .. D/16 - 1, and the 16 partial sums are tree-reduced.
 //   RoPE    partner elements arrive with ds_bpermute; no FMA contraction.
-//   FWHT    strides 1 and 2 inside the lane, 4..128 across lanes (xor 1..32);
+//   FWHT    strides below EPL inside the lane, the rest across lanes (xor 1..32);
 //           the lower element of each pair becomes a+b, the upper a-b, in the
 //           reference's stage order (butterquant/fwht.mojo:20-57), so the
 //           rotated values -- and with them the int8 codes -- are the
 //           reference's bit for bit.
 //   absmax  wave max, 127/amax, round-to-nearest-even, clamp [-128, 127].
-// Attention, one wave per (work item, kv head): 4 lanes per position, 16
+// Attention (head_dim 256, gqa 2; head_dim 512 with gqa 8 runs the kernel of
+// attention_wide.hip), one wave per (work item, kv head): 4 lanes per position, 16
 // positions per pass (one tile); integer scores with v_dot4_i32_i8 (exact),
 // scaled as (((float)dot * f_q) * k_scale) / 127^2 like the reference; PV with
 // lane L owning output dims 4L..4L+3 and fma in position order.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
 namespace ifr {
 namespace {
 
-constexpr int kBqD = 256;
+constexpr int kBqD = 256;  // head_dim of bq_partial_kernel
 
 __device__ __forceinline__ float bpermute_f32(float v, int src_lane) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
 }
 
-// Absmax int8 quantisation of the wave's 256 values (4 per lane); returns
-// amax and writes the lane's 4 codes packed little-endian into *codes.
+// Absmax int8 quantisation of the wave's 64 * EPL values (EPL per lane);
+// returns amax and writes the lane's EPL codes packed little-endian into
+// codes[EPL / 4].
+template <int EPL>
 __device__ __forceinline__ float absmax_quantize(const float* r, uint32_t* codes,
                                                  int* qsum) {
   float vmax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < EPL; ++e) {
     const float a = fabsf(r[e]);
     vmax = a > vmax ? a : vmax;
   }
@@ -49,54 +55,60 @@ __device__ __forceinline__ float absmax_quantize(const float* r, uint32_t* codes
   float amax = vmax;
   if (amax < 1e-10f) amax = 1e-10f;
   const float inv = 127.0f / amax;
-  uint32_t packed = 0;
   int s = 0;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float v = rintf(r[e] * inv);
-    v = v < -128.0f ? -128.0f : v;
-    v = v > 127.0f ? 127.0f : v;
-    const int qi = static_cast<int>(v);
-    s += qi;
-    packed |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * e);
+  for (int w = 0; w < EPL / 4; ++w) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = rintf(r[4 * w + e] * inv);
+      v = v < -128.0f ? -128.0f : v;
+      v = v > 127.0f ? 127.0f : v;
+      const int qi = static_cast<int>(v);
+      s += qi;
+      packed |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * e);
+    }
+    codes[w] = packed;
   }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) s += shfl_xor_i32(s, m);
-  *codes = packed;
   *qsum = s;
   return amax;
 }
 
-// fwht_apply over 256 values held 4 per lane.
-__device__ __forceinline__ void fwht256(float* r, int lane) {
-  {  // stride 1
-    const float a0 = r[0], b0 = r[1], a1 = r[2], b1 = r[3];
-    r[0] = a0 + b0;
-    r[1] = a0 - b0;
-    r[2] = a1 + b1;
-    r[3] = a1 - b1;
-  }
-  {  // stride 2
-    const float a0 = r[0], b0 = r[2], a1 = r[1], b1 = r[3];
-    r[0] = a0 + b0;
-    r[2] = a0 - b0;
-    r[1] = a1 + b1;
-    r[3] = a1 - b1;
+// fwht_apply over 64 * EPL values held EPL per lane (element EPL*lane + e):
+// strides below EPL inside the lane, the rest across lanes (xor 1 .. 32), in
+// the reference's stage order; the lower element of each pair becomes a + b,
+// the upper a - b.
+template <int EPL>
+__device__ __forceinline__ void fwht_wave(float* r, int lane) {
+#pragma unroll
+  for (int st = 1; st < EPL; st <<= 1) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      if (e & st) continue;
+      const float a = r[e], b = r[e + st];
+      r[e] = a + b;
+      r[e + st] = a - b;
+    }
   }
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {  // strides 4 .. 128
+  for (int m = 1; m < 64; m <<= 1) {  // strides EPL .. 32 * EPL
     const bool upper = (lane & m) != 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < EPL; ++e) {
       const float p = shfl_xor_f32(r[e], m);
       r[e] = upper ? (p - r[e]) : (r[e] + p);
     }
   }
-  const float sc = static_cast<float>(1.0 / static_cast<double>(sqrtf(256.0f)));
+  const float sc = static_cast<float>(1.0 / static_cast<double>(sqrtf(64.0f * EPL)));
 #pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = r[e] * sc;
+  for (int e = 0; e < EPL; ++e) r[e] = r[e] * sc;
 }
 
+// One wave per head; head_dim D = 64 * EPL, lane L owns elements
+// EPL*L .. EPL*L + EPL - 1.
+template <int EPL>
 __global__ __launch_bounds__(256) void bq_prep_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q_src,
     const uint16_t* __restrict__ k_src, const uint16_t* __restrict__ v_src,
@@ -108,6 +120,8 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
     const float* __restrict__ sin_table, int num_q, int num_kv, int shift,
     int row_mask, int page_mask, int rope_half, int pair_stride, float sqrt_n,
     float n_eps) {
+  constexpr int D = 64 * EPL;
+  using Raw = typename std::conditional<EPL == 4, uint2, uint4>::type;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int tok = blockIdx.x;
@@ -119,7 +133,7 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
   const float* sin_row = sin_table + static_cast<int64_t>(pos) * rope_half;
   const int64_t slot =
       static_cast<int64_t>(rows[(pos >> shift) & page_mask]) + (pos & row_mask);
-  const int64_t kv_stride = static_cast<int64_t>(num_kv) * kBqD;
+  const int64_t kv_stride = static_cast<int64_t>(num_kv) * D;
   const float inv_sqrt_n = 1.0f / sqrt_n;
   const int n_heads = num_q + 2 * num_kv;
 
@@ -128,10 +142,18 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
     const bool is_k = !is_q && hh < num_q + num_kv;
     const int h = is_q ? hh : (is_k ? hh - num_q : hh - num_q - num_kv);
     const uint16_t* src =
-        is_q ? q_src + (static_cast<int64_t>(tok) * num_q + h) * kBqD
-             : (is_k ? k_src : v_src) + (static_cast<int64_t>(tok) * num_kv + h) * kBqD;
-    const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * lane);
-    float r[4] = {bf16_lo(raw.x), bf16_hi(raw.x), bf16_lo(raw.y), bf16_hi(raw.y)};
+        is_q ? q_src + (static_cast<int64_t>(tok) * num_q + h) * D
+             : (is_k ? k_src : v_src) + (static_cast<int64_t>(tok) * num_kv + h) * D;
+    float r[EPL];
+    {
+      const Raw raw = *reinterpret_cast<const Raw*>(src + EPL * lane);
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw);
+#pragma unroll
+      for (int i = 0; i < EPL / 2; ++i) {
+        r[2 * i] = bf16_lo(w[i]);
+        r[2 * i + 1] = bf16_hi(w[i]);
+      }
+    }
 
     if (is_q || is_k) {
       // head_inv_rms: lane j < 16 replays the reference's 16-lane register
@@ -141,7 +163,7 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
         const float x0 = bf16_to_f32(src[lane]);
         ssq = x0 * x0;
 #pragma unroll
-        for (int ri = 1; ri < 16; ++ri) {
+        for (int ri = 1; ri < D / 16; ++ri) {
           const float x = bf16_to_f32(src[16 * ri + lane]);
           ssq = fmaf(x, x, ssq);
         }
@@ -154,29 +176,30 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
       const float inv_rms = sqrt_n / sqrtf(total + n_eps);
       const uint16_t* gamma = is_q ? q_norm : k_norm;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float g = bf16_to_f32(gamma[4 * lane + e]);
+      for (int e = 0; e < EPL; ++e) {
+        const float g = bf16_to_f32(gamma[EPL * lane + e]);
         const float t = r[e] * inv_rms;
         r[e] = t * g;
       }
-      // RoPE pairs (j, pair_stride + j), j < rope_half.
-      const int e0 = 4 * lane;
+      // RoPE pairs (j, pair_stride + j), j < rope_half (both multiples of EPL,
+      // so a lane's elements are all rotated or all passed through).
+      const int e0 = EPL * lane;
       int partner = lane;
-      if (e0 < rope_half) partner = (e0 + pair_stride) >> 2;
-      else if (e0 >= pair_stride && e0 < pair_stride + rope_half) partner = (e0 - pair_stride) >> 2;
-      float pv[4];
+      if (e0 < rope_half) partner = (e0 + pair_stride) / EPL;
+      else if (e0 >= pair_stride && e0 < pair_stride + rope_half) partner = (e0 - pair_stride) / EPL;
+      float pv[EPL];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pv[e] = bpermute_f32(r[e], partner);
+      for (int e = 0; e < EPL; ++e) pv[e] = bpermute_f32(r[e], partner);
       if (e0 < rope_half) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < EPL; ++e) {
           const float cv = cos_row[e0 + e], sv = sin_row[e0 + e];
           const float a = r[e] * cv, b = pv[e] * sv;
           r[e] = a - b;
         }
       } else if (e0 >= pair_stride && e0 < pair_stride + rope_half) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < EPL; ++e) {
           const int j = e0 - pair_stride + e;
           const float cv = cos_row[j], sv = sin_row[j];
           const float c = r[e] * cv, d = pv[e] * sv;
@@ -185,23 +208,28 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
       }
     }
 
-    fwht256(r, lane);
-    uint32_t codes;
+    fwht_wave<EPL>(r, lane);
+    uint32_t codes[EPL / 4];
     int qsum;
-    const float amax = absmax_quantize(r, &codes, &qsum);
+    const float amax = absmax_quantize<EPL>(r, codes, &qsum);
+    int8_t* dst;
     if (is_q) {
-      *reinterpret_cast<uint32_t*>(q_i8 + (static_cast<int64_t>(tok) * num_q + h) * kBqD +
-                                   4 * lane) = codes;
+      dst = q_i8 + (static_cast<int64_t>(tok) * num_q + h) * D;
       if (lane == 0) {
         qi_bias[static_cast<int64_t>(tok) * num_q + h] = static_cast<float>(qsum) * 128.0f;
         f_q[static_cast<int64_t>(tok) * num_q + h] = amax * inv_sqrt_n;
       }
     } else if (is_k) {
-      *reinterpret_cast<uint32_t*>(k_cache + slot * kv_stride + h * kBqD + 4 * lane) = codes;
+      dst = k_cache + slot * kv_stride + h * D;
       if (lane == 0) k_scale[slot * num_kv + h] = amax;
     } else {
-      *reinterpret_cast<uint32_t*>(v_cache + slot * kv_stride + h * kBqD + 4 * lane) = codes;
+      dst = v_cache + slot * kv_stride + h * D;
       if (lane == 0) v_scale[slot * num_kv + h] = amax;
+    }
+    if constexpr (EPL == 4) {
+      *reinterpret_cast<uint32_t*>(dst + 4 * lane) = codes[0];
+    } else {
+      *reinterpret_cast<uint2*>(dst + 8 * lane) = make_uint2(codes[0], codes[1]);
     }
   }
 }
@@ -435,9 +463,9 @@ hipError_t launch_bq_attn_prep(const int32_t* image, int seq_len, const void* q_
                                PagedGeom geom, int head_dim, int rope_half,
                                int pair_stride, float sqrt_n, float n_eps,
                                hipStream_t stream) {
-  (void)head_dim;
   if (seq_len <= 0) return hipSuccess;
-  hipLaunchKernelGGL(bq_prep_kernel, dim3(seq_len), dim3(256), 0, stream, image,
+  auto kernel = head_dim == 512 ? bq_prep_kernel<8> : bq_prep_kernel<4>;
+  hipLaunchKernelGGL(kernel, dim3(seq_len), dim3(256), 0, stream, image,
                      static_cast<const uint16_t*>(q_src), static_cast<const uint16_t*>(k_src),
                      static_cast<const uint16_t*>(v_src), static_cast<const uint16_t*>(q_norm),
                      static_cast<const uint16_t*>(k_norm), static_cast<int8_t*>(q_i8),
@@ -455,7 +483,12 @@ hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_unit
                                float* partials, int64_t ps, int num_q, int num_kv,
                                int head_dim, int64_t kv_stride, PagedGeom geom,
                                hipStream_t stream, int8_t* q_out, float* q_scale) {
-  if (num_items > 0) {
+  if (num_items > 0 && head_dim == 512) {
+    hipError_t err = launch_partials_wide_bq(image, num_items, q_i8, qi_bias, f_q, k_base,
+                                             k_scale, v_base, v_scale, partials, ps, num_q,
+                                             num_kv, kv_stride, geom, stream);
+    if (err != hipSuccess) return err;
+  } else if (num_items > 0) {
     dim3 grid(num_items, (num_kv + 3) / 4);
     if (geom.row_mask + 1 >= kTile)
       hipLaunchKernelGGL((bq_partial_kernel<2, true>), grid, dim3(256), 0, stream, image,

@@ -30,6 +30,18 @@ hipError_t launch_partials_bf16(const int32_t* image_dev, int num_items,
                                 int head_dim, int64_t kv_stride, PagedGeom geom,
                                 hipStream_t stream);
 
+// The partials of Gemma-4's full-attention shape (head_dim 512, 8 q heads per
+// kv head), bf16 and butterquant int8 KV (attention_wide.hip).
+hipError_t launch_partials_wide_bf16(const int32_t* image, int num_items, const void* q,
+                                     const void* k, const void* v, float* partials,
+                                     int64_t ps, int num_q, int num_kv, int64_t kv_stride,
+                                     PagedGeom geom, hipStream_t stream);
+hipError_t launch_partials_wide_bq(const int32_t* image, int num_items, const void* q_i8,
+                                   const float* qi_bias, const float* f_q, const void* k,
+                                   const float* k_scale, const void* v, const float* v_scale,
+                                   float* partials, int64_t ps, int num_q, int num_kv,
+                                   int64_t kv_stride, PagedGeom geom, hipStream_t stream);
+
 // MFMA chunked prefill, full attention, head_dim 256, gqa 2: writes the
 // finalised output of every query block of a token plan.
 hipError_t launch_prefill_full_mfma(const int32_t* image_dev, int num_qblocks,

@@ -1,6 +1,6 @@
 """GPU parity of the bf16 decode and token-partitioned prefill routes for the
 other head shapes the kernels are built for: head_dim 256 and 512, GQA 1 and
-2 (attention_shape_supported).  Both merge kernels are reached: a unit of 32
+2, and head_dim 512 with GQA 8 (attention_shape_supported).  Both merge kernels are reached: a unit of 32
 or more splits takes merge_sliced_kernel, fewer take merge_kernel.  Outputs
 are within 1e-2 max-abs of the oracle (one bf16 spacing where |x| >= 2)."""
 import numpy as np
@@ -14,7 +14,7 @@ from tests.helpers import PAGE_LEN, compare_bf16, make_decode_case, make_prefill
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(16, 8, 512), (8, 8, 256), (8, 8, 512), (4, 4, 256)]
+SHAPES = [(16, 8, 512), (8, 8, 256), (8, 8, 512), (4, 4, 256), (16, 2, 512)]
 
 
 def _table(runs, rows) -> KVRunTable:
