@@ -187,6 +187,23 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
                            int64_t page_len, int64_t page_mask,
                            uint64_t stream);
 
+/* ifr_attention_bf16 without a partials argument: the partials live in a
+ * library-owned device array of IFR_STATIC_SCRATCH_BYTES per GPU (held from
+ * the library's first call on that GPU until the process ends), so the call
+ * allocates nothing, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  partial_stride is ifr_flash_partial_stride(
+ * num_q, head_dim); a plan whose info[3] stripes need more than the array
+ * returns IFR_ESPACE.  Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (two streams, or two host threads) race. */
+#define IFR_STATIC_SCRATCH_BYTES (32LL << 20)
+int32_t ifr_attention_bf16_noalloc(const void* image_dev, const int64_t* info,
+                                   const void* q, const void* k_base,
+                                   const void* v_base, void* output, int64_t num_q,
+                                   int64_t num_kv, int64_t head_dim,
+                                   int64_t kv_stride, int64_t page_len,
+                                   int64_t page_mask, uint64_t stream);
+
 /* The two phases of ifr_attention_bf16 as separate launches: the split-KV
  * partials (the FlashAttentionKernel fan-out of dispatch_flash_sliding /
  * dispatch_flash_full, kernels/attention_dispatch_kernels.mojo:116-134) and

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                             F32, F32, U64]),
     "ifr_attention_bf16": (I32, [VP, P_I64, VP, VP, VP, VP, VP, I64, I64, I64, I64,
                                  I64, I64, I64, I64, U64]),
+    "ifr_attention_bf16_noalloc": (I32, [VP, P_I64, VP, VP, VP, VP, I64, I64, I64, I64,
+                                         I64, I64, U64]),
     "ifr_flash_partials_bf16": (I32, [VP, P_I64, VP, VP, VP, VP, I64, I64, I64, I64, I64,
                                       I64, I64, I64, U64]),
     "ifr_merge_flash_partials": (I32, [VP, P_I64, VP, I64, VP, I64, I64, I64, U64]),

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <array>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -732,6 +733,63 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
                                      as_stream(stream)),
           "attention_bf16");
   return ok();
+}
+
+}  // extern "C"
+
+// ---- the no-allocation variant of ifr_attention_bf16 --------------------------
+// The partials live in a file-scope device array instead of a caller buffer.
+// `scratch` names a host-side stand-in in host code; the array's device
+// address, which differs per GPU, comes from hipGetSymbolAddress once per
+// device (with that device current) and is the only form passed to kernels.
+namespace {
+constexpr int64_t kStaticScratchBytes = IFR_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxScratchDevices] = {};
+
+int32_t static_scratch(void** out) {
+  int dev = 0;
+  IFR_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(IFR_EUNSUPPORTED, "device %d is beyond the %d devices with a static scratch",
+                dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    IFR_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(IFR_EHIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return IFR_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t ifr_attention_bf16_noalloc(const void* image_dev, const int64_t* info, const void* q,
+                                   const void* k_base, const void* v_base, void* output,
+                                   int64_t num_q, int64_t num_kv, int64_t head_dim,
+                                   int64_t kv_stride, int64_t page_len, int64_t page_mask,
+                                   uint64_t stream) {
+  int32_t st = check_info(info);
+  if (st) return st;
+  if (num_q <= 0 || head_dim <= 0 || num_q > 64 || head_dim > 4096)
+    return fail(IFR_EINVAL, "bad num_q or head_dim");
+  const int64_t ps = ifr_flash_partial_stride(num_q, head_dim);
+  const int64_t need = info[3] * ps * 4;
+  if (need > kStaticScratchBytes)
+    return fail(IFR_ESPACE,
+                "the plan's %lld partial stripes need %lld bytes; the static scratch holds %lld",
+                (long long)info[3], (long long)need, (long long)kStaticScratchBytes);
+  void* p = nullptr;
+  st = static_scratch(&p);
+  if (st) return st;
+  return ifr_attention_bf16(image_dev, info, q, k_base, v_base, output, p, kStaticScratchBytes,
+                            num_q, num_kv, head_dim, ps, kv_stride, page_len, page_mask,
+                            stream);
 }
 
 int32_t ifr_flash_partials_bf16(const void* image_dev, const int64_t* info,
