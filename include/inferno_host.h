@@ -222,9 +222,13 @@ int64_t ifr_scheduler_query(const ifr_scheduler* sched, int64_t what,
 /* The built schedule (schedule.mojo:29-90): slots int64 [n][6] = {seq_id,
  * request_id, base_pos, n_tokens, prompt_len, emit}, tokens int32 [sum of
  * n_tokens], copies int64 [m][5] = {pool, src_page, dst_page, pos_start,
- * pos_count}.  Sizes from IFR_SQ_NUM_*; any output may be NULL. */
+ * pos_count}.  Sizes from IFR_SQ_NUM_*; the caps count rows (slots, copies)
+ * and tokens; any output may be NULL.  IFR_ESPACE, with nothing written,
+ * when a cap is below the schedule's count. */
 int32_t ifr_scheduler_export_schedule(const ifr_scheduler* sched, int64_t* slots,
-                                      int32_t* tokens, int64_t* copies);
+                                      int64_t slots_cap, int32_t* tokens,
+                                      int64_t tokens_cap, int64_t* copies,
+                                      int64_t copies_cap);
 /* A request's tokens (prompt + generated) and generated tokens. */
 int32_t ifr_scheduler_export_request(const ifr_scheduler* sched,
                                      int64_t request_id, int32_t* tokens,

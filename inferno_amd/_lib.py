@@ -128,7 +128,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ifr_scheduler_absorb": (I32, [VP, VP, I64, U64]),
     "ifr_scheduler_discard_step": (I32, [VP]),
     "ifr_scheduler_query": (I64, [VP, I64, I64]),
-    "ifr_scheduler_export_schedule": (I32, [VP, VP, VP, VP]),
+    "ifr_scheduler_export_schedule": (I32, [VP, VP, I64, VP, I64, VP, I64]),
     "ifr_scheduler_export_request": (I32, [VP, I64, VP, I64, VP, I64]),
     "ifr_scheduler_export_pending": (I32, [VP, VP, I64, P_I64]),
     "ifr_bind_pool_run_table": (I32, [VP, I64, I64, I64, VP, I64, VP, I64, P_I64, P_I64]),

@@ -171,8 +171,14 @@ int32_t check_runs(const int32_t* runs, int64_t num_runs,
       return fail(IFR_EINVAL, "run %lld: rows [%lld, +%lld) outside base_rows[%lld]",
                   (long long)i, (long long)rows_off, (long long)page_count,
                   (long long)num_rows);
+    // Every run carries at least one token (a schedule slot feeds >= 1,
+    // modeling/kv_policy.mojo:105-123): the seq_len == 1 route plans run 0
+    // and the batched route one run per token, so an empty run would be
+    // planned over rows that belong to no token of the step.
     const int64_t n_tok = next - buf_start;
-    if (n_tok <= 0) continue;
+    if (n_tok <= 0)
+      return fail(IFR_EINVAL, "run %lld holds no token (buf_start %lld, next run at %lld)",
+                  (long long)i, (long long)buf_start, (long long)next);
     const int64_t hi_pos = base_pos + n_tok - 1;
     if (hi_pos > INT32_MAX / 2) return fail(IFR_EINVAL, "run %lld: position overflow", (long long)i);
     int64_t lo_pos = 0;

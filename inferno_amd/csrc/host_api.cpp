@@ -502,37 +502,44 @@ int64_t ifr_scheduler_query(const ifr_scheduler* s, int64_t what, int64_t arg) {
   });
 }
 
-int32_t ifr_scheduler_export_schedule(const ifr_scheduler* s, int64_t* slots, int32_t* tokens,
-                                      int64_t* copies) {
-  return guarded([&] {
-    need_ptr(s, "scheduler");
-    const auto& sc = sch(s)->schedule();
-    if (slots) {
-      for (size_t k = 0; k < sc.slots.size(); ++k) {
-        const auto& sl = sc.slots[k];
-        int64_t* o = slots + 6 * k;
-        o[0] = sl.seq_id;
-        o[1] = sl.request_id;
-        o[2] = sl.base_pos;
-        o[3] = sl.n_tokens;
-        o[4] = sl.prompt_len;
-        o[5] = sl.emit ? 1 : 0;
-      }
+int32_t ifr_scheduler_export_schedule(const ifr_scheduler* s, int64_t* slots, int64_t slots_cap,
+                                      int32_t* tokens, int64_t tokens_cap, int64_t* copies,
+                                      int64_t copies_cap) {
+  if (!s) return ifr::abi_fail(IFR_EINVAL, "scheduler is null");
+  const auto& sc = sch(s)->schedule();
+  // Every capacity is checked before anything is written.
+  if (slots && static_cast<int64_t>(sc.slots.size()) > slots_cap)
+    return ifr::abi_fail(IFR_ESPACE, "slots_cap too small");
+  if (tokens && static_cast<int64_t>(sc.tokens.size()) > tokens_cap)
+    return ifr::abi_fail(IFR_ESPACE, "tokens_cap too small");
+  if (copies && static_cast<int64_t>(sc.copies.size()) > copies_cap)
+    return ifr::abi_fail(IFR_ESPACE, "copies_cap too small");
+  if (slots) {
+    for (size_t k = 0; k < sc.slots.size(); ++k) {
+      const auto& sl = sc.slots[k];
+      int64_t* o = slots + 6 * k;
+      o[0] = sl.seq_id;
+      o[1] = sl.request_id;
+      o[2] = sl.base_pos;
+      o[3] = sl.n_tokens;
+      o[4] = sl.prompt_len;
+      o[5] = sl.emit ? 1 : 0;
     }
-    if (tokens && !sc.tokens.empty())
-      memcpy(tokens, sc.tokens.data(), sc.tokens.size() * sizeof(int32_t));
-    if (copies) {
-      for (size_t k = 0; k < sc.copies.size(); ++k) {
-        const auto& c = sc.copies[k];
-        int64_t* o = copies + 5 * k;
-        o[0] = c.pool;
-        o[1] = c.src_page;
-        o[2] = c.dst_page;
-        o[3] = c.pos_start;
-        o[4] = c.pos_count;
-      }
+  }
+  if (tokens && !sc.tokens.empty())
+    memcpy(tokens, sc.tokens.data(), sc.tokens.size() * sizeof(int32_t));
+  if (copies) {
+    for (size_t k = 0; k < sc.copies.size(); ++k) {
+      const auto& c = sc.copies[k];
+      int64_t* o = copies + 5 * k;
+      o[0] = c.pool;
+      o[1] = c.src_page;
+      o[2] = c.dst_page;
+      o[3] = c.pos_start;
+      o[4] = c.pos_count;
     }
-  });
+  }
+  return ifr::abi_ok();
 }
 
 int32_t ifr_scheduler_export_request(const ifr_scheduler* s, int64_t rid, int32_t* tokens,

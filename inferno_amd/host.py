@@ -478,7 +478,9 @@ class ContinuousBatchScheduler:
         slots = np.empty((max(ns, 1), 6), dtype=np.int64)
         toks = np.empty(max(nt, 1), dtype=np.int32)
         copies = np.empty((max(nc, 1), 5), dtype=np.int64)
-        check(lib().ifr_scheduler_export_schedule(self._h, _vp(slots), _vp(toks), _vp(copies)))
+        check(lib().ifr_scheduler_export_schedule(self._h, _vp(slots), slots.shape[0],
+                                                  _vp(toks), toks.size, _vp(copies),
+                                                  copies.shape[0]))
         return Schedule(
             [BatchSlot(int(r[0]), int(r[1]), int(r[2]), int(r[3]), int(r[4]), bool(r[5]))
              for r in slots[:ns]],
@@ -490,7 +492,8 @@ class ContinuousBatchScheduler:
         """The step's copies as int64 [n][5] (the ifr_prefix_copy_jobs input)."""
         nc = self._query("NUM_COPIES")
         copies = np.zeros((max(nc, 1), 5), dtype=np.int64)
-        check(lib().ifr_scheduler_export_schedule(self._h, None, None, _vp(copies)))
+        check(lib().ifr_scheduler_export_schedule(self._h, None, 0, None, 0, _vp(copies),
+                                                  copies.shape[0]))
         return copies[:nc]
 
     def absorb(self, emitted: Sequence[int], now: Optional[int] = None) -> None:

@@ -154,3 +154,24 @@ def test_plan_image_too_small_is_reported():
                                 case.base_rows.ctypes.data_as(_lib.P_I32), 1, 1, FULL, 0,
                                 PAGE_LEN, PAGE_LEN, case.cache_rows, 4, 4096, info)
     assert st == -4
+
+
+@pytest.mark.parametrize("layout", ["empty_first_single", "empty_middle_batched"])
+def test_planner_rejects_runs_without_tokens(layout):
+    """A run with no token would be planned over rows of no token of the
+    step (seq_len 1 plans run 0; the batched route plans one run per token):
+    the planner refuses it instead of letting the kernels read those rows."""
+    case = make_decode_case(6, [300, 700, 90])
+    runs = case.runs.copy()
+    if layout == "empty_first_single":
+        # Run 0 empty, run 1 holds the step's one token.
+        runs = runs[:2].copy()
+        runs[:, 0] = [0, 0]
+        seq_len = 1
+    else:
+        # Three runs over two tokens: run 1 is empty.
+        runs[:, 0] = [0, 1, 1]
+        seq_len = 2
+    st, _, _ = _plan(runs, case.base_rows, seq_len, FULL, 0, PAGE_LEN, case.cache_rows, 16,
+                     KV_STRIDE * 2)
+    assert st == -1 and "no token" in _lib.last_error()

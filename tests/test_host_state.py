@@ -405,3 +405,32 @@ def test_config3_ring_256_decode_steps_lockstep():
     wrapped = sum(ps.registry.length(sid) > ring_pages * ppp for sid in range(B))
     assert wrapped > B // 2, "most rings wrapped"
     assert ps.invariant_failures == (0, 0)
+
+
+def test_export_schedule_checks_every_capacity():
+    """ifr_scheduler_export_schedule refuses a slots, tokens or copies
+    capacity below the built schedule's count with IFR_ESPACE and writes
+    nothing, like the other exports."""
+    import ctypes as C
+
+    from inferno_amd._lib import lib
+
+    geo = P.BatchGeometry(4, 4, 64, [P.PagePoolSpec(8, 2, 2), P.PagePoolSpec(40, 0, 10)])
+    s = P.ContinuousBatchScheduler(PPP, geo, 64, [-1])
+    s.submit(list(range(10)), 3, False)
+    s.submit(list(range(20, 27)), 3, False)
+    assert s.build_schedule(1000)
+    ns, nt = s._query("NUM_SLOTS"), s._query("NUM_TOKENS")
+    assert ns == 2 and nt == 17
+    slots = np.full((ns, 6), -7, dtype=np.int64)
+    toks = np.full(nt, -7, dtype=np.int32)
+    vp = lambda a: a.ctypes.data_as(C.c_void_p)
+    f = lib().ifr_scheduler_export_schedule
+    assert f(s._h, vp(slots), ns - 1, vp(toks), nt, None, 0) == -4
+    assert f(s._h, vp(slots), ns, vp(toks), nt - 1, None, 0) == -4
+    assert (slots == -7).all() and (toks == -7).all(), "a refused export wrote"
+    assert f(s._h, vp(slots), ns, vp(toks), nt, None, 0) == 0
+    assert list(slots[:, 3]) == [10, 7] and list(toks[:10]) == list(range(10))
+    # With no copies in the schedule a zero copies capacity is enough.
+    copies = np.full((1, 5), -7, dtype=np.int64)
+    assert f(s._h, None, 0, None, 0, vp(copies), 0) == 0 and (copies == -7).all()
