@@ -6,7 +6,10 @@ Headline (default): config 2 of BASELINE.json -- one layer of batched paged
 decode for 64 sequences with contexts ~ U[512, 32768]: append one token per
 sequence (RoPE + paged cache write), split-KV flash-decode partials over every
 page, log-sum-exp merge.  --config 1, 3 and 5 run the other decode configs
-(single sequence, sliding ring, butterquant int8) the same way.
+(single sequence, sliding ring, butterquant int8) the same way, --config 4 the
+chunked prefill.  Widening rows: --config 6 (MiniMax-M3 sparse decode), 7 and
+8 (Gemma-4's full-attention layer, head_dim 512 with 16q/2kv, bf16 and bq),
+9 (copy-on-write page copy) and 10 (row gather).
 
 Inputs (KV pages, queries, RoPE tables, the plan image) are resident in HBM
 before the timed region; the plan is built once, as the reference binds its
@@ -33,8 +36,36 @@ NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 HIDDEN = 2816  # Gemma 4 26B-A4B hidden size: o_proj maps 16 x 256 -> 2816
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
-DEFAULT_CAP = {1: 128, 2: 512, 3: 384, 4: 16, 5: 2048, 6: 0}
+DEFAULT_CAP = {1: 128, 2: 512, 3: 384, 4: 16, 5: 2048, 6: 0, 7: 512, 8: 2048, 9: 0, 10: 0}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Gemma-4's two attention layer shapes (modeling/gemma4_common.mojo:10-20):
+# (num_q, num_kv, head_dim, rope_half, pair_stride).  BASELINE's configs 1-5
+# are the sliding-layer shape; the five full-attention layers are 16q/2kv at
+# head_dim 512 with 64 rotated pairs.
+SLIDING_SHAPE = (16, 8, 256, 128, 128)
+FULL_SHAPE = (16, 2, 512, 64, 256)
+# The GPU box allots 16 CPUs to a one-GPU job; the CPU baselines use that many
+# threads (the host may show more logical CPUs).
+CPU_SHARE = 16
+
+
+def host_cpu() -> dict:
+    """CPU model and counts of the host the CPU baseline runs on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "affinity_cpus": avail,
+            "threads": max(1, min(CPU_SHARE, avail))}
 
 
 def splitmix64(x: int) -> int:
@@ -68,8 +99,46 @@ def _fill(t, seed, sid, outlier_every=0, scale=1.0):
                                      outlier_every, scale, sid))
 
 
+class CopyStager:
+    """ifr_dispatch_copy_jobs (kernels/page_copy.mojo:63-94) with a ring of
+    pinned host + device staging buffers: a buffer is reused only after the
+    stream has passed the call that last used it (the ws_host contract), so a
+    timed loop of copies never waits on the host."""
+
+    def __init__(self, jobs, dev, ring: int = 4):
+        import torch
+
+        from inferno_amd._lib import lib
+
+        self.jobs = np.ascontiguousarray(jobs, dtype=np.int64).reshape(-1, 3)
+        self.nbytes = int(lib().ifr_copy_jobs_bytes(self.jobs.shape[0],
+                                                    int(self.jobs[:, 2].sum())))
+        self.bufs = [(torch.empty(self.nbytes, dtype=torch.uint8, pin_memory=True),
+                      torch.empty(self.nbytes, dtype=torch.uint8, device=dev),
+                      torch.cuda.Event()) for _ in range(ring)]
+        self.used = [False] * ring
+        self.i = 0
+
+    @property
+    def copied_bytes(self) -> int:
+        return int(self.jobs[:, 2].sum())
+
+    def __call__(self, arena, stream) -> None:
+        from inferno_amd._lib import P_I64, check, lib
+
+        host, devb, ev = self.bufs[self.i]
+        if self.used[self.i]:
+            ev.synchronize()
+        check(lib().ifr_dispatch_copy_jobs(
+            arena.data_ptr(), self.jobs.ctypes.data_as(P_I64), self.jobs.shape[0],
+            host.data_ptr(), devb.data_ptr(), self.nbytes, int(stream.cuda_stream)))
+        ev.record(stream)
+        self.used[self.i] = True
+        self.i = (self.i + 1) % len(self.bufs)
+
+
 class DecodeBf16:
-    """Configs 1-3: bf16 append + split-KV decode + merge."""
+    """Configs 1-3 and 7: bf16 append + split-KV decode + merge."""
 
     dtype = "bf16"
     phases = ("append", "partials", "merge")
@@ -77,7 +146,17 @@ class DecodeBf16:
 
     def __init__(self, config: int, seed: int):
         self.cfg, self.seed = config, seed
-        if config == 1:
+        self.nq, self.nkv, self.hd, self.half, self.pair = SLIDING_SHAPE
+        if config == 7:
+            self.nq, self.nkv, self.hd, self.half, self.pair = FULL_SHAPE
+            self.pos = uniform_ints(seed, 64, 512, 32768)
+            self.kind, self.window, self.ring = 1, 0, 0
+            self.extra_pages = 0
+            self.dominant = "flash_partial_wide_kernel<bf16> (hd512, 8 q heads per kv head)"
+            self.name = ("config7 (Gemma-4 full-attention layer): B=64 batched paged decode, "
+                         "ctx ~ U[512,32768], 16q/2kv hd512 bf16, partial RoPE (64 pairs), "
+                         "64-token pages, append 1 + split-KV decode + merge")
+        elif config == 1:
             self.pos = [4096]
             self.kind, self.window, self.ring = 1, 0, 0
             self.extra_pages = 128 - 65
@@ -134,12 +213,13 @@ class DecodeBf16:
         self.pool, self.table = pool, table
         self.cache_size = cache_size
         rows = pool * PAGE_LEN
+        self.kvs = self.nkv * self.hd
         self.stream = torch.cuda.current_stream()
         sid = int(self.stream.cuda_stream)
-        self.k = torch.empty(rows * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.k = torch.empty(rows * self.kvs, dtype=torch.int16, device=dev)
         self.v = torch.empty_like(self.k)
-        self.q = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
-        self.ks = torch.empty(B * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.q = torch.empty(B * self.nq * self.hd, dtype=torch.int16, device=dev)
+        self.ks = torch.empty(B * self.kvs, dtype=torch.int16, device=dev)
         self.vs = torch.empty_like(self.ks)
         for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
             _fill(t, self.seed * 16 + i, sid)
@@ -147,7 +227,7 @@ class DecodeBf16:
         # decode step walks every layer before it returns to this one: a
         # configuration whose step touches less than 2 GiB of K/V would
         # otherwise find it in the 256 MB last-level cache (MALL) again.
-        self.layers = layer_count(self.kv_positions() * KV_STRIDE * 4)
+        self.layers = layer_count(self.kv_positions() * self.kvs * 4)
         self.kl = [(self.k, self.v)]
         for j in range(1, self.layers):
             kj, vj = torch.empty_like(self.k), torch.empty_like(self.v)
@@ -155,21 +235,23 @@ class DecodeBf16:
             _fill(vj, self.seed * 16 + 32 * j + 1, sid)
             self.kl.append((kj, vj))
         self.layer = 0
-        cos, sin = rope_tables(max(self.pos) + 2)
+        cos, sin = rope_tables(max(self.pos) + 2, half=self.half)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.plan = AttentionPlan(table, B, kind=self.kind, window=self.window,
                                   cache_size=cache_size, page_len=PAGE_LEN, cache_rows=rows,
-                                  cap=a.cap, kv_row_bytes=KV_STRIDE * 2, device=dev)
-        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
-        self.out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+                                  cap=a.cap, kv_row_bytes=self.kvs * 2, device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, self.nq, self.hd)
+        self.out = torch.empty(B * self.nq * self.hd, dtype=torch.int16, device=dev)
         self.q_host = self.q.cpu().numpy().view(np.uint16).copy()
         self.cap = a.cap
+        self.sqrt_n = float(np.sqrt(np.float32(self.hd)))
+        self.n_eps = float(np.float32(self.hd) * np.float32(1e-6))
         # Optional head RMS norm ahead of the append (dispatch_rms_norm_qkv_heads):
         # "separate" runs it as its own in-place pass, "fused" folds it into the
         # append kernel.
         self.norm = a.norm
         if self.norm != "none":
-            self.qw = torch.empty(HEAD_DIM, dtype=torch.int16, device=dev)
+            self.qw = torch.empty(self.hd, dtype=torch.int16, device=dev)
             self.kw = torch.empty_like(self.qw)
             _fill(self.qw, self.seed * 16 + 7, sid)
             _fill(self.kw, self.seed * 16 + 8, sid)
@@ -180,10 +262,10 @@ class DecodeBf16:
         # a random bf16 weight [HIDDEN][num_q * head_dim].
         self.oproj = a.oproj
         if self.oproj:
-            self.o_w = torch.empty(HIDDEN * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+            self.o_w = torch.empty(HIDDEN * self.nq * self.hd, dtype=torch.int16, device=dev)
             _fill(self.o_w, self.seed * 16 + 9, sid, scale=0.02)
             self.o_out = torch.empty(B * HIDDEN, dtype=torch.int16, device=dev)
-            self.o_ws = A.gemm_cols_workspace(HIDDEN, NUM_Q * HEAD_DIM, B, device=dev)
+            self.o_ws = A.gemm_cols_workspace(HIDDEN, self.nq * self.hd, B, device=dev)
             self.phases = self.phases + ("oproj",)
             self.name += ", o_proj bf16 GEMM"
 
@@ -194,28 +276,31 @@ class DecodeBf16:
         kc, vc = self.kl[self.layer]
         if phase == "oproj":
             A.dispatch_gemm_cols(self.out, self.o_w, self.o_out, rows=HIDDEN,
-                                 cols=NUM_Q * HEAD_DIM, seq_len=len(self.pos),
+                                 cols=self.nq * self.hd, seq_len=len(self.pos),
                                  workspace=self.o_ws)
         elif phase == "norm":
             A.dispatch_rms_norm_qkv_heads(self.q, self.ks, self.vs, self.qw, self.kw,
-                                          num_q=NUM_Q, num_kv=NUM_KV, seq_len=len(self.pos),
-                                          head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
+                                          num_q=self.nq, num_kv=self.nkv,
+                                          seq_len=len(self.pos), head_dim=self.hd,
+                                          sqrt_n=self.sqrt_n, n_eps=self.n_eps)
         elif phase == "append" and self.norm == "fused":
             A.dispatch_rms_norm_rope_cache_write(
                 p, self.q, self.ks, self.vs, kc, vc, self.qw, self.kw, self.cos,
-                self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128, pair_stride=128,
-                head_dim=HEAD_DIM, sqrt_n=16.0, n_eps=HEAD_DIM * 1e-6)
+                self.sin, num_q=self.nq, num_kv=self.nkv, half=self.half,
+                pair_stride=self.pair, head_dim=self.hd, sqrt_n=self.sqrt_n,
+                n_eps=self.n_eps)
         elif phase == "append":
             A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, kc, vc, self.cos,
-                                        self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
-                                        pair_stride=128, head_dim=HEAD_DIM)
+                                        self.sin, num_q=self.nq, num_kv=self.nkv,
+                                        half=self.half, pair_stride=self.pair,
+                                        head_dim=self.hd)
         elif phase == "partials":
             A.flash_partials_bf16(p, self.q, kc, vc, self.partials, self.ps,
-                                  num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
-                                  kv_stride=KV_STRIDE)
+                                  num_q=self.nq, num_kv=self.nkv, head_dim=self.hd,
+                                  kv_stride=self.kvs)
         else:
-            A.merge_flash_partials(p, self.partials, self.out, self.ps, num_q=NUM_Q,
-                                   head_dim=HEAD_DIM)
+            A.merge_flash_partials(p, self.partials, self.out, self.ps, num_q=self.nq,
+                                   head_dim=self.hd)
 
     def kv_positions(self, pos=None) -> int:
         pos = self.pos if pos is None else pos
@@ -226,22 +311,23 @@ class DecodeBf16:
     def dominant_bytes(self) -> int:
         """Partial kernel: K+V of every attended position, q and the page table."""
         B = len(self.pos)
-        return (self.kv_positions() * KV_STRIDE * 4 + B * NUM_Q * HEAD_DIM * 2
+        return (self.kv_positions() * self.kvs * 4 + B * self.nq * self.hd * 2
                 + 4 * len(self.table.base_rows))
 
     def step_bytes(self) -> int:
         """Whole step: the partial kernel's bytes, the output and the append."""
         B = len(self.pos)
-        append = B * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 2)
+        append = B * (self.kvs * 2 * 2 * 2 + self.nq * self.hd * 2 * 2)
         # o_proj: its weight, the attention output read back, the bf16 result.
-        oproj = (HIDDEN * NUM_Q * HEAD_DIM * 2 + B * NUM_Q * HEAD_DIM * 2 + B * HIDDEN * 2
+        oproj = (HIDDEN * self.nq * self.hd * 2 + B * self.nq * self.hd * 2 + B * HIDDEN * 2
                  if self.oproj else 0)
-        return self.dominant_bytes() + B * NUM_Q * HEAD_DIM * 2 + append + oproj
+        return self.dominant_bytes() + B * self.nq * self.hd * 2 + append + oproj
 
     def config(self) -> dict:
         return {"workload": self.name, "batch": len(self.pos),
                 "attended_positions": self.kv_positions(), "pool_pages": self.pool,
-                "page_len": PAGE_LEN, "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM,
+                "page_len": PAGE_LEN, "num_q": self.nq, "num_kv": self.nkv,
+                "head_dim": self.hd, "rope_half": self.half, "pair_stride": self.pair,
                 "window": self.window or None, "cap": self.cap, "seed": self.seed,
                 "plan_items": self.plan.summary.num_items, "layer_caches": self.layers}
 
@@ -250,12 +336,14 @@ class DecodeBf16:
 
         import oracle
 
-        threads = min(16, os.cpu_count() or 1)
+        hc = host_cpu()
+        threads = hc["threads"]
         n_seq = min(len(self.pos), max(threads, 8))
+        kc, vc = self.kl[self.layer]
         pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
-        idx = torch.from_numpy(pages.astype(np.int64)).to(self.k.device)
-        kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
-        vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        idx = torch.from_numpy(pages.astype(np.int64)).to(kc.device)
+        kp = kc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
+        vp = vc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
         kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
         vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
         runs, rows, off = [], [], 0
@@ -265,21 +353,22 @@ class DecodeBf16:
             rows.extend((off + j) * PAGE_LEN for j in range(n))
             off += n
         runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
-        q = np.ascontiguousarray(self.q_host[:n_seq * NUM_Q * HEAD_DIM])
+        q = np.ascontiguousarray(self.q_host[:n_seq * self.nq * self.hd])
         sample_pos = self.kv_positions(self.pos[:n_seq])
-        nbytes = sample_pos * KV_STRIDE * 4
+        nbytes = sample_pos * self.kvs * 4
         times = []
         t_end = time.perf_counter() + budget_s
         while len(times) < 5 and (not times or time.perf_counter() < t_end):
             t0 = time.perf_counter()
-            oracle.attention(self.kind, runs, rows, q, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
-                             head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=self.window,
+            oracle.attention(self.kind, runs, rows, q, kp, vp, num_q=self.nq, num_kv=self.nkv,
+                             head_dim=self.hd, kv_stride=self.kvs, window=self.window,
                              cache_size=self.cache_size, page_len=PAGE_LEN, seq_len=n_seq,
                              cap=threads, threads=threads)
             times.append(time.perf_counter() - t0)
         med = statistics.median(times)
         return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-                "kind": "port",
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
                 "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
                            f"({nbytes / 1e9:.3f} GB of K+V), the reference's routing at "
                            f"cap={threads} workers, median of {len(times)}"),
@@ -287,18 +376,30 @@ class DecodeBf16:
 
 
 class DecodeBq:
-    """Config 5: butterquant int8 KV -- quantizing append + int8 decode + merge."""
+    """Configs 5 and 8: butterquant int8 KV -- quantizing append + int8 decode +
+    merge."""
 
     dtype = "int8 KV (f32 scales), f32 accumulate"
     phases = ("append", "attention")
     dominant = "bq_partial_kernel<2> + merge_kernel<256>"
 
-    def __init__(self, seed: int):
-        self.seed = seed
+    def __init__(self, config: int, seed: int):
+        self.cfg, self.seed = config, seed
         self.pos = uniform_ints(seed, 128, 1024, 65536)
-        self.name = ("config5: B=128 butterquant decode, ctx ~ U[1024,65536], 16q/8kv hd256, "
-                     "int8 FWHT-256 codes + f32 per-(position, kv head) scales (the reference's "
-                     "bq format), quantizing append 1 + int8 split-KV decode + merge")
+        if config == 8:
+            self.nq, self.nkv, self.hd, self.half, self.pair = FULL_SHAPE
+            self.dominant = "flash_partial_wide_kernel<int8> + merge_kernel<512>"
+            self.name = ("config8 (Gemma-4 full-attention layer, bq): B=128 butterquant decode, "
+                         "ctx ~ U[1024,65536], 16q/2kv hd512, int8 FWHT-512 codes + f32 scales, "
+                         "partial RoPE (64 pairs), quantizing append 1 + int8 split-KV decode "
+                         "+ merge")
+        else:
+            self.nq, self.nkv, self.hd, self.half, self.pair = SLIDING_SHAPE
+            self.name = ("config5: B=128 butterquant decode, ctx ~ U[1024,65536], 16q/8kv "
+                         "hd256, int8 FWHT-256 codes + f32 per-(position, kv head) scales (the "
+                         "reference's bq format), quantizing append 1 + int8 split-KV decode "
+                         "+ merge")
+        self.kvs = self.nkv * self.hd
 
     def setup(self, dev, a):
         import torch
@@ -320,40 +421,45 @@ class DecodeBq:
             off += need[i]
         rows = pool * PAGE_LEN
         self.pool, self.table = pool, table
+        self.pages = []
+        off = 0
+        for n in need:
+            self.pages.append([int(x) for x in perm[off:off + n]])
+            off += n
         self.stream = torch.cuda.current_stream()
         sid = int(self.stream.cuda_stream)
-        self.kc = torch.empty(rows * KV_STRIDE, dtype=torch.int8, device=dev)
+        self.kc = torch.empty(rows * self.kvs, dtype=torch.int8, device=dev)
         self.vc = torch.empty_like(self.kc)
         _fill(self.kc, self.seed * 16 + 1, sid)
         _fill(self.vc, self.seed * 16 + 2, sid)
         gen = torch.Generator(device=dev)
         gen.manual_seed(self.seed)
-        self.ksc = torch.rand(rows * NUM_KV, device=dev, generator=gen) * 4 + 0.5
-        self.vsc = torch.rand(rows * NUM_KV, device=dev, generator=gen) * 4 + 0.5
-        self.qs = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
-        self.kss = torch.empty(B * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.ksc = torch.rand(rows * self.nkv, device=dev, generator=gen) * 4 + 0.5
+        self.vsc = torch.rand(rows * self.nkv, device=dev, generator=gen) * 4 + 0.5
+        self.qs = torch.empty(B * self.nq * self.hd, dtype=torch.int16, device=dev)
+        self.kss = torch.empty(B * self.kvs, dtype=torch.int16, device=dev)
         self.vss = torch.empty_like(self.kss)
         for i, t in enumerate((self.qs, self.kss, self.vss)):
             _fill(t, self.seed * 16 + 3 + i, sid, outlier_every=100, scale=20.0)
-        self.qn = torch.full((HEAD_DIM,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
+        self.qn = torch.full((self.hd,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
         self.kn = self.qn
-        cos, sin = rope_tables(max(self.pos) + 2)
+        cos, sin = rope_tables(max(self.pos) + 2, half=self.half)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
-        self.q_i8 = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int8, device=dev)
-        self.qb = torch.empty(B * NUM_Q, dtype=torch.float32, device=dev)
+        self.q_i8 = torch.empty(B * self.nq * self.hd, dtype=torch.int8, device=dev)
+        self.qb = torch.empty(B * self.nq, dtype=torch.float32, device=dev)
         self.fq = torch.empty_like(self.qb)
         self.plan = AttentionPlan(table, B, kind=1, window=0, cache_size=PAGE_LEN,
                                   page_len=PAGE_LEN, cache_rows=rows, cap=a.cap,
-                                  kv_row_bytes=KV_STRIDE, device=dev)
-        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
-        self.out = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+                                  kv_row_bytes=self.kvs, device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, self.nq, self.hd)
+        self.out = torch.empty(B * self.nq * self.hd, dtype=torch.int16, device=dev)
         self.cap = a.cap
         # Optional o_proj input quantisation (dispatch_bq_block_quant,
         # block = head_dim): its own pass over the output, or fused into the merge.
         self.oquant = a.oquant
         if self.oquant != "none":
-            self.o_i8 = torch.empty(B * NUM_Q * HEAD_DIM, dtype=torch.int8, device=dev)
-            self.o_sa = torch.empty(B * NUM_Q, dtype=torch.float32, device=dev)
+            self.o_i8 = torch.empty(B * self.nq * self.hd, dtype=torch.int8, device=dev)
+            self.o_sa = torch.empty(B * self.nq, dtype=torch.float32, device=dev)
             self.name += f", o_proj int8 block quant {self.oquant}"
         if self.oquant == "separate":
             self.phases = DecodeBq.phases + ("oquant",)
@@ -361,46 +467,98 @@ class DecodeBq:
     def launch(self, phase):
         A, p = self.A, self.plan
         if phase == "oquant":
-            A.dispatch_bq_block_quant(self.out, self.o_i8, self.o_sa, cols=NUM_Q * HEAD_DIM,
-                                      block=HEAD_DIM, seq_len=len(self.pos))
+            A.dispatch_bq_block_quant(self.out, self.o_i8, self.o_sa, cols=self.nq * self.hd,
+                                      block=self.hd, seq_len=len(self.pos))
         elif phase == "append":
-            A.dispatch_bq_attn_prep(p, self.qs, self.kss, self.vss, self.qn, self.kn,
+            # The full layer's V is its raw K projection (gemma_4_moe_bq.mojo:566-573).
+            vsrc = self.kss if self.cfg == 8 else self.vss
+            A.dispatch_bq_attn_prep(p, self.qs, self.kss, vsrc, self.qn, self.kn,
                                     self.q_i8, self.qb, self.fq, self.kc, self.ksc, self.vc,
-                                    self.vsc, self.cos, self.sin, num_q=NUM_Q, num_kv=NUM_KV,
-                                    head_dim=HEAD_DIM, rope_half=128, pair_stride=128,
-                                    sqrt_n=16.0,
-                                    n_eps=float(np.float32(256) * np.float32(1e-6)))
+                                    self.vsc, self.cos, self.sin, num_q=self.nq,
+                                    num_kv=self.nkv, head_dim=self.hd, rope_half=self.half,
+                                    pair_stride=self.pair,
+                                    sqrt_n=float(np.sqrt(np.float32(self.hd))),
+                                    n_eps=float(np.float32(self.hd) * np.float32(1e-6)))
         else:
             fused = self.oquant == "fused"
             A.bq_attention(p, self.q_i8, self.qb, self.fq, self.kc, self.ksc, self.vc,
-                           self.vsc, self.out, self.partials, self.ps, num_q=NUM_Q,
-                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE,
+                           self.vsc, self.out, self.partials, self.ps, num_q=self.nq,
+                           num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs,
                            o_i8=self.o_i8 if fused else None,
                            o_sa=self.o_sa if fused else None)
 
     def dominant_bytes(self) -> int:
         B = len(self.pos)
-        kv = sum(p + 1 for p in self.pos) * (KV_STRIDE * 2 + NUM_KV * 4 * 2)
-        return (kv + B * NUM_Q * (HEAD_DIM + 8) + 4 * len(self.table.base_rows)
-                + B * NUM_Q * HEAD_DIM * 2)
+        kv = sum(p + 1 for p in self.pos) * (self.kvs * 2 + self.nkv * 4 * 2)
+        return (kv + B * self.nq * (self.hd + 8) + 4 * len(self.table.base_rows)
+                + B * self.nq * self.hd * 2)
 
     def step_bytes(self) -> int:
         B = len(self.pos)
-        append = B * ((NUM_Q + 2 * NUM_KV) * HEAD_DIM * 2 + (NUM_Q + 2 * NUM_KV) * HEAD_DIM)
+        append = B * ((self.nq + 2 * self.nkv) * self.hd * 2 +
+                      (self.nq + 2 * self.nkv) * self.hd)
         # o_proj quant: int8 codes + f32 scales written; the separate pass
         # also re-reads the bf16 output.
-        oquant = {"none": 0, "fused": B * NUM_Q * (HEAD_DIM + 4),
-                  "separate": B * NUM_Q * (3 * HEAD_DIM + 4)}[self.oquant]
+        oquant = {"none": 0, "fused": B * self.nq * (self.hd + 4),
+                  "separate": B * self.nq * (3 * self.hd + 4)}[self.oquant]
         return self.dominant_bytes() + append + oquant
 
     def config(self) -> dict:
         return {"workload": self.name, "batch": len(self.pos),
                 "attended_positions": sum(p + 1 for p in self.pos), "pool_pages": self.pool,
-                "page_len": PAGE_LEN, "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM,
+                "page_len": PAGE_LEN, "num_q": self.nq, "num_kv": self.nkv,
+                "head_dim": self.hd, "rope_half": self.half, "pair_stride": self.pair,
                 "cap": self.cap, "seed": self.seed, "plan_items": self.plan.summary.num_items}
 
     def cpu_baseline(self, budget_s):
-        return None
+        """The oracle's bq attention (bq_process_kv_tile and the merge, the
+        reference's routing) on the first sequences of the batch."""
+        import torch
+
+        import oracle
+
+        hc = host_cpu()
+        threads = hc["threads"]
+        n_seq = min(len(self.pos), max(threads, 8))
+        pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
+        idx = torch.from_numpy(pages.astype(np.int64)).to(self.kc.device)
+        kp = self.kc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
+        vp = self.vc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
+        ksp = self.ksc.view(-1, PAGE_LEN * self.nkv).index_select(0, idx).cpu().numpy()
+        vsp = self.vsc.view(-1, PAGE_LEN * self.nkv).index_select(0, idx).cpu().numpy()
+        kp, vp = (np.ascontiguousarray(x.reshape(-1)) for x in (kp, vp))
+        ksp, vsp = (np.ascontiguousarray(x.reshape(-1)) for x in (ksp, vsp))
+        runs, rows, off = [], [], 0
+        for i in range(n_seq):
+            n = len(self.pages[i])
+            runs.append([i, self.pos[i], off, n])
+            rows.extend((off + j) * PAGE_LEN for j in range(n))
+            off += n
+        runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
+        nq = n_seq * self.nq
+        q_i8 = np.ascontiguousarray(self.q_i8.cpu().numpy()[:nq * self.hd])
+        qb = np.ascontiguousarray(self.qb.cpu().numpy()[:nq])
+        fq = np.ascontiguousarray(self.fq.cpu().numpy()[:nq])
+        sample_pos = sum(p + 1 for p in self.pos[:n_seq])
+        nbytes = sample_pos * (self.kvs * 2 + self.nkv * 8)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.bq_attention(1, runs, rows, q_i8, qb, fq, kp, ksp, vp, vsp, num_q=self.nq,
+                                num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs,
+                                window=0, cache_size=PAGE_LEN, page_len=PAGE_LEN,
+                                seq_len=n_seq, cap=threads, threads=threads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        total_pos = sum(p + 1 for p in self.pos)
+        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
+                "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
+                           f"({nbytes / 1e9:.3f} GB of int8 K+V and scales), the reference's "
+                           f"bq routing at cap={threads} workers, median of {len(times)}"),
+                "us_per_layer_equiv": round(med * 1e6 * total_pos / sample_pos, 1)}
 
 
 class SparseM3:
@@ -594,21 +752,28 @@ class SparseM3:
 
 class PrefillBf16:
     """Config 4: chunked prefill -- 8 sequences append 2048 tokens each onto
-    prefixes ~ U[0, 16384] (RoPE + cache write), then causal full-attention
-    prefill over the paged prefix + chunk (MFMA)."""
+    prefixes ~ U[0, 16384]; sequences 2k and 2k+1 share one prefix, its sealed
+    pages by reference and its partial last page by a copy-on-write page copy
+    (ContinuousBatchScheduler.fork_prefix, continuous_batching/scheduler.mojo:
+    395-466, copies at :427-436).  A step: the COW copies, the append (RoPE +
+    cache write), then causal full-attention prefill over the paged prefix +
+    chunk (MFMA)."""
 
     dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
-    phases = ("append", "attention")
+    phases = ("cow", "append", "attention")
     dominant = "prefill_full_mfma_kernel"
+    dominant_phase = "attention"
     bound = "mfma"
 
     def __init__(self, seed: int):
         self.seed = seed
-        self.prefix = uniform_ints(seed, 8, 0, 16384)
+        shared = uniform_ints(seed, 4, 0, 16384)
+        self.prefix = [p for p in shared for _ in range(2)]
         self.new = 2048
         self.name = ("config4: chunked prefill, 8 sequences x 2048 new tokens on prefixes "
-                     "~ U[0,16384], 16q/8kv hd256 bf16, 64-token pages, append + causal MFMA "
-                     "prefill over the paged prefix and chunk")
+                     "~ U[0,16384] shared by sequence pairs (sealed pages shared, the partial "
+                     "page copied on write), 16q/8kv hd256 bf16, 64-token pages, COW copy + "
+                     "append + causal MFMA prefill over the paged prefix and chunk")
 
     def setup(self, dev, a):
         import torch
@@ -618,28 +783,64 @@ class PrefillBf16:
 
         self.A = A
         n_seq = len(self.prefix)
-        need = [(p + self.new + PAGE_LEN - 1) // PAGE_LEN for p in self.prefix]
-        pool = sum(need)
-        perm = np.random.default_rng(self.seed).permutation(pool)
-        table = KVRunTable()
+        # Page ordinals per sequence; the second of a pair takes the first's
+        # sealed prefix pages and owns the rest (its partial prefix page is the
+        # COW copy).
+        rng = np.random.default_rng(self.seed)
+        owned, tables = [], []
+        for i, p in enumerate(self.prefix):
+            n_ord = (p + self.new + PAGE_LEN - 1) // PAGE_LEN
+            n_shared = p // PAGE_LEN if i % 2 == 1 else 0
+            owned.append(n_ord - n_shared)
+            tables.append([None] * n_shared + [0] * (n_ord - n_shared))
+        pool = sum(owned)
+        perm = [int(x) for x in rng.permutation(pool)]
         off = 0
+        for i in range(n_seq):
+            t = tables[i]
+            for o in range(len(t)):
+                if t[o] is None:
+                    t[o] = tables[i - 1][o]
+                else:
+                    t[o] = perm[off]
+                    off += 1
+        table = KVRunTable()
         for i, p in enumerate(self.prefix):
             table.begin_run(i * self.new, p)
-            for x in perm[off:off + need[i]]:
-                table.add_base_row(int(x) * PAGE_LEN)
-            off += need[i]
+            for pg in tables[i]:
+                table.add_base_row(pg * PAGE_LEN)
         n = n_seq * self.new
         rows = pool * PAGE_LEN
-        self.pool, self.table, self.n = pool, table, n
+        self.pool, self.table, self.n, self.tables = pool, table, n, tables
         self.stream = torch.cuda.current_stream()
         sid = int(self.stream.cuda_stream)
-        self.k = torch.empty(rows * KV_STRIDE, dtype=torch.int16, device=dev)
-        self.v = torch.empty_like(self.k)
+        # K and V share one arena, as the reference's KV mirror lays the
+        # components out, so the copy jobs address both with byte offsets.
+        self.arena = torch.empty(2 * rows * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.k = self.arena[:rows * KV_STRIDE]
+        self.v = self.arena[rows * KV_STRIDE:]
         self.q = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
         self.ks = torch.empty(n * KV_STRIDE, dtype=torch.int16, device=dev)
         self.vs = torch.empty_like(self.ks)
         for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
             _fill(t, self.seed * 16 + i, sid)
+        # COW jobs: rows [0, p % 64) of the first's partial prefix page into the
+        # second's own page at the same ordinal, for K and V
+        # (append_prefix_copy_jobs, modeling/kv_policy.mojo:59-78).
+        row_bytes = KV_STRIDE * 2
+        v_base = rows * row_bytes
+        jobs = []
+        for i in range(1, n_seq, 2):
+            p = self.prefix[i]
+            if p % PAGE_LEN == 0:
+                continue
+            o = p // PAGE_LEN
+            src, dst = tables[i - 1][o] * PAGE_LEN, tables[i][o] * PAGE_LEN
+            nb = (p % PAGE_LEN) * row_bytes
+            for base in (0, v_base):
+                jobs.append([base + src * row_bytes, base + dst * row_bytes, nb])
+        self.jobs = np.asarray(jobs, dtype=np.int64).reshape(-1, 3)
+        self.cow = CopyStager(self.jobs, dev) if len(jobs) else None
         cos, sin = rope_tables(max(self.prefix) + self.new + 1)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.plan = AttentionPlan(table, n, kind=1, window=0, cache_size=PAGE_LEN,
@@ -651,7 +852,10 @@ class PrefillBf16:
 
     def launch(self, phase):
         A, p = self.A, self.plan
-        if phase == "append":
+        if phase == "cow":
+            if self.cow is not None:
+                self.cow(self.arena, self.stream)
+        elif phase == "append":
             A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
                                         self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
                                         pair_stride=128, head_dim=HEAD_DIM)
@@ -666,7 +870,8 @@ class PrefillBf16:
         return 4 * HEAD_DIM * NUM_Q * keys
 
     def step_bytes(self) -> int:
-        return self.n * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 3)
+        cow = 2 * int(self.jobs[:, 2].sum()) if self.jobs.size else 0
+        return self.n * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 3) + cow
 
     def dominant_bytes(self) -> int:
         return 0
@@ -674,6 +879,9 @@ class PrefillBf16:
     def config(self) -> dict:
         return {"workload": self.name, "sequences": len(self.prefix), "new_tokens": self.new,
                 "prefixes": self.prefix, "pool_pages": self.pool, "page_len": PAGE_LEN,
+                "shared_pages": sum(p // PAGE_LEN for p in self.prefix[1::2]),
+                "cow_jobs": int(self.jobs.shape[0]),
+                "cow_bytes": int(self.jobs[:, 2].sum()) if self.jobs.size else 0,
                 "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM, "cap": self.cap,
                 "seed": self.seed, "query_blocks": int(self.plan.info[14]),
                 "algorithmic_tflop": round(self.flops() / 1e12, 3)}
@@ -685,12 +893,13 @@ class PrefillBf16:
 
         import oracle
 
-        threads = min(16, os.cpu_count() or 1)
+        hc = host_cpu()
+        threads = hc["threads"]
         i = int(np.argmax(self.prefix))
         p0 = self.prefix[i]
-        npage = (p0 + self.new + PAGE_LEN - 1) // PAGE_LEN
-        rows = np.asarray(self.table.base_rows[self.table.runs[i][2]:][:npage], dtype=np.int64)
-        idx = torch.from_numpy(rows // PAGE_LEN).to(self.k.device)
+        pages = np.asarray(self.tables[i], dtype=np.int64)
+        npage = pages.size
+        idx = torch.from_numpy(pages).to(self.k.device)
         kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
         vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
         kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
@@ -714,10 +923,167 @@ class PrefillBf16:
             times.append(time.perf_counter() - t0)
         med = statistics.median(times)
         return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port",
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
                 "sample": (f"last {n_s} query tokens of the longest sequence "
                            f"({keys} query-key pairs), the reference's token route at "
                            f"cap={threads} workers, median of {len(times)}")}
+
+
+class PageCopyBench:
+    """Config 9 (widening): dispatch_copy_jobs (kernels/page_copy.mojo:63-94) as
+    copy-on-write of bf16 pages of the 16q/8kv hd256 cache: 2048 page copies
+    per component (K and V) between shuffled pages of one arena, every fourth a
+    partial page of 1-63 rows (a fork's divergent page).  The timed dispatch
+    includes the job list's upload."""
+
+    dtype = "bytes"
+    phases = ("copy",)
+    dominant = "copy dispatch (job-list upload + copy_chunks_kernel)"
+    dominant_phase = "copy"
+
+    def __init__(self, seed: int):
+        self.seed = seed
+        self.copies = 2048
+        self.name = ("config9 (widening): copy-on-write page copy, 2048 page copies per K/V "
+                     "component of a 16q/8kv hd256 bf16 cache (256 KiB pages), every 4th a "
+                     "partial page of 1-63 rows, shuffled source/destination pages of one "
+                     "arena, dispatch_copy_jobs")
+
+    def setup(self, dev, a):
+        import torch
+
+        rng = np.random.default_rng(self.seed)
+        row_bytes = KV_STRIDE * 2
+        page_bytes = PAGE_LEN * row_bytes
+        pages = 2 * self.copies  # per component: sources, then destinations
+        comp = pages * page_bytes
+        self.stream = torch.cuda.current_stream()
+        self.arena = torch.empty(2 * comp, dtype=torch.uint8, device=dev)
+        _fill(self.arena, self.seed * 16 + 1, int(self.stream.cuda_stream))
+        src = rng.permutation(self.copies)
+        dst = self.copies + rng.permutation(self.copies)
+        nrows = np.where(np.arange(self.copies) % 4 == 3,
+                         rng.integers(1, PAGE_LEN, self.copies), PAGE_LEN)
+        jobs = []
+        for c in range(2):
+            for j in range(self.copies):
+                jobs.append([c * comp + int(src[j]) * page_bytes,
+                             c * comp + int(dst[j]) * page_bytes, int(nrows[j]) * row_bytes])
+        self.jobs = np.asarray(jobs, dtype=np.int64)
+        self.stager = CopyStager(self.jobs, dev)
+        self.cap = 0
+
+    def launch(self, phase):
+        self.stager(self.arena, self.stream)
+
+    def dominant_bytes(self) -> int:
+        return 2 * self.stager.copied_bytes  # read + write
+
+    def step_bytes(self) -> int:
+        return self.dominant_bytes()
+
+    def config(self) -> dict:
+        return {"workload": self.name, "jobs": int(self.jobs.shape[0]),
+                "copied_bytes": self.stager.copied_bytes, "page_len": PAGE_LEN,
+                "row_bytes": KV_STRIDE * 2, "seed": self.seed}
+
+    def cpu_baseline(self, budget_s):
+        """The oracle's copy (one memcpy per job, as a PageCopyKernel worker
+        does for its byte range) over the first 512 jobs, remapped into a
+        compact host arena, one thread."""
+        import oracle
+
+        n = 512
+        page_bytes = PAGE_LEN * KV_STRIDE * 2
+        jobs = np.empty((n, 3), dtype=np.int64)
+        jobs[:, 0] = np.arange(n) * page_bytes
+        jobs[:, 1] = (n + np.arange(n)) * page_bytes
+        jobs[:, 2] = self.jobs[:n, 2]
+        arena = np.ones(2 * n * page_bytes, dtype=np.uint8)
+        oracle.copy_jobs(arena, jobs)  # first touch of every page
+        nbytes = 2 * int(jobs[:, 2].sum())
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.copy_jobs(arena, jobs)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        hc = host_cpu()
+        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
+                "sample": (f"the first {n} jobs ({nbytes / 2e6:.1f} MB copied) in a "
+                           f"compact host arena, one thread, median of {len(times)}")}
+
+
+class GatherBench:
+    """Config 10 (widening): dispatch_gather_rows (kernels/gather.mojo:30-55)
+    of bf16 hidden rows (cols = Gemma-4's 2816): 16384 of 65536 rows in a
+    seeded random order."""
+
+    dtype = "bytes"
+    phases = ("gather",)
+    dominant = "gather_rows_kernel"
+    dominant_phase = "gather"
+    SRC_ROWS, ROWS, COLS = 65536, 16384, HIDDEN
+
+    def __init__(self, seed: int):
+        self.seed = seed
+        self.name = ("config10 (widening): row gather, 16384 of 65536 bf16 hidden rows "
+                     "(cols 2816, the emit-row gather of stage_sampling_inputs at prefill "
+                     "scale), seeded random order, dispatch_gather_rows")
+
+    def setup(self, dev, a):
+        import torch
+
+        from inferno_amd import attention as A
+
+        self.A = A
+        self.stream = torch.cuda.current_stream()
+        self.src = torch.empty(self.SRC_ROWS * self.COLS, dtype=torch.int16, device=dev)
+        _fill(self.src, self.seed * 16 + 1, int(self.stream.cuda_stream))
+        rows = np.random.default_rng(self.seed).choice(self.SRC_ROWS, self.ROWS, replace=False)
+        self.rows_host = rows.astype(np.int32)
+        self.rows = torch.from_numpy(self.rows_host).to(dev)
+        self.dst = torch.empty(self.ROWS * self.COLS, dtype=torch.int16, device=dev)
+        self.cap = 0
+
+    def launch(self, phase):
+        self.A.dispatch_gather_rows(self.src, self.dst, self.rows, self.ROWS, self.COLS)
+
+    def dominant_bytes(self) -> int:
+        return 2 * self.ROWS * self.COLS * 2 + 4 * self.ROWS
+
+    def step_bytes(self) -> int:
+        return self.dominant_bytes()
+
+    def config(self) -> dict:
+        return {"workload": self.name, "rows": self.ROWS, "source_rows": self.SRC_ROWS,
+                "cols": self.COLS, "seed": self.seed}
+
+    def cpu_baseline(self, budget_s):
+        """The oracle's gather over the first 4096 rows, one thread."""
+        import oracle
+
+        n = 4096
+        src = self.src.cpu().numpy().view(np.uint16)
+        rows = self.rows_host[:n]
+        nbytes = 2 * n * self.COLS * 2
+        oracle.gather_rows(src, rows, self.COLS)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.gather_rows(src, rows, self.COLS)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        hc = host_cpu()
+        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
+                "sample": f"the first {n} rows, one thread, median of {len(times)}"}
 
 
 def measure(w, steps: int, warmup: int):
@@ -769,7 +1135,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6))
+    ap.add_argument("--config", type=int, default=2, choices=tuple(range(1, 11)))
     ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -800,14 +1166,18 @@ def main() -> None:
     if a.copy_calibration:
         copy_calibration(dev)
         return
-    if a.cap <= 0 and a.config != 6:
+    if a.cap <= 0 and DEFAULT_CAP[a.config] > 0:
         a.cap = DEFAULT_CAP[a.config]
     if a.config == 6:
         w = SparseM3(a.seed)
-    elif a.config == 5:
-        w = DecodeBq(a.seed)
+    elif a.config in (5, 8):
+        w = DecodeBq(a.config, a.seed)
     elif a.config == 4:
         w = PrefillBf16(a.seed)
+    elif a.config == 9:
+        w = PageCopyBench(a.seed)
+    elif a.config == 10:
+        w = GatherBench(a.seed)
     else:
         w = DecodeBf16(a.config, a.seed)
     w.setup(dev, a)

@@ -925,14 +925,12 @@ int32_t ifr_dispatch_copy_jobs(void* arena, const int64_t* jobs, int64_t num_job
   if (num_jobs <= 0) return ok();  // page_copy.mojo:72-74
   if (!arena || !jobs || !ws_host || !ws_dev) return fail(IFR_EINVAL, "null pointer");
   int64_t total = 0;
-  bool aligned16 = aligned(arena, 16);
   for (int64_t i = 0; i < num_jobs; ++i) {
     const int64_t s = jobs[3 * i], d = jobs[3 * i + 1], n = jobs[3 * i + 2];
     if (s < 0 || d < 0 || n < 0) return fail(IFR_EINVAL, "job %lld has a negative field", (long long)i);
     if (n > 0 && ((s < d) ? (s + n > d) : (d + n > s)))
       return fail(IFR_EINVAL, "job %lld copies between overlapping ranges", (long long)i);
     total += n;
-    if ((s | d | n) & 15) aligned16 = false;
   }
   if (total == 0) return ok();
   int64_t* chunks = static_cast<int64_t*>(ws_host);
@@ -953,8 +951,7 @@ int32_t ifr_dispatch_copy_jobs(void* arena, const int64_t* jobs, int64_t num_job
                          hipMemcpyHostToDevice, as_stream(stream)),
           "copy job upload");
   IFR_HIP(ifr::launch_copy_chunks(arena, static_cast<const int64_t*>(ws_dev),
-                                  static_cast<int>(nc), aligned16 ? 1 : 0,
-                                  as_stream(stream)),
+                                  static_cast<int>(nc), as_stream(stream)),
           "copy_chunks");
   return ok();
 }

@@ -9,21 +9,39 @@ namespace {
 
 // PageCopyKernel (kernels/page_copy.mojo:25-60): the host splits every
 // CopyJob into chunks of at most kCopyChunk bytes; one workgroup copies one
-// chunk.
+// chunk.  A chunk whose source and destination addresses agree modulo 16
+// is copied as a byte head up to 16-byte alignment, 16-byte vectors (four
+// loads in flight per thread before their stores) and a byte tail; any other
+// chunk byte by byte.  The choice is per chunk, so one odd job does not slow
+// the others of its call.
 __global__ __launch_bounds__(256) void copy_chunks_kernel(
-    uint8_t* __restrict__ arena, const int64_t* __restrict__ chunks,
-    int aligned16) {
+    uint8_t* __restrict__ arena, const int64_t* __restrict__ chunks) {
   const int64_t* ch = chunks + static_cast<int64_t>(blockIdx.x) * 4;
   const int64_t src = ch[0], dst = ch[1], bytes = ch[2];
-  if (aligned16) {
-    const uint4* s = reinterpret_cast<const uint4*>(arena + src);
-    uint4* d = reinterpret_cast<uint4*>(arena + dst);
-    const int64_t n = bytes >> 4;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) d[i] = s[i];
-  } else {
-    for (int64_t i = threadIdx.x; i < bytes; i += blockDim.x)
-      arena[dst + i] = arena[src + i];
+  const int tid = threadIdx.x;
+  const uintptr_t sa = reinterpret_cast<uintptr_t>(arena + src);
+  const uintptr_t da = reinterpret_cast<uintptr_t>(arena + dst);
+  if (((sa ^ da) & 15) != 0) {
+    for (int64_t i = tid; i < bytes; i += blockDim.x) arena[dst + i] = arena[src + i];
+    return;
   }
+  const int64_t head = min<int64_t>(static_cast<int64_t>((16 - (da & 15)) & 15), bytes);
+  if (tid < head) arena[dst + tid] = arena[src + tid];
+  const int64_t n16 = (bytes - head) >> 4;
+  const uint4* s = reinterpret_cast<const uint4*>(arena + src + head);
+  uint4* d = reinterpret_cast<uint4*>(arena + dst + head);
+  constexpr int kIn = 4;  // loads in flight per thread
+  int64_t i = tid;
+  for (; i + (kIn - 1) * 256 < n16; i += kIn * 256) {
+    uint4 v[kIn];
+#pragma unroll
+    for (int u = 0; u < kIn; ++u) v[u] = s[i + u * 256];
+#pragma unroll
+    for (int u = 0; u < kIn; ++u) d[i + u * 256] = v[u];
+  }
+  for (; i < n16; i += 256) d[i] = s[i];
+  const int64_t tail0 = head + (n16 << 4);
+  if (tail0 + tid < bytes) arena[dst + tail0 + tid] = arena[src + tail0 + tid];
 }
 
 // GatherRowsKernel (kernels/gather.mojo:8-27): one workgroup per output row.
@@ -77,12 +95,11 @@ __global__ __launch_bounds__(256) void fill_normal_bf16_kernel(
 
 }  // namespace
 
-hipError_t launch_copy_chunks(void* arena, const int64_t* chunks,
-                              int num_chunks, int aligned16,
+hipError_t launch_copy_chunks(void* arena, const int64_t* chunks, int num_chunks,
                               hipStream_t stream) {
   if (num_chunks <= 0) return hipSuccess;
   hipLaunchKernelGGL(copy_chunks_kernel, dim3(num_chunks), dim3(256), 0,
-                     stream, static_cast<uint8_t*>(arena), chunks, aligned16);
+                     stream, static_cast<uint8_t*>(arena), chunks);
   return hipGetLastError();
 }
 

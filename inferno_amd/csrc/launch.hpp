@@ -145,8 +145,7 @@ hipError_t launch_bq_attn_prep(const int32_t* image_dev, int seq_len,
                                float sqrt_n, float n_eps, hipStream_t stream);
 
 // Copy chunks: int64 [n][4] = {src_off, dst_off, bytes, 0}.
-hipError_t launch_copy_chunks(void* arena, const int64_t* chunks_dev,
-                              int num_chunks, int aligned16,
+hipError_t launch_copy_chunks(void* arena, const int64_t* chunks_dev, int num_chunks,
                               hipStream_t stream);
 
 hipError_t launch_gather_rows(const void* src, void* dst, const int32_t* rows,

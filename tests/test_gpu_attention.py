@@ -221,3 +221,30 @@ def test_page_copy_and_gather_bit_exact():
     dst = empty_dev(77 * 4096, np.uint16)
     A.dispatch_gather_rows(to_dev(src), dst, to_dev(rows), 77, 4096)
     assert np.array_equal(from_dev(dst, np.uint16), oracle.gather_rows(src, rows, 4096))
+
+
+@pytest.mark.parametrize("base_off", [0, 3])
+def test_page_copy_alignment_cases(base_off):
+    """Each chunk picks its own path: co-aligned source and destination take
+    the byte head / 16-byte body / byte tail path, others byte copies, in
+    one call; the arena base itself may be unaligned (base_off 3)."""
+    announce(f"page copy alignment base_off={base_off}")
+    rng = np.random.default_rng(80 + base_off)
+    n = 3 << 20
+    arena = rng.integers(0, 256, n, dtype=np.uint8)
+    # Sources below 1.5 MB, destinations above: no job reads another's output.
+    jobs = np.array([
+        [16, 1_500_000, 200_000],           # aligned, several 64 KiB chunks
+        [200_021, 1_700_005, 70_001],       # co-aligned (offset 5): head/body/tail
+        [300_009, 1_800_004, 131_077],      # offsets 9 and 4: bytes only
+        [450_000, 1_950_003, 7],            # shorter than one vector
+        [460_001, 1_960_001, 15],           # co-aligned, the head covers it all
+        [470_000, 1_970_000, 0],            # empty job
+        [500_000, 2_000_000, 4096 * 64],    # a whole bf16 page of rows
+    ], dtype=np.int64)
+    dev = to_dev(arena)
+    A.dispatch_copy_jobs(dev[base_off:], jobs)
+    ref = arena.copy()
+    oracle.copy_jobs(ref[base_off:], jobs)
+    got = from_dev(dev, np.uint8)
+    assert np.array_equal(got, ref), int((got != ref).sum())
