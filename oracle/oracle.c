@@ -20,13 +20,19 @@
  *   ifo_paged_slot      hand-computed slots for the reference test's ring
  *                       pages (tests/test_sliding_attention_degree_parity
  *                       .mojo:83-86 ring_slot).
- *   ifo_attention       float64 brute-force softmax attention restricted to
- *                       the same tile/split structure (the fexp bias makes the
- *                       result plan dependent); with a one-split plan and a
- *                       single tile it reduces to textbook softmax within the
- *                       fexp error bound; merge identity (merging partials of a
- *                       2-way split equals the sequential pass up to the
- *                       documented per-tile fexp(0) factor).
+ *   ifo_attention       the q = 0 closed form on every dispatch route (tile
+ *                       and split structure); with a one-split plan and a
+ *                       single tile, textbook softmax within the fexp error
+ *                       bound.
+ *   ifo_flash_partial   a float64 model of the tile-wise online softmax (the
+ *                       same tiles and biased exp, exact dots) on profiles
+ *                       with a dominant score in an early tile and a later
+ *                       new maximum, where a missing max carry, a rescale
+ *                       after the add or l without corr each move the
+ *                       partials far beyond the tolerance
+ *                       (tests/test_oracle_pins.py).
+ *   ifo_finalize_head   a float64 model of merge_segments on the oracle's own
+ *                       partials with spread maxima and empty stripes.
  *   ifo_rope_cache_write identity tables (cos=1, sin=0) make it a copy;
  *                       90-degree tables (cos=0, sin=1) swap pairs with sign.
  *   ifo_copy_jobs / ifo_gather_rows  byte-exact closed forms (memcpy/index).
