@@ -175,3 +175,47 @@ def test_planner_rejects_runs_without_tokens(layout):
     st, _, _ = _plan(runs, case.base_rows, seq_len, FULL, 0, PAGE_LEN, case.cache_rows, 16,
                      KV_STRIDE * 2)
     assert st == -1 and "no token" in _lib.last_error()
+
+
+def _header_prototypes():
+    """name -> (return C type, [param C types]) from both headers."""
+    protos = {}
+    for h in HEADERS:
+        src = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*([a-z_0-9]+(?:\s*\*)?)\s+(ifr_\w+)\s*\(([^;]*?)\)\s*;", src,
+                             re.M | re.S):
+            params = [" ".join(a.split()) for a in m.group(3).split(",")]
+            params = [re.match(r"(.*?)\w+$", a).group(1).strip() for a in params
+                      if a not in ("void", "")]
+            protos[m.group(2)] = (m.group(1).strip(), params)
+    return protos
+
+
+def test_mojo_bindings_match_headers():
+    """include/inferno_hip.mojo has one wrapper per declared C function, with
+    the same arity, the agreed type mapping (pointers as Int64 addresses,
+    int64_t Int64, uint64_t UInt64, int32_t Int32, float Float32), and each
+    wrapper calls its own symbol with its parameters in order."""
+    def mojo_type(c):
+        c = c.replace("const ", "").strip()
+        if c.endswith("*"):
+            return "Int64"
+        return {"int64_t": "Int64", "uint64_t": "UInt64", "int32_t": "Int32",
+                "float": "Float32"}[c]
+
+    protos = _header_prototypes()
+    text = (INCLUDE / "inferno_hip.mojo").read_text()
+    defs = re.findall(r"^def (ifr_\w+)\((.*?)\)(?: -> (\w+))?:\n(.*?)(?=\n\n|\Z)", text,
+                      re.M | re.S)
+    assert sorted(d[0] for d in defs) == sorted(protos), "wrapper set differs from the headers"
+    for name, params, ret, body in defs:
+        cret, cparams = protos[name]
+        ps = [p.strip() for p in params.split(",") if p.strip()]
+        names = [p.split(":")[0].strip() for p in ps]
+        types = [p.split(":")[1].strip() for p in ps]
+        assert types == [mojo_type(c) for c in cparams], name
+        want_ret = None if cret == "void" else mojo_type(cret)
+        assert (ret or None) == want_ret, name
+        assert f'func = "{name}".value' in body, name
+        call = re.search(r"\]\((.*?)\)\s*$", body, re.S).group(1)
+        assert [a.strip() for a in call.split(",") if a.strip()] == names, name
