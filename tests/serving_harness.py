@@ -64,30 +64,34 @@ class PoolLayer:
     max_pages: int
     kind: int          # SLIDING for the ring pool, FULL for the growing pool
     window: int = 0
+    page_len: int = PAGE_LEN
 
     @property
     def cache_size(self) -> int:
-        return self.fixed_pages * PAGE_LEN if self.kind == SLIDING else PAGE_LEN
+        return self.fixed_pages * self.page_len if self.kind == SLIDING else self.page_len
 
     @property
     def rows(self) -> int:
-        return self.num_pages * PAGE_LEN
+        return self.num_pages * self.page_len
 
 
 class ServingHarness:
     def __init__(self, *, max_seqs, max_slots, max_step_tokens, pools, step_budget,
-                 cap=128, max_pos=8192, seed=0, stops=(-1,)):
+                 cap=128, max_pos=8192, seed=0, stops=(-1,), page_len=PAGE_LEN):
         import torch
 
+        assert all(p.page_len == page_len for p in pools)
         self.pools = pools
         self.cap = cap
+        self.page_len = page_len
+        self.page_shift = page_len.bit_length() - 1
         pspecs = [P.PagePoolSpec(p.num_pages, p.fixed_pages, p.max_pages) for p in pools]
         ospecs = [O.PagePoolSpec(p.num_pages, p.fixed_pages, p.max_pages) for p in pools]
         self.ps = P.ContinuousBatchScheduler(
-            PAGE_LEN, P.BatchGeometry(max_seqs, max_slots, max_step_tokens, pspecs),
+            page_len, P.BatchGeometry(max_seqs, max_slots, max_step_tokens, pspecs),
             step_budget, list(stops))
         self.os = O.ContinuousBatchScheduler(
-            PAGE_LEN, O.BatchGeometry(max_seqs, max_slots, max_step_tokens, ospecs),
+            page_len, O.BatchGeometry(max_seqs, max_slots, max_step_tokens, ospecs),
             step_budget, list(stops))
         # Arena: per pool, the K region then the V region (bytes).
         self.k_off, self.v_off, off = [], [], 0
@@ -99,7 +103,7 @@ class ServingHarness:
         self.arena_bytes = off
         self.arena_cpu = np.zeros(off // 2, dtype=np.uint16)
         self.arena_dev = torch.zeros(off // 2, dtype=torch.int16, device="cuda")
-        self.mirrors = [P.KVPoolMirror(PAGE_LEN, 1, self.k_off[i], 0, 1,
+        self.mirrors = [P.KVPoolMirror(page_len, 1, self.k_off[i], 0, 1,
                                        [(0, ROW_BYTES), (self.v_off[i] - self.k_off[i], ROW_BYTES)],
                                        pspecs[i]) for i in range(len(pools))]
         self.omirrors = [O.KVPoolMirror(m.page_len, m.pos_shard, m.region_off, m.stride,
@@ -177,7 +181,7 @@ class ServingHarness:
             ks = hashed_bf16(pos, toks, 10 * li + 2, KV_STRIDE)
             vs = hashed_bf16(pos, toks, 10 * li + 3, KV_STRIDE)
             plan = AttentionPlan(table, n, kind=layer.kind, window=layer.window,
-                                 cache_size=layer.cache_size, page_len=PAGE_LEN,
+                                 cache_size=layer.cache_size, page_len=self.page_len,
                                  cache_rows=layer.rows, cap=self.cap, kv_row_bytes=ROW_BYTES)
             kd, vd = self._dev(self.k_off[li], layer.rows), self._dev(self.v_off[li], layer.rows)
             qd = to_dev(q)
@@ -193,7 +197,8 @@ class ServingHarness:
             q_ref = q.copy()
             kc, vc = self._cpu(self.k_off[li], layer.rows), self._cpu(self.v_off[li], layer.rows)
             oracle.rope_cache_write(runs, rows, q_ref, ks, vs, kc, vc, self.cos, self.sin,
-                                    num_q=NUM_Q, num_kv=NUM_KV, page_shift=6, row_mask=63,
+                                    num_q=NUM_Q, num_kv=NUM_KV, page_shift=self.page_shift,
+                                    row_mask=self.page_len - 1,
                                     page_mask=plan.page_mask, seq_len=n, half=HALF,
                                     pair_stride=HALF, head_dim=HEAD_DIM)
             assert np.array_equal(from_dev(qd, np.uint16).ravel(), q_ref.ravel()), "rotated q"
@@ -236,7 +241,7 @@ class ServingHarness:
         ref = oracle.attention(layer.kind, sub_runs, rows, np.ascontiguousarray(q_ref[sel]),
                                kc, vc, num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
                                kv_stride=KV_STRIDE, window=layer.window,
-                               cache_size=layer.cache_size, page_len=PAGE_LEN,
+                               cache_size=layer.cache_size, page_len=self.page_len,
                                seq_len=len(sel), cap=self.cap, threads=16)
         res = compare_bf16(got[sel].ravel(), ref)
         res["tokens"] = int(len(sel))

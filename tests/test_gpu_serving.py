@@ -99,3 +99,44 @@ def test_config4_prefix_sharing_copy_on_write():
                 f"fork {k} ordinal {o} shares the donor's page"
     assert copies > 0 and h.copies_done > 0
     assert h.ps.invariant_failures == (0, 0)
+
+
+def test_config3_ring_serving_loop_page1024():
+    """The same loop at Gemma-4's production geometry: 1024-token pages, the
+    sliding pool on 2-page rings (modeling/gemma4_topology.mojo:36,40), the
+    full layer's pool growing in 1024-token pages; prompts of 1100-2600
+    tokens wrap most rings, then 256 decode steps."""
+    announce("serving loop config3 ring, 1024-token pages")
+    rng = np.random.default_rng(17)
+    B, ring, page = 8, 2, 1024
+    ctx = [int(x) for x in rng.integers(1100, 2601, B)]
+    new_tokens = 300
+    grow_pages = sum((c + new_tokens) // page + 1 for c in ctx) + 2
+    h = ServingHarness(max_seqs=B, max_slots=B, max_step_tokens=1024, step_budget=1024,
+                       pools=[PoolLayer(B * ring, ring, ring, SLIDING, window=1024,
+                                        page_len=page),
+                              PoolLayer(grow_pages, 0, 4, FULL, page_len=page)],
+                       cap=128, max_pos=4096, seed=18, page_len=page)
+    for i in range(B):
+        toks = [int(x) for x in rng.integers(0, 30000, ctx[i])]
+        toks[0] = 42000 + i
+        h.submit(toks, new_tokens)
+    decode_steps = steps = 0
+    while decode_steps < 256:
+        check = steps < 3 or steps % 32 == 0
+        rep = h.step(check_attention=check, rng=rng)
+        assert rep is not None
+        if rep["tokens"] == rep["slots"] == B:
+            decode_steps += 1
+        if steps % 64 == 0:
+            h.compare_arena()
+        if check:
+            print(f"  step {steps}: {rep['tokens']} tokens {rep['slots']} slots "
+                  f"{rep['checks']}", flush=True)
+        steps += 1
+    h.compare_arena()
+    wrapped = sum(h.ps.registry.length(s) > ring * page for s in range(B))
+    print(f"  {steps} steps, {len(h.checked)} attention checks, {wrapped} rings wrapped",
+          flush=True)
+    assert wrapped >= B // 2
+    assert h.ps.invariant_failures == (0, 0)

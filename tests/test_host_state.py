@@ -368,14 +368,16 @@ def test_bind_pool_run_table_matches_pages_and_oracle():
         os_.absorb(om.execute(os_, os_.schedule, os_.pages), oc())
 
 
-def test_config3_ring_256_decode_steps_lockstep():
-    """Config 3's page-state check: 64 sequences on 32-page rings (window
-    1024 at 64-token pages) plus a growing pool, prefilled past the ring
-    wrap, then 256 decode steps of the whole batch; page tables, holds, free
-    stacks and ring floors of the C++ scheduler equal the oracle's after
-    every step."""
+@pytest.mark.parametrize("ring_pages,ppp", [(32, 64), (2, 1024)])
+def test_config3_ring_256_decode_steps_lockstep(ring_pages, ppp):
+    """Config 3's page-state check: 64 sequences on rings of window 1024 x 2
+    positions -- 32 pages of 64 tokens, or Gemma-4's production 2 pages of
+    1024 (modeling/gemma4_topology.mojo:36,40) -- plus a growing pool,
+    prefilled past the ring wrap, then 256 decode steps of the whole batch;
+    page tables, holds, free stacks and ring floors of the C++ scheduler
+    equal the oracle's after every step."""
     rng = np.random.default_rng(33)
-    B, ring_pages, ppp = 64, 32, 64
+    B = 64
     ctx = [int(x) for x in rng.integers(1023, 4096, B)]
     new_tokens = 700
     grow_pages = sum((c + new_tokens) // ppp + 1 for c in ctx)
