@@ -367,14 +367,20 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   // Query blocks for the MFMA prefill (token plans of full attention).
   hdr[kHdrOffQBlocks] = static_cast<int32_t>(off);
   int64_t n_qblocks = 0;
-  // Only when every run's page table fits the kernel's LDS copy.
+  // Only when every run's page table fits the kernel's LDS copy (a sliding
+  // run's table is its ring), and for sliding windows whose span is whole
+  // 16-key tiles (the kernel aligns every row's tiles to 16 up to lo % 16).
   bool mfma_tables_fit = true;
-  for (int64_t r = 0; r < num_runs; ++r) {
-    const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
-    if (e > b && ((runs[4 * r + 1] + (e - 1 - b)) >> g.shift) + 1 > kPrefillLdsPages)
-      mfma_tables_fit = false;
+  if (sliding) {
+    mfma_tables_fit = g.page_mask + 1 <= kPrefillLdsPages && window % kTile == 0;
+  } else {
+    for (int64_t r = 0; r < num_runs; ++r) {
+      const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
+      if (e > b && ((runs[4 * r + 1] + (e - 1 - b)) >> g.shift) + 1 > kPrefillLdsPages)
+        mfma_tables_fit = false;
+    }
   }
-  if (mode == IFR_PLAN_TOKEN_MERGE && mfma_tables_fit) {
+  if ((mode == IFR_PLAN_TOKEN_MERGE || mode == IFR_PLAN_TOKEN_DIRECT) && mfma_tables_fit) {
     std::vector<std::array<int64_t, 4>> qbs;
     for (int64_t r = 0; r < num_runs; ++r) {
       const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
@@ -728,6 +734,17 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
                                           static_cast<int>(num_kv), kv_stride, g,
                                           as_stream(stream)),
             "prefill_full_mfma");
+    return ok();
+  }
+  if (info[2] == IFR_PLAN_TOKEN_DIRECT && info[14] > 0 && head_dim == 256 &&
+      num_q == 2 * num_kv && page_mask >= 0) {
+    // Prefill chunk of a sliding-window layer: MFMA query blocks.
+    IFR_HIP(ifr::launch_prefill_sliding_mfma(static_cast<const int32_t*>(image_dev),
+                                             static_cast<int>(info[14]), q, k_base, v_base,
+                                             output, static_cast<int>(num_q),
+                                             static_cast<int>(num_kv), kv_stride, g,
+                                             static_cast<int>(info[12]), as_stream(stream)),
+            "prefill_sliding_mfma");
     return ok();
   }
   IFR_HIP(ifr::launch_attention_bf16(static_cast<const int32_t*>(image_dev),

@@ -50,6 +50,13 @@ hipError_t launch_prefill_full_mfma(const int32_t* image_dev, int num_qblocks,
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream);
 
+// MFMA chunked prefill, sliding window (head_dim 256, gqa 2, window a
+// multiple of 16): the finalised output of every query block.
+hipError_t launch_prefill_sliding_mfma(const int32_t* image_dev, int num_qblocks,
+                                       const void* q, const void* k_base, const void* v_base,
+                                       void* output, int num_q, int num_kv, int64_t kv_stride,
+                                       PagedGeom geom, int window, hipStream_t stream);
+
 hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
                                int num_units, int mode, const void* q_i8,
                                const float* qi_bias, const float* f_q,

@@ -47,57 +47,14 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "prefill_common.hpp"
 
 namespace ifr {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
+using namespace prefill;
 
-constexpr int kPD = 256;             // head_dim
-constexpr int kPWaves = 4;           // waves per block (one per SIMD, one block per CU)
-constexpr int kPThreads = 64 * kPWaves;
-constexpr int kPTokensPerWave = 16;  // x 2 q heads = 32 rows
-constexpr int kPTokens = kPWaves * kPTokensPerWave;  // tokens per block
-static_assert(kPTokens == kPrefillTokens, "plan query blocks must match the kernel");
-constexpr int kKeys = 64;                // keys per iteration
-constexpr int kBlocks = kKeys / 32;      // 32-key S blocks (tile pairs) per iteration
-constexpr int kDimBlocks = kPD / 32;     // 32-dim blocks of O^T
-constexpr int kRowBytes = kPD * 2;       // one key row of K or V in LDS
-constexpr int kTileBytes = kKeys * kRowBytes;  // 32 KiB: one iteration of K (or V)
-constexpr int kStageRows = kKeys / kPWaves;  // key rows each wave stages per iteration
-static_assert(kStageRows % 2 == 0, "two rows per 64-lane load");
-static_assert(4 * kTileBytes + 4 * kPrefillLdsPages <= 160 * 1024, "LDS budget");
 
-// x + x[lane ^ 32] and max(x, x[lane ^ 32]) through the gfx950 lane swap:
-// with both operands x, the two results hold the low and high member of
-// each pair, so their sum (low + high) is the same in both lanes.
-__device__ __forceinline__ float sum_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
-                                                  false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float max_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
-                                                  false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-// The reference's biased exp (the steps of fexp) with fused multiply-adds.
-// The argument arrives pre-scaled: t = a_magic * x + bias_f, clamped below
-// at x = -87 by the caller.
-constexpr float kExpA = 12102203.16156148f;
-constexpr float kExpBias = 1059208216.0f;
-// The quadratic a + f*(b + c*f) in the mantissa fraction f = F - 1 is
-// evaluated in F = 1 + f itself, F taken straight from the bits:
-// (a - b + c) + F*((b - 2c) + c*F).
-constexpr double kExpQa = 1.6501418352127075, kExpQb = -0.37554836273193359,
-                 kExpQc = 0.38696467876434326;
 // P.V takes P as bf16 hi parts; a tile whose weight sum exceeds this share
 // of the row's running l (l after the tile) also takes the lo parts
 // p - bf16(p).  The row's final share of a tile can only be smaller (later
@@ -105,17 +62,6 @@ constexpr double kExpQa = 1.6501418352127075, kExpQb = -0.37554836273193359,
 // out of a tile below the share moves the output by at most
 // 2^-9 * kLoShare * max|v|.
 constexpr float kLoShare = 0x1p-7f;
-
-__device__ __forceinline__ float fexp_fused_t(float t) {
-  const int32_t i = static_cast<int32_t>(t);
-  const float F = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u);
-  float p = __builtin_fmaf(F, static_cast<float>(kExpQc), static_cast<float>(kExpQb - 2 * kExpQc));
-  p = __builtin_fmaf(F, p, static_cast<float>(kExpQa - kExpQb + kExpQc));
-  return __int_as_float(i) * p;
-}
-__device__ __forceinline__ float fexp_fused(float x) {
-  return fexp_fused_t(__builtin_fmaf(kExpA, fmaxf(x, -87.0f), kExpBias));
-}
 
 // One tile's online-softmax step for this lane's row (process_kv_tile's
 // m / corr / w / l updates, attention_ops.mojo:165-180).  sv[0..7] are the

@@ -1,0 +1,368 @@
+// Chunked prefill with MFMA for sliding-window layers (gfx950).  Semantics:
+// FlashPrefillSlidingKernel (kernels/flash_attention_prefill.mojo:18-114) at
+// degree 1 -- every query token at absolute position p walks keys
+// [lo, p], lo = max(0, p - window + 1), in tiles of 16 from lo with the
+// online softmax of process_kv_tile (kernels/attention_ops.mojo:165-253), and
+// is finalised as acc * (1/l).
+//
+// The block shape, LDS staging, score MFMAs (S^T = K . Q^T on
+// v_mfma_f32_32x32x16_bf16) and P.V MFMAs are those of the full-attention
+// kernel (prefill.hip).  What differs is where a row's tiles start: lo moves
+// by one key per query token, so the reference's tiles of the rows of a
+// block are not aligned with each other.  They are aligned with the key
+// space up to a per-row offset r = lo % 16: each aligned 16-key tile t (keys
+// 16t .. 16t + 15) splits at r into a low part (keys < 16t + r) and a high
+// part, and the row's reference tile J is the high part of aligned tile
+// t - 1 followed by the low part of aligned tile t (r = 0: tile t - 1 whole).
+// A row's tile J is therefore complete once aligned tile t is scored: at
+// that step the row takes the tile's max over its 16 keys (its lane and lane
+// ^ 32), m_new, corr = fexp(m - m_new), the 16 weights and l = l*corr + sum,
+// exactly the reference's per-tile steps.  The weights of aligned tile t - 1
+// are then complete (its low part belonged to tile J - 1, its high part to J)
+// and its P.V MFMA runs; tile t's low-part weights wait one step.  Rows whose
+// window lies before the tile, or that ended earlier, add nothing.  A final
+// step past the last staged tile completes the last reference tile of rows
+// with r = 0.  Pads (keys past p in the last tile of a row with lo = 0) score
+// -1e30: their fexp(-87) enters l, a zero weight P.V.
+//
+// As in the full kernel the accumulator is kept as acc_stored with acc =
+// acc_stored * S; a weight enters the MFMA divided by S right after its own
+// tile, so later rescales need not touch the 128 accumulators (the pending
+// low-part weights follow the rare S -> 1 renormalisation).  P enters as
+// bf16 hi + lo parts, and the biased exp is the fused-FMA form (about 2e-5
+// relative from the reference's separately rounded steps).
+#include "common.hpp"
+#include "launch.hpp"
+#include "prefill_common.hpp"
+
+namespace ifr {
+namespace {
+
+using namespace prefill;
+
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_sliding_mfma_kernel(
+    const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride, int shift,
+    int row_mask, int page_mask, int window) {
+  __shared__ __align__(16) uint8_t kbuf0[kTileBytes];
+  __shared__ __align__(16) uint8_t kbuf1[kTileBytes];
+  __shared__ __align__(16) uint8_t vbuf0[kTileBytes];
+  __shared__ __align__(16) uint8_t vbuf1[kTileBytes];
+  __shared__ int32_t page_rows[kPrefillLdsPages];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int half = lane >> 5;
+  const int row = lane & 31;
+  const int g = blockIdx.x % num_kv;
+  const int qb = blockIdx.x / num_kv;
+
+  const int32_t* blk = image + image[kHdrOffQBlocks] + qb * kQBlockWords;
+  const int run = blk[0];
+  const int t0 = blk[1];
+  const int ntok = blk[2];
+  const int32_t* rp = image + image[kHdrOffRuns] + run * 4;
+  const int buf_start = rp[0];
+  const int base_pos = rp[1];
+  const int32_t* rows = image + image[kHdrOffRows] + rp[2];
+
+  // Keys of the block: [k_lo, p_last]; iterations of 64 keys from k_lo
+  // rounded down to 64.
+  const int p_first = base_pos + (t0 - buf_start);
+  const int p_last = p_first + ntok - 1;
+  const int k_lo = max(0, p_first - window + 1);
+  const int kb0 = k_lo & ~(kKeys - 1);
+  const int n_iters = (p_last + 1 - kb0 + kKeys - 1) / kKeys;
+  const int tile0 = kb0 >> 4;
+
+  // This lane's row: token wave*16 + (l%32)/2, q head 2g + (l%32)%2.
+  const int tok_local = wave * kPTokensPerWave + (row >> 1);
+  const int head = g * 2 + (row & 1);
+  const bool row_live = tok_local < ntok;
+  const int tok = t0 + tok_local;
+  const int p = p_first + tok_local;
+  const int lo = max(0, p - window + 1);
+  const int r = lo & 15;
+  // Aligned tiles at which the row completes a reference tile: (t_first, t_end].
+  const int t_first = row_live ? (lo >> 4) : (1 << 30);
+  const int t_end = row_live ? (p >> 4) + (r == 0 ? 1 : 0) : -1;
+
+  bf16x8_t qf[kPD / 16];
+  {
+    const uint16_t* qr =
+        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * half;
+#pragma unroll
+    for (int d = 0; d < kPD / 16; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
+      qf[d] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
+
+  f32x16_t acc[kDimBlocks];
+#pragma unroll
+  for (int b = 0; b < kDimBlocks; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+  float m = kNegBig, l = 0.0f, S = 1.0f;
+
+  // The run's ring of pages (the planner validated every ordinal the keys
+  // [k_lo, p_last] reach; a run may list fewer pages than the ring holds).
+  const int n_pages = min(page_mask + 1, rp[3]);
+  for (int i = tid; i < n_pages; i += kPThreads) page_rows[i] = rows[i];
+  __syncthreads();
+
+  // Staging of one iteration (as the full kernel's): keys clamped into
+  // [k_lo, p_last]; V rows of keys outside it are zeroed after landing.
+  const uint16_t* kbase = kc + static_cast<int64_t>(g) * kPD;
+  const uint16_t* vbase = vc + static_cast<int64_t>(g) * kPD;
+  const int stage_row0 = wave * kStageRows + half;
+  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+#pragma unroll
+    for (int i = 0; i < kStageRows / 2; ++i) {
+      const int rr = stage_row0 + 2 * i;
+      const int key = min(max(kb0 + it * kKeys + rr, k_lo), p_last);
+      const int64_t slot =
+          static_cast<int64_t>(page_rows[(key >> shift) & page_mask]) + (key & row_mask);
+      const int64_t off = slot * kv_stride;
+      const int lds_row = wave * kStageRows + 2 * i;
+      __builtin_amdgcn_global_load_lds(kbase + off + 8 * (row ^ (rr & 15)),
+                                       (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + off + 8 * (row ^ (2 * (rr & 3))),
+                                       (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+    }
+  };
+  auto zero_outside = [&](int it, uint8_t* vdst) {
+    const int first = kb0 + it * kKeys;
+    if (first >= k_lo && first + kKeys <= p_last + 1) return;  // block-uniform
+#pragma unroll
+    for (int i = 0; i < kStageRows / 2; ++i) {
+      const int rr = stage_row0 + 2 * i;
+      const int key = first + rr;
+      if (key < k_lo || key > p_last)
+        *reinterpret_cast<uint4*>(vdst + rr * kRowBytes + 16 * row) = make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+
+  if (n_iters > 0) stage(0, kbuf0, vbuf0);
+  __builtin_amdgcn_s_waitcnt(0);
+  if (n_iters > 0) zero_outside(0, vbuf0);
+  __syncthreads();
+
+  const int k_lane = row * kRowBytes + 16 * ((row & 15) ^ half);
+  const int vj = lane & 15;
+  const int v_row = (4 * half + (vj >> 2)) * kRowBytes +
+                    32 * (((lane >> 4) & 1) ^ ((vj >> 2) & 1)) + 8 * (vj & 3);
+  const int v_even = v_row + 64 * (vj >> 3);
+  const int v_odd = v_row - 64 * (vj >> 3);
+
+  constexpr int kKAhead = 6;
+  auto qk = [&](const uint8_t* kl, int h) {
+    f32x16_t sblk;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
+    const uint8_t* kh = kl + 32 * h * kRowBytes;
+    uint4 kf[kPD / 16];
+#pragma unroll
+    for (int d = 0; d < kKAhead; ++d)
+      kf[d] = *reinterpret_cast<const uint4*>(kh + (k_lane ^ (32 * d)));
+#pragma unroll
+    for (int d = 0; d < kPD / 16; ++d) {
+      if (d + kKAhead < kPD / 16)
+        kf[d + kKAhead] = *reinterpret_cast<const uint4*>(kh + (k_lane ^ (32 * (d + kKAhead))));
+      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]), qf[d],
+                                                     sblk, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+    for (int d = 0; d < kPD / 16 - kKAhead; ++d) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
+    return sblk;
+  };
+
+  // acc_stored += V^T P^T for the 16-key tile at rows tile_row .. +15 of vl
+  // (P as bf16 hi + lo).
+  auto pv = [&](const uint8_t* vl, int tile_row, const float (&pw)[8]) {
+    bf16x8_t phi, plo;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const bf16x2_t hb = __builtin_convertvector(f32x2_t{pw[i], pw[i + 1]}, bf16x2_t);
+      phi[i] = hb[0];
+      phi[i + 1] = hb[1];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) plo[i] = static_cast<__bf16>(pw[i] - static_cast<float>(phi[i]));
+    const uint8_t* vt = vl + tile_row * kRowBytes;
+#pragma unroll
+    for (int b = 0; b < kDimBlocks; ++b) {
+      const uint8_t* vb = vt + ((b & 1) ? v_odd : v_even) + 64 * b;
+      const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
+      const s16x4_t v1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kRowBytes));
+      const bf16x8_t av =
+          __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, phi, acc[b], 0, 0, 0);
+      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, plo, acc[b], 0, 0, 0);
+    }
+  };
+
+  // Per-step state: the previous aligned tile's scores and the pending
+  // (low-part) weights of the current one.
+  float s_prev[8], pend[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    s_prev[i] = kNegBig;
+    pend[i] = 0.0f;
+  }
+  // Key offset inside an aligned tile of the lane's value i (32x32 C layout).
+  auto key_of = [&](int i) { return 8 * (i >> 2) + 4 * half + (i & 3); };
+
+  // Step of aligned tile t with scores st: completes the row's reference
+  // tile (high part of t - 1, low part of t) when t_first < t <= t_end, then
+  // P.V of tile t - 1 (vprev, rows prev_row ..) unless do_pv is false.
+  auto step = [&](int t, const float (&st)[8], const uint8_t* vprev, int prev_row,
+                  bool do_pv) {
+    const bool fin = t > t_first && t <= t_end;
+    float sel[8];
+    bool low[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kk = key_of(i);
+      low[i] = kk < r;
+      const bool pad = !low[i] && (16 * (t - 1) + kk > p);
+      sel[i] = (fin && !pad) ? (low[i] ? st[i] : s_prev[i]) : kNegBig;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(sel[0], sel[1]), fmaxf(sel[2], sel[3])),
+                     fmaxf(fmaxf(sel[4], sel[5]), fmaxf(sel[6], sel[7])));
+    mx = max_xor32(mx);
+    const float m_new = fmaxf(mx, m);
+    const float c = fexp_fused(m - m_new);
+    const float te = __builtin_fmaf(-kExpA, m_new, kExpBias);
+    const float t_min = __builtin_fmaf(kExpA, -87.0f, kExpBias);
+    float e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = fexp_fused_t(fmaxf(__builtin_fmaf(kExpA, sel[i], te), t_min));
+    float ts = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    ts = sum_xor32(ts);
+    const float corr = fin ? c : 1.0f;
+    if (fin) {
+      l = l * c + ts;
+      m = m_new;
+    }
+    float S_new = S * corr;
+    if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
+#pragma unroll
+      for (int b = 0; b < kDimBlocks; ++b) {
+        f32x16_t tv = acc[b];
+        asm volatile("" : "+v"(tv));
+        acc[b] = tv * S_new;
+        asm volatile("" : "+a"(acc[b]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pend[i] = pend[i] * S_new;
+      S_new = 1.0f;
+    }
+    S = S_new;
+    const float inv_s = __builtin_amdgcn_rcpf(S_new);
+    float pw[8];
+    bool any = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kk = key_of(i);
+      const bool pad = !low[i] && (16 * (t - 1) + kk > p);
+      const float w = (fin && !pad) ? e[i] * inv_s : 0.0f;
+      pw[i] = low[i] ? pend[i] : w;
+      pend[i] = low[i] ? w : 0.0f;
+      s_prev[i] = st[i];
+      any = any || pw[i] != 0.0f;
+    }
+    if (do_pv && __builtin_amdgcn_ballot_w64(any) != 0) pv(vprev, prev_row, pw);  // wave-uniform
+  };
+
+  for (int it = 0; it < n_iters; ++it) {
+    uint8_t* kl = (it & 1) ? kbuf1 : kbuf0;
+    uint8_t* vl = (it & 1) ? vbuf1 : vbuf0;
+    uint8_t* kn = (it & 1) ? kbuf0 : kbuf1;
+    uint8_t* vn = (it & 1) ? vbuf0 : vbuf1;
+    const int tb = tile0 + 4 * it;
+    float st[8];
+    const f32x16_t s0 = qk(kl, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = s0[i];
+    // Tile tb - 1 lies in the other buffer (the previous iteration's last
+    // tile); it is read before that buffer is restaged.
+    step(tb, st, vn, 48, it > 0);
+    __syncthreads();
+    if (it + 1 < n_iters) stage(it + 1, kn, vn);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = s0[8 + i];
+    step(tb + 1, st, vl, 0, true);
+    const f32x16_t s1 = qk(kl, 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = s1[i];
+    step(tb + 2, st, vl, 16, true);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = s1[8 + i];
+    step(tb + 3, st, vl, 32, true);
+#pragma unroll
+    for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
+#pragma unroll
+    for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
+    __builtin_amdgcn_s_waitcnt(0);
+    if (it + 1 < n_iters) zero_outside(it + 1, vn);
+    __syncthreads();
+  }
+  // The step past the last staged tile: completes the last reference tile of
+  // rows with r = 0 and runs the last tile's P.V.
+  if (n_iters > 0) {
+    float st[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = kNegBig;
+    step(tile0 + 4 * n_iters, st, ((n_iters - 1) & 1) ? vbuf1 : vbuf0, 48, true);
+  }
+
+  // Finalisation of the sliding prefill: acc * (1/l).
+  if (row_live) {
+    const bool live = l > 0.0f;
+    const float inv_l = live ? 1.0f / l : 0.0f;
+    uint16_t* dst = out + (static_cast<int64_t>(tok) * num_q + head) * kPD + 4 * half;
+#pragma unroll
+    for (int b = 0; b < kDimBlocks; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float av = acc[b][4 * j + i] * S;
+          e[i] = live ? f32_to_bf16_bits(av * inv_l) : 0u;
+        }
+        *reinterpret_cast<uint2*>(dst + 32 * b + 8 * j) =
+            make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_prefill_sliding_mfma(const int32_t* image, int num_qblocks, const void* q,
+                                       const void* k, const void* v, void* output, int num_q,
+                                       int num_kv, int64_t kv_stride, PagedGeom geom,
+                                       int window, hipStream_t stream) {
+  if (num_qblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(prefill_sliding_mfma_kernel, dim3(num_qblocks * num_kv), dim3(kPThreads),
+                     0, stream, image, static_cast<const uint16_t*>(q),
+                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                     static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
+                     geom.row_mask, geom.page_mask, window);
+  return hipGetLastError();
+}
+
+}  // namespace ifr
