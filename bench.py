@@ -9,7 +9,8 @@ page, log-sum-exp merge.  --config 1, 3 and 5 run the other decode configs
 (single sequence, sliding ring, butterquant int8) the same way, --config 4 the
 chunked prefill.  Widening rows: --config 6 (MiniMax-M3 sparse decode), 7 and
 8 (Gemma-4's full-attention layer, head_dim 512 with 16q/2kv, bf16 and bq),
-9 (copy-on-write page copy) and 10 (row gather).
+9 (copy-on-write page copy), 10 (row gather) and 11 (sliding-window chunked
+prefill).
 
 Inputs (KV pages, queries, RoPE tables, the plan image) are resident in HBM
 before the timed region; the plan is built once, as the reference binds its
@@ -36,7 +37,8 @@ NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 HIDDEN = 2816  # Gemma 4 26B-A4B hidden size: o_proj maps 16 x 256 -> 2816
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
-DEFAULT_CAP = {1: 128, 2: 512, 3: 384, 4: 16, 5: 2048, 6: 0, 7: 1024, 8: 2048, 9: 0, 10: 0}
+DEFAULT_CAP = {1: 128, 2: 512, 3: 384, 4: 16, 5: 2048, 6: 0, 7: 1024, 8: 2048, 9: 0, 10: 0,
+               11: 16}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Gemma-4's two attention layer shapes (modeling/gemma4_common.mojo:10-20):
 # (num_q, num_kv, head_dim, rope_half, pair_stride).  BASELINE's configs 1-5
@@ -930,6 +932,139 @@ class PrefillBf16:
                            f"cap={threads} workers, median of {len(times)}")}
 
 
+class PrefillSliding:
+    """Config 11 (widening): chunked prefill of a sliding-window layer --
+    8 sequences append 2048 tokens each onto prefixes ~ U[0, 16384], each
+    sequence on its own 64-page ring (4096 positions, enough for the chunk
+    and its window), then the sliding prefill over window 1024
+    (FlashPrefillSlidingKernel, kernels/flash_attention_prefill.mojo:18-114),
+    on MFMA when the window is a multiple of 16."""
+
+    dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
+    phases = ("append", "attention")
+    dominant = "prefill_sliding_mfma_kernel"
+    dominant_phase = "attention"
+    bound = "mfma"
+    RING = 64
+
+    def __init__(self, seed: int, window: int):
+        self.seed, self.window = seed, window
+        self.prefix = uniform_ints(seed, 8, 0, 16384)
+        self.new = 2048
+        self.name = (f"config11 (widening): sliding-window chunked prefill, 8 sequences x 2048 "
+                     f"new tokens on prefixes ~ U[0,16384], window {window}, 64-page rings of "
+                     f"64-token pages, 16q/8kv hd256 bf16, append + causal sliding prefill")
+
+    def setup(self, dev, a):
+        import torch
+
+        from inferno_amd import attention as A
+        from inferno_amd.kv import AttentionPlan, KVRunTable
+
+        self.A = A
+        n_seq = len(self.prefix)
+        perm = np.random.default_rng(self.seed).permutation(n_seq * self.RING)
+        table = KVRunTable()
+        for i, p in enumerate(self.prefix):
+            table.begin_run(i * self.new, p)
+            for x in perm[i * self.RING:(i + 1) * self.RING]:
+                table.add_base_row(int(x) * PAGE_LEN)
+        n = n_seq * self.new
+        rows = n_seq * self.RING * PAGE_LEN
+        self.table, self.n = table, n
+        self.stream = torch.cuda.current_stream()
+        sid = int(self.stream.cuda_stream)
+        self.k = torch.empty(rows * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.v = torch.empty_like(self.k)
+        self.q = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.ks = torch.empty(n * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.vs = torch.empty_like(self.ks)
+        for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
+            _fill(t, self.seed * 16 + i, sid)
+        cos, sin = rope_tables(max(self.prefix) + self.new + 1)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        self.plan = AttentionPlan(table, n, kind=0, window=self.window,
+                                  cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN,
+                                  cache_rows=rows, cap=a.cap, kv_row_bytes=KV_STRIDE * 2,
+                                  device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
+        self.out = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+        self.cap = a.cap
+        if int(self.plan.info[14]) == 0:
+            self.dominant = "flash_partial_bf16_kernel (token route) + merge_kernel"
+
+    def launch(self, phase):
+        A, p = self.A, self.plan
+        if phase == "append":
+            A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
+                                        self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
+                                        pair_stride=128, head_dim=HEAD_DIM)
+        else:
+            A.attention_bf16(p, self.q, self.k, self.v, self.out, self.partials, self.ps,
+                             num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
+                             kv_stride=KV_STRIDE)
+
+    def flops(self) -> int:
+        """4 * D * Hq * sum over query tokens of attended keys (QK^T + PV)."""
+        keys = sum(sum(min(p + t + 1, self.window) for t in range(self.new))
+                   for p in self.prefix)
+        return 4 * HEAD_DIM * NUM_Q * keys
+
+    def step_bytes(self) -> int:
+        return self.n * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 3)
+
+    def dominant_bytes(self) -> int:
+        return 0
+
+    def config(self) -> dict:
+        return {"workload": self.name, "sequences": len(self.prefix), "new_tokens": self.new,
+                "prefixes": self.prefix, "window": self.window, "ring_pages": self.RING,
+                "page_len": PAGE_LEN, "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM,
+                "cap": self.cap, "seed": self.seed, "query_blocks": int(self.plan.info[14]),
+                "algorithmic_tflop": round(self.flops() / 1e12, 3)}
+
+    def cpu_baseline(self, budget_s):
+        """The oracle's sliding token route (FlashPrefillSlidingKernel) on the
+        last 16 query tokens of the first sequence."""
+        import torch
+
+        import oracle
+
+        hc = host_cpu()
+        threads = hc["threads"]
+        p0 = self.prefix[0]
+        pages = np.asarray(self.table.base_rows[:self.RING], dtype=np.int64) // PAGE_LEN
+        idx = torch.from_numpy(pages).to(self.k.device)
+        kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
+        vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
+        n_s = 16
+        first = self.new - n_s
+        runs = np.asarray([[0, p0 + first, 0, self.RING]], dtype=np.int32)
+        base = np.arange(self.RING, dtype=np.int32) * PAGE_LEN
+        qh = self.q.view(-1, NUM_Q * HEAD_DIM)[first:self.new]
+        qh = np.ascontiguousarray(qh.cpu().numpy().view(np.uint16).reshape(-1))
+        keys = sum(min(p0 + first + t + 1, self.window) for t in range(n_s))
+        fl = 4 * HEAD_DIM * NUM_Q * keys
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.attention(0, runs, base, qh, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
+                             head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=self.window,
+                             cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
+                             cap=threads, threads=threads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
+                "sample": (f"last {n_s} query tokens of the first sequence ({keys} query-key "
+                           f"pairs), the reference's sliding token route at cap={threads} "
+                           f"workers, median of {len(times)}")}
+
+
 class PageCopyBench:
     """Config 9 (widening): dispatch_copy_jobs (kernels/page_copy.mojo:63-94) as
     copy-on-write of bf16 pages of the 16q/8kv hd256 cache: 2048 page copies
@@ -1135,7 +1270,9 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=tuple(range(1, 11)))
+    ap.add_argument("--config", type=int, default=2, choices=tuple(range(1, 12)))
+    ap.add_argument("--window", type=int, default=1024,
+                    help="config 11: sliding window (a multiple of 16 takes the MFMA kernel)")
     ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
     ap.add_argument("--seed", type=int, default=20241)
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -1178,6 +1315,8 @@ def main() -> None:
         w = PageCopyBench(a.seed)
     elif a.config == 10:
         w = GatherBench(a.seed)
+    elif a.config == 11:
+        w = PrefillSliding(a.seed, a.window)
     else:
         w = DecodeBf16(a.config, a.seed)
     w.setup(dev, a)

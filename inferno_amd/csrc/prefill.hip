@@ -55,13 +55,6 @@ namespace {
 using namespace prefill;
 
 
-// P.V takes P as bf16 hi parts; a tile whose weight sum exceeds this share
-// of the row's running l (l after the tile) also takes the lo parts
-// p - bf16(p).  The row's final share of a tile can only be smaller (later
-// tiles rescale the tile and l alike and add to l), so leaving the lo parts
-// out of a tile below the share moves the output by at most
-// 2^-9 * kLoShare * max|v|.
-constexpr float kLoShare = 0x1p-7f;
 
 // One tile's online-softmax step for this lane's row (process_kv_tile's
 // m / corr / w / l updates, attention_ops.mojo:165-180).  sv[0..7] are the

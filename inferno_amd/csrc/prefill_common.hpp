@@ -55,6 +55,14 @@ constexpr float kExpBias = 1059208216.0f;
 // (a - b + c) + F*((b - 2c) + c*F).
 constexpr double kExpQa = 1.6501418352127075, kExpQb = -0.37554836273193359,
                  kExpQc = 0.38696467876434326;
+// P.V takes P as bf16 hi parts; a tile whose weight sum exceeds this share
+// of the row's running l (l after the tile) also takes the lo parts
+// p - bf16(p).  The row's final share of a tile can only be smaller (later
+// tiles rescale the tile and l alike and add to l), so leaving the lo parts
+// out of a tile below the share moves the output by at most
+// 2^-9 * kLoShare * max|v|.
+constexpr float kLoShare = 0x1p-7f;
+
 __device__ __forceinline__ float fexp_fused_t(float t) {
   const int32_t i = static_cast<int32_t>(t);
   const float F = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u);

@@ -29,8 +29,9 @@
 // acc_stored * S; a weight enters the MFMA divided by S right after its own
 // tile, so later rescales need not touch the 128 accumulators (the pending
 // low-part weights follow the rare S -> 1 renormalisation).  P enters as
-// bf16 hi + lo parts, and the biased exp is the fused-FMA form (about 2e-5
-// relative from the reference's separately rounded steps).
+// bf16 hi parts plus, for tiles that hold a large share of some row's l, the
+// lo parts (the full kernel's gate), and the biased exp is the fused-FMA form
+// (about 2e-5 relative from the reference's separately rounded steps).
 #include "common.hpp"
 #include "launch.hpp"
 #include "prefill_common.hpp"
@@ -186,35 +187,45 @@ void prefill_sliding_mfma_kernel(
     return sblk;
   };
 
-  // acc_stored += V^T P^T for the 16-key tile at rows tile_row .. +15 of vl
-  // (P as bf16 hi + lo).
-  auto pv = [&](const uint8_t* vl, int tile_row, const float (&pw)[8]) {
-    bf16x8_t phi, plo;
+  // acc_stored += V^T P^T for the 16-key tile at rows tile_row .. +15 of vl:
+  // P as bf16 hi parts, and the lo parts p - bf16(p) in a second pass when
+  // some row of the wave draws more than kLoShare of its running l from a
+  // reference tile with weights in this tile (the full kernel's gate: the
+  // lo parts of a smaller share move that row's output by at most
+  // 2^-9 * kLoShare * max|v|).
+  auto pv = [&](const uint8_t* vl, int tile_row, const float (&pw)[8], bool need_lo) {
+    bf16x8_t phi;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
       const bf16x2_t hb = __builtin_convertvector(f32x2_t{pw[i], pw[i + 1]}, bf16x2_t);
       phi[i] = hb[0];
       phi[i + 1] = hb[1];
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) plo[i] = static_cast<__bf16>(pw[i] - static_cast<float>(phi[i]));
     const uint8_t* vt = vl + tile_row * kRowBytes;
+    bf16x8_t av[kDimBlocks];
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) {
       const uint8_t* vb = vt + ((b & 1) ? v_odd : v_even) + 64 * b;
       const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
       const s16x4_t v1 =
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kRowBytes));
-      const bf16x8_t av =
-          __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, phi, acc[b], 0, 0, 0);
-      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, plo, acc[b], 0, 0, 0);
+      av[b] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], phi, acc[b], 0, 0, 0);
+    }
+    if (__builtin_amdgcn_ballot_w64(need_lo) != 0) {  // wave-uniform
+      bf16x8_t plo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) plo[i] = static_cast<__bf16>(pw[i] - static_cast<float>(phi[i]));
+#pragma unroll
+      for (int b = 0; b < kDimBlocks; ++b)
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], plo, acc[b], 0, 0, 0);
     }
   };
 
   // Per-step state: the previous aligned tile's scores and the pending
   // (low-part) weights of the current one.
   float s_prev[8], pend[8];
+  bool pend_big = false;  // the pending weights' reference tile exceeded kLoShare
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     s_prev[i] = kNegBig;
@@ -255,6 +266,7 @@ void prefill_sliding_mfma_kernel(
       l = l * c + ts;
       m = m_new;
     }
+    const bool big = fin && ts > kLoShare * l;
     float S_new = S * corr;
     if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
 #pragma unroll
@@ -272,7 +284,6 @@ void prefill_sliding_mfma_kernel(
     S = S_new;
     const float inv_s = __builtin_amdgcn_rcpf(S_new);
     float pw[8];
-    bool any = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kk = key_of(i);
@@ -281,9 +292,10 @@ void prefill_sliding_mfma_kernel(
       pw[i] = low[i] ? pend[i] : w;
       pend[i] = low[i] ? w : 0.0f;
       s_prev[i] = st[i];
-      any = any || pw[i] != 0.0f;
     }
-    if (do_pv && __builtin_amdgcn_ballot_w64(any) != 0) pv(vprev, prev_row, pw);  // wave-uniform
+    const bool need_lo = pend_big || big;
+    pend_big = big && r != 0;
+    if (do_pv) pv(vprev, prev_row, pw, need_lo);
   };
 
   for (int it = 0; it < n_iters; ++it) {
