@@ -196,6 +196,119 @@ __global__ __launch_bounds__(256) void append_kernel(
   }
 }
 
+// The append without the norm on 16-byte vectors.  A q unit owns 8
+// consecutive rotation pairs (j .. j+7 with their partners at pair_stride +
+// j), a k unit 8 rotation pairs or 8 unrotated elements, a v unit 8
+// elements, so every source element is read once and every output element
+// written once, all with 16-byte loads and stores; each unit issues its
+// loads before any of its math.  The rotation of every pair is rotate()'s, so
+// the bits equal append_kernel<false>'s.  Requires half, pair_stride and
+// head_dim to be multiples of 8 and every base 16-byte aligned (checked by
+// the launcher).
+__device__ __forceinline__ void unpack8_bf16(const uint4& w, float* f) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(x[i]);
+    f[2 * i + 1] = bf16_hi(x[i]);
+  }
+}
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+}
+__device__ __forceinline__ void rotate8(const uint4& lo_in, const uint4& hi_in, const float4& c0,
+                                        const float4& c1, const float4& s0, const float4& s1,
+                                        uint4& lo_out, uint4& hi_out) {
+  float xl[8], xh[8], lo[8], hi[8];
+  unpack8_bf16(lo_in, xl);
+  unpack8_bf16(hi_in, xh);
+  const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rotate(xl[i], xh[i], c[i], sn[i], lo[i], hi[i]);
+  lo_out = make_uint4(pack2_bf16(lo[0], lo[1]), pack2_bf16(lo[2], lo[3]),
+                      pack2_bf16(lo[4], lo[5]), pack2_bf16(lo[6], lo[7]));
+  hi_out = make_uint4(pack2_bf16(hi[0], hi[1]), pack2_bf16(hi[2], hi[3]),
+                      pack2_bf16(hi[4], hi[5]), pack2_bf16(hi[6], hi[7]));
+}
+
+__global__ __launch_bounds__(128) void append_vec_kernel(
+    const int32_t* __restrict__ image, uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ k_src, const uint16_t* __restrict__ v_src,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const float* __restrict__ cos_table, const float* __restrict__ sin_table, int num_q,
+    int num_kv, int shift, int row_mask, int page_mask, int half, int pair_stride,
+    int head_dim) {
+  const int tok = blockIdx.x;
+  const HeadGroup grp = head_group(blockIdx.y, num_q, num_kv);
+  const int n_heads = grp.h1 - grp.h0;
+  const int pairs8 = half >> 3;
+  const int gap = pair_stride - half;
+  const int units_k = pairs8 + ((head_dim - 2 * half) >> 3);
+  const int64_t q_stride = static_cast<int64_t>(num_q) * head_dim;
+  const int64_t kv_stride = static_cast<int64_t>(num_kv) * head_dim;
+  const int64_t g_off = static_cast<int64_t>(grp.h0) * head_dim;
+  const int run = image[image[kHdrOffTokRun] + tok];
+  const int32_t* rp = image + image[kHdrOffRuns] + run * 4;
+  const int pos = rp[1] + (tok - rp[0]);
+  const float* cos_row = cos_table + static_cast<int64_t>(pos) * half;
+  const float* sin_row = sin_table + static_cast<int64_t>(pos) * half;
+
+  if (grp.kind == 0) {
+    uint16_t* qg = q + tok * q_stride + g_off;
+    for (int u = threadIdx.x; u < n_heads * pairs8; u += blockDim.x) {
+      const int h = u / pairs8, j = (u - h * pairs8) * 8;
+      uint16_t* qh = qg + static_cast<int64_t>(h) * head_dim;
+      const uint4 xl = *reinterpret_cast<const uint4*>(qh + j);
+      const uint4 xh = *reinterpret_cast<const uint4*>(qh + pair_stride + j);
+      const float4 c0 = *reinterpret_cast<const float4*>(cos_row + j);
+      const float4 c1 = *reinterpret_cast<const float4*>(cos_row + j + 4);
+      const float4 s0 = *reinterpret_cast<const float4*>(sin_row + j);
+      const float4 s1 = *reinterpret_cast<const float4*>(sin_row + j + 4);
+      uint4 lo, hi;
+      rotate8(xl, xh, c0, c1, s0, s1, lo, hi);
+      *reinterpret_cast<uint4*>(qh + j) = lo;
+      *reinterpret_cast<uint4*>(qh + pair_stride + j) = hi;
+    }
+    return;
+  }
+
+  const int32_t* rows = image + image[kHdrOffRows] + rp[2];
+  const int64_t slot =
+      static_cast<int64_t>(rows[(pos >> shift) & page_mask]) + (pos & row_mask);
+  if (grp.kind == 1) {
+    const uint16_t* kg = k_src + tok * kv_stride + g_off;
+    uint16_t* dg = k_cache + slot * kv_stride + g_off;
+    for (int u = threadIdx.x; u < n_heads * units_k; u += blockDim.x) {
+      const int h = u / units_k, r = u - h * units_k;
+      const uint16_t* sh = kg + static_cast<int64_t>(h) * head_dim;
+      uint16_t* dh = dg + static_cast<int64_t>(h) * head_dim;
+      if (r < pairs8) {
+        const int j = r * 8;
+        const uint4 xl = *reinterpret_cast<const uint4*>(sh + j);
+        const uint4 xh = *reinterpret_cast<const uint4*>(sh + pair_stride + j);
+        const float4 c0 = *reinterpret_cast<const float4*>(cos_row + j);
+        const float4 c1 = *reinterpret_cast<const float4*>(cos_row + j + 4);
+        const float4 s0 = *reinterpret_cast<const float4*>(sin_row + j);
+        const float4 s1 = *reinterpret_cast<const float4*>(sin_row + j + 4);
+        uint4 lo, hi;
+        rotate8(xl, xh, c0, c1, s0, s1, lo, hi);
+        *reinterpret_cast<uint4*>(dh + j) = lo;
+        *reinterpret_cast<uint4*>(dh + pair_stride + j) = hi;
+      } else {
+        const int v = (r - pairs8) * 8;
+        const int e = v < gap ? half + v : pair_stride + half + (v - gap);
+        *reinterpret_cast<uint4*>(dh + e) = *reinterpret_cast<const uint4*>(sh + e);
+      }
+    }
+    return;
+  }
+
+  const uint4* vs = reinterpret_cast<const uint4*>(v_src + tok * kv_stride + g_off);
+  uint4* vd = reinterpret_cast<uint4*>(v_cache + slot * kv_stride + g_off);
+  for (int i = threadIdx.x; i < (n_heads * head_dim) >> 3; i += blockDim.x) vd[i] = vs[i];
+}
+
 // In-place head RMS norm of q, k and v (one block per token and head group).
 __global__ __launch_bounds__(256) void rms_norm_qkv_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v,
@@ -236,6 +349,21 @@ hipError_t launch_rope_cache_write(const int32_t* image, int seq_len, void* q,
                                    int pair_stride, int head_dim,
                                    hipStream_t stream) {
   if (seq_len <= 0) return hipSuccess;
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_src) |
+                          reinterpret_cast<uintptr_t>(v_src) |
+                          reinterpret_cast<uintptr_t>(k_cache) |
+                          reinterpret_cast<uintptr_t>(v_cache) |
+                          reinterpret_cast<uintptr_t>(cos_table) |
+                          reinterpret_cast<uintptr_t>(sin_table);
+  if ((bases & 15) == 0 && half % 8 == 0 && pair_stride % 8 == 0 && head_dim % 8 == 0) {
+    hipLaunchKernelGGL(append_vec_kernel, dim3(seq_len, num_head_groups(num_q, num_kv)),
+                       dim3(128), 0, stream, image, static_cast<uint16_t*>(q),
+                       static_cast<const uint16_t*>(k_src), static_cast<const uint16_t*>(v_src),
+                       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                       cos_table, sin_table, num_q, num_kv, geom.shift, geom.row_mask,
+                       geom.page_mask, half, pair_stride, head_dim);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(append_kernel<false>, dim3(seq_len, num_head_groups(num_q, num_kv)),
                      dim3(256), 0, stream, image, static_cast<uint16_t*>(q),
                      static_cast<const uint16_t*>(k_src), static_cast<const uint16_t*>(v_src),

@@ -96,6 +96,53 @@ def test_config1_append_then_decode(cap):
     _assert_close(from_dev(out, np.uint16), ref, f"config1 cap={cap}")
 
 
+@pytest.mark.parametrize("half,pair,d,q_off", [(128, 128, 256, 0), (64, 256, 512, 0),
+                                               (40, 100, 256, 0), (128, 128, 256, 1)])
+def test_append_vector_and_element_paths(half, pair, d, q_off):
+    """The append's 16-byte path (rope half, pair stride and head_dim
+    multiples of 8 and aligned bases: both Gemma-4 layer geometries, the
+    second with unrotated chunks between and after the pairs) and its element
+    path (a rope half of 40 with pair stride 100; a q base 2 bytes off
+    16-byte alignment), bit-exact against the oracle over 5 runs of 1-40 new
+    tokens whose positions cross page boundaries."""
+    import torch
+
+    announce(f"append paths half={half} pair={pair} d={d} q_off={q_off}")
+    nq, nkv = 4, 2
+    kvs = nkv * d
+    prefix, new = [0, 63, 100, 1000, 5], [40, 2, 29, 1, 17]
+    rng = np.random.default_rng(d + half + q_off)
+    n_pages = [(p + m + PAGE_LEN - 1) // PAGE_LEN for p, m in zip(prefix, new)]
+    perm = rng.permutation(sum(n_pages) + 3)
+    runs, rows, buf, off = [], [], 0, 0
+    for p, m, np_ in zip(prefix, new, n_pages):
+        runs.append([buf, p, len(rows), np_])
+        rows.extend(int(x) * PAGE_LEN for x in perm[off:off + np_])
+        buf, off = buf + m, off + np_
+    runs, rows = np.asarray(runs, np.int32), np.asarray(rows, np.int32)
+    n, cache_rows = buf, (len(perm)) * PAGE_LEN
+    ang = rng.uniform(-3, 3, (max(p + m for p, m in zip(prefix, new)) + 1) * half)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    q = seeded_bf16(n * nq * d, 31)
+    ks, vs = seeded_bf16(n * kvs, 32), seeded_bf16(n * kvs, 33)
+    kc, vc = seeded_bf16(cache_rows * kvs, 34), seeded_bf16(cache_rows * kvs, 35)
+    plan = AttentionPlan(_table(runs, rows), n, kind=FULL, window=0, cache_size=PAGE_LEN,
+                         page_len=PAGE_LEN, cache_rows=cache_rows, cap=16, kv_row_bytes=kvs * 2)
+    q_store = to_dev(np.concatenate([np.zeros(q_off, np.uint16), q]))
+    qd = q_store[q_off:]
+    kd, vd = to_dev(kc), to_dev(vc)
+    A.dispatch_rope_cache_write(plan, qd, to_dev(ks), to_dev(vs), kd, vd, to_dev(cos),
+                                to_dev(sin), num_q=nq, num_kv=nkv, half=half, pair_stride=pair,
+                                head_dim=d)
+    torch.cuda.synchronize()
+    oracle.rope_cache_write(runs, rows, q, ks, vs, kc, vc, cos, sin, num_q=nq, num_kv=nkv,
+                            page_shift=6, row_mask=PAGE_LEN - 1, page_mask=-1, seq_len=n,
+                            half=half, pair_stride=pair, head_dim=d)
+    assert np.array_equal(from_dev(qd, np.uint16), q), "rotated q"
+    assert np.array_equal(from_dev(kd, np.uint16), kc), "k cache"
+    assert np.array_equal(from_dev(vd, np.uint16), vc), "v cache"
+
+
 @pytest.mark.parametrize("cap,ctx_seed", [(64, 0), (1024, 1), (8, 2), (4096, 3)])
 def test_batched_full_decode(cap, ctx_seed):
     """Config 2 shape at reduced batch: ctx ~ U[512, 8192], shared shuffled pool."""
