@@ -9,8 +9,9 @@ page, log-sum-exp merge.  --config 1, 3 and 5 run the other decode configs
 (single sequence, sliding ring, butterquant int8) the same way, --config 4 the
 chunked prefill.  Widening rows: --config 6 (MiniMax-M3 sparse decode), 7 and
 8 (Gemma-4's full-attention layer, head_dim 512 with 16q/2kv, bf16 and bq),
-9 (copy-on-write page copy), 10 (row gather) and 11 (sliding-window chunked
-prefill).
+9 (copy-on-write page copy), 10 (row gather), 11 (sliding-window chunked
+prefill) and 12 (config 4's chunked prefill at the full-attention layer
+shape).
 
 Inputs (KV pages, queries, RoPE tables, the plan image) are resident in HBM
 before the timed region; the plan is built once, as the reference binds its
@@ -38,7 +39,7 @@ HIDDEN = 2816  # Gemma 4 26B-A4B hidden size: o_proj maps 16 x 256 -> 2816
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
 DEFAULT_CAP = {1: 128, 2: 512, 3: 384, 4: 16, 5: 2048, 6: 0, 7: 1024, 8: 2048, 9: 0, 10: 0,
-               11: 16}
+               11: 16, 12: 16}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Gemma-4's two attention layer shapes (modeling/gemma4_common.mojo:10-20):
 # (num_q, num_kv, head_dim, rope_half, pair_stride).  BASELINE's configs 1-5
@@ -759,23 +760,36 @@ class PrefillBf16:
     (ContinuousBatchScheduler.fork_prefix, continuous_batching/scheduler.mojo:
     395-466, copies at :427-436).  A step: the COW copies, the append (RoPE +
     cache write), then causal full-attention prefill over the paged prefix +
-    chunk (MFMA)."""
+    chunk (MFMA).  Config 12 (widening): the same at Gemma-4's full-attention
+    layer shape (16 q / 2 kv heads x 512, partial RoPE over 64 pairs at
+    pair_stride 256; modeling/gemma4_common.mojo:14-20)."""
 
     dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
     phases = ("cow", "append", "attention")
-    dominant = "prefill_full_mfma_kernel"
     dominant_phase = "attention"
     bound = "mfma"
 
-    def __init__(self, seed: int):
+    def __init__(self, seed: int, config: int = 4):
         self.seed = seed
         shared = uniform_ints(seed, 4, 0, 16384)
         self.prefix = [p for p in shared for _ in range(2)]
         self.new = 2048
-        self.name = ("config4: chunked prefill, 8 sequences x 2048 new tokens on prefixes "
+        if config == 12:
+            self.nq, self.nkv, self.hd, self.half, self.pair = 16, 2, 512, 64, 256
+            self.dominant = "prefill_wide_mfma_kernel"
+            label = ("config12 (widening, Gemma-4 full-attention layer): chunked prefill, "
+                     "8 sequences x 2048 new tokens on prefixes ~ U[0,16384] shared by "
+                     "sequence pairs (sealed pages shared, the partial page copied on "
+                     "write), 16q/2kv hd512 bf16, partial RoPE (half 64, pair_stride 256)")
+        else:
+            self.nq, self.nkv, self.hd, self.half, self.pair = 16, 8, 256, 128, 128
+            self.dominant = "prefill_full_mfma_kernel"
+            label = ("config4: chunked prefill, 8 sequences x 2048 new tokens on prefixes "
                      "~ U[0,16384] shared by sequence pairs (sealed pages shared, the partial "
-                     "page copied on write), 16q/8kv hd256 bf16, 64-token pages, COW copy + "
-                     "append + causal MFMA prefill over the paged prefix and chunk")
+                     "page copied on write), 16q/8kv hd256 bf16")
+        self.kvs = self.nkv * self.hd
+        self.name = label + (", 64-token pages, COW copy + append + causal MFMA prefill "
+                             "over the paged prefix and chunk")
 
     def setup(self, dev, a):
         import torch
@@ -818,18 +832,18 @@ class PrefillBf16:
         sid = int(self.stream.cuda_stream)
         # K and V share one arena, as the reference's KV mirror lays the
         # components out, so the copy jobs address both with byte offsets.
-        self.arena = torch.empty(2 * rows * KV_STRIDE, dtype=torch.int16, device=dev)
-        self.k = self.arena[:rows * KV_STRIDE]
-        self.v = self.arena[rows * KV_STRIDE:]
-        self.q = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
-        self.ks = torch.empty(n * KV_STRIDE, dtype=torch.int16, device=dev)
+        self.arena = torch.empty(2 * rows * self.kvs, dtype=torch.int16, device=dev)
+        self.k = self.arena[:rows * self.kvs]
+        self.v = self.arena[rows * self.kvs:]
+        self.q = torch.empty(n * self.nq * self.hd, dtype=torch.int16, device=dev)
+        self.ks = torch.empty(n * self.kvs, dtype=torch.int16, device=dev)
         self.vs = torch.empty_like(self.ks)
         for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
             _fill(t, self.seed * 16 + i, sid)
         # COW jobs: rows [0, p % 64) of the first's partial prefix page into the
         # second's own page at the same ordinal, for K and V
         # (append_prefix_copy_jobs, modeling/kv_policy.mojo:59-78).
-        row_bytes = KV_STRIDE * 2
+        row_bytes = self.kvs * 2
         v_base = rows * row_bytes
         jobs = []
         for i in range(1, n_seq, 2):
@@ -843,13 +857,13 @@ class PrefillBf16:
                 jobs.append([base + src * row_bytes, base + dst * row_bytes, nb])
         self.jobs = np.asarray(jobs, dtype=np.int64).reshape(-1, 3)
         self.cow = CopyStager(self.jobs, dev) if len(jobs) else None
-        cos, sin = rope_tables(max(self.prefix) + self.new + 1)
+        cos, sin = rope_tables(max(self.prefix) + self.new + 1, self.half)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.plan = AttentionPlan(table, n, kind=1, window=0, cache_size=PAGE_LEN,
                                   page_len=PAGE_LEN, cache_rows=rows, cap=a.cap,
-                                  kv_row_bytes=KV_STRIDE * 2, device=dev)
-        self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
-        self.out = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
+                                  kv_row_bytes=self.kvs * 2, device=dev)
+        self.partials, self.ps = A.partials_buffer(self.plan, self.nq, self.hd)
+        self.out = torch.empty(n * self.nq * self.hd, dtype=torch.int16, device=dev)
         self.cap = a.cap
 
     def launch(self, phase):
@@ -859,21 +873,21 @@ class PrefillBf16:
                 self.cow(self.arena, self.stream)
         elif phase == "append":
             A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
-                                        self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
-                                        pair_stride=128, head_dim=HEAD_DIM)
+                                        self.sin, num_q=self.nq, num_kv=self.nkv,
+                                        half=self.half, pair_stride=self.pair, head_dim=self.hd)
         else:
             A.attention_bf16(p, self.q, self.k, self.v, self.out, self.partials, self.ps,
-                             num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
-                             kv_stride=KV_STRIDE)
+                             num_q=self.nq, num_kv=self.nkv, head_dim=self.hd,
+                             kv_stride=self.kvs)
 
     def flops(self) -> int:
         """4 * D * Hq * sum over query tokens of attended keys (QK^T + PV)."""
         keys = sum(sum(p + t + 1 for t in range(self.new)) for p in self.prefix)
-        return 4 * HEAD_DIM * NUM_Q * keys
+        return 4 * self.hd * self.nq * keys
 
     def step_bytes(self) -> int:
         cow = 2 * int(self.jobs[:, 2].sum()) if self.jobs.size else 0
-        return self.n * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 3) + cow
+        return self.n * (self.kvs * 2 * 2 * 2 + self.nq * self.hd * 2 * 3) + cow
 
     def dominant_bytes(self) -> int:
         return 0
@@ -884,7 +898,7 @@ class PrefillBf16:
                 "shared_pages": sum(p // PAGE_LEN for p in self.prefix[1::2]),
                 "cow_jobs": int(self.jobs.shape[0]),
                 "cow_bytes": int(self.jobs[:, 2].sum()) if self.jobs.size else 0,
-                "num_q": NUM_Q, "num_kv": NUM_KV, "head_dim": HEAD_DIM, "cap": self.cap,
+                "num_q": self.nq, "num_kv": self.nkv, "head_dim": self.hd, "cap": self.cap,
                 "seed": self.seed, "query_blocks": int(self.plan.info[14]),
                 "algorithmic_tflop": round(self.flops() / 1e12, 3)}
 
@@ -902,24 +916,24 @@ class PrefillBf16:
         pages = np.asarray(self.tables[i], dtype=np.int64)
         npage = pages.size
         idx = torch.from_numpy(pages).to(self.k.device)
-        kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
-        vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
+        kp = self.k.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
+        vp = self.v.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
         kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
         vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
         n_s = 16
         first = self.new - n_s
         runs = np.asarray([[0, p0 + first, 0, npage]], dtype=np.int32)
         base = np.arange(npage, dtype=np.int32) * PAGE_LEN
-        qh = self.q.view(-1, NUM_Q * HEAD_DIM)[i * self.new + first:(i + 1) * self.new]
+        qh = self.q.view(-1, self.nq * self.hd)[i * self.new + first:(i + 1) * self.new]
         qh = np.ascontiguousarray(qh.cpu().numpy().view(np.uint16).reshape(-1))
         keys = sum(p0 + first + t + 1 for t in range(n_s))
-        fl = 4 * HEAD_DIM * NUM_Q * keys
+        fl = 4 * self.hd * self.nq * keys
         times = []
         t_end = time.perf_counter() + budget_s
         while len(times) < 5 and (not times or time.perf_counter() < t_end):
             t0 = time.perf_counter()
-            oracle.attention(1, runs, base, qh, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
-                             head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
+            oracle.attention(1, runs, base, qh, kp, vp, num_q=self.nq, num_kv=self.nkv,
+                             head_dim=self.hd, kv_stride=self.kvs, window=0,
                              cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
                              cap=threads, threads=threads)
             times.append(time.perf_counter() - t0)
@@ -1270,7 +1284,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=tuple(range(1, 12)))
+    ap.add_argument("--config", type=int, default=2, choices=tuple(range(1, 13)))
     ap.add_argument("--window", type=int, default=1024,
                     help="config 11: sliding window (a multiple of 16 takes the MFMA kernel)")
     ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
@@ -1309,8 +1323,8 @@ def main() -> None:
         w = SparseM3(a.seed)
     elif a.config in (5, 8):
         w = DecodeBq(a.config, a.seed)
-    elif a.config == 4:
-        w = PrefillBf16(a.seed)
+    elif a.config in (4, 12):
+        w = PrefillBf16(a.seed, a.config)
     elif a.config == 9:
         w = PageCopyBench(a.seed)
     elif a.config == 10:

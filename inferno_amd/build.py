@@ -29,8 +29,8 @@ LIB = PKG / "libinferno_hip.so"
 OBJ_DIR = PKG.parent / "_build" / "obj"
 ARCH = "gfx950"
 
-SOURCES = ["api.hip", "attention.hip", "attention_wide.hip", "append.hip", "copy.hip", "bq.hip", "prefill.hip", "prefill_sliding.hip",
-           "gemm.hip", "sparse.hip"]
+SOURCES = ["api.hip", "attention.hip", "attention_wide.hip", "append.hip", "copy.hip", "bq.hip",
+           "prefill.hip", "prefill_sliding.hip", "prefill_wide.hip", "gemm.hip", "sparse.hip"]
 # Host-only C++ (page state, scheduler): built with the host compiler.
 HOST_SOURCES = ["host_state.cpp", "host_api.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}"]

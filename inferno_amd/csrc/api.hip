@@ -736,6 +736,19 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
             "prefill_full_mfma");
     return ok();
   }
+  if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 512 &&
+      num_q == 8 * num_kv && page_mask < 0 &&
+      (info[13] >> g.shift) + 1 <= ifr::prefill_wide_max_pages()) {
+    // The same at Gemma-4's full-attention shape (head_dim 512, GQA 8); its
+    // LDS page table is smaller, so longer runs take the token route.
+    IFR_HIP(ifr::launch_prefill_wide_mfma(static_cast<const int32_t*>(image_dev),
+                                          static_cast<int>(info[14]), q, k_base, v_base,
+                                          output, static_cast<int>(num_q),
+                                          static_cast<int>(num_kv), kv_stride, g,
+                                          as_stream(stream)),
+            "prefill_wide_mfma");
+    return ok();
+  }
   if (info[2] == IFR_PLAN_TOKEN_DIRECT && info[14] > 0 && head_dim == 256 &&
       num_q == 2 * num_kv && page_mask >= 0) {
     // Prefill chunk of a sliding-window layer: MFMA query blocks.

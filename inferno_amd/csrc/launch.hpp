@@ -49,6 +49,13 @@ hipError_t launch_prefill_full_mfma(const int32_t* image_dev, int num_qblocks,
                                     const void* v_base, void* output, int num_q,
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream);
+// The same for head_dim 512 / 8 q heads per kv head (prefill_wide.hip), for
+// runs of at most prefill_wide_max_pages() pages.
+int prefill_wide_max_pages();
+hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const void* q,
+                                    const void* k, const void* v, void* output, int num_q,
+                                    int num_kv, int64_t kv_stride, PagedGeom geom,
+                                    hipStream_t stream);
 
 // MFMA chunked prefill, sliding window (head_dim 256, gqa 2, window a
 // multiple of 16): the finalised output of every query block.

@@ -1,6 +1,8 @@
 // Shared pieces of the MFMA chunked-prefill kernels (prefill.hip: full
-// attention; prefill_sliding.hip: sliding window): block geometry, LDS tile
-// sizes, lane-pair reductions and the biased exp with fused multiply-adds.
+// attention; prefill_wide.hip: full attention at head_dim 512 / GQA 8;
+// prefill_sliding.hip: sliding window): block geometry, LDS tile sizes,
+// lane-pair reductions, the biased exp with fused multiply-adds and the
+// per-tile online-softmax step.
 #pragma once
 
 #include "common.hpp"
@@ -72,6 +74,60 @@ __device__ __forceinline__ float fexp_fused_t(float t) {
 }
 __device__ __forceinline__ float fexp_fused(float x) {
   return fexp_fused_t(__builtin_fmaf(kExpA, fmaxf(x, -87.0f), kExpBias));
+}
+
+// One tile's online-softmax step for this lane's row (process_kv_tile's
+// m / corr / w / l updates, attention_ops.mojo:165-180).  sv[0..7] are the
+// lane's 8 keys of the tile, key 8*(i/4) + 4*half + i%4 for value i.
+// Masked: the tile reaches past some row's last key (or the row is empty);
+// a row with no key in the tile is left untouched (corr 1, weights 0), pads
+// score -1e30 and enter l only.  The in-lane sum of the 8 weights comes
+// first, then lane ^32's (the same 16 weights as the reference's halving
+// tree, added in another order).  Maxima use v_max_f32 (the scores are
+// finite for finite inputs).  big: the tile's weight sum exceeds kLoShare of
+// the updated l.
+template <bool kMasked>
+__device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, int half,
+                                             float& m, float& l, float& corr, float (&w)[8],
+                                             bool& big) {
+  float sc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int key = 8 * (i >> 2) + 4 * half + (i & 3);
+    sc[i] = (!kMasked || key < valid) ? sv[i] : kNegBig;
+  }
+  float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                   fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+  mx = max_xor32(mx);
+  const float m_new = fmaxf(mx, m);
+  const float c = fexp_fused(m - m_new);
+  // a*(s - m_new) + bias as one fma per key, clamped at s - m_new = -87.
+  const float t0 = __builtin_fmaf(-kExpA, m_new, kExpBias);
+  const float t_min = __builtin_fmaf(kExpA, -87.0f, kExpBias);
+  float e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = fexp_fused_t(fmaxf(__builtin_fmaf(kExpA, sc[i], t0), t_min));
+  float ts = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+  ts = sum_xor32(ts);
+  if (kMasked) {
+    const bool any = valid > 0;
+    l = any ? l * c + ts : l;
+    m = any ? m_new : m;
+    corr = any ? c : 1.0f;
+    big = any && ts > kLoShare * l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = 8 * (i >> 2) + 4 * half + (i & 3);
+      w[i] = key < valid ? e[i] : 0.0f;
+    }
+  } else {
+    l = l * c + ts;
+    m = m_new;
+    corr = c;
+    big = ts > kLoShare * l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = e[i];
+  }
 }
 
 }  // namespace prefill

@@ -1,0 +1,459 @@
+// Chunked causal prefill with MFMA for Gemma-4's full-attention layers:
+// head_dim 512 with 8 q heads per kv head (16 q / 2 kv heads,
+// modeling/gemma4_common.mojo:14-20, prefilled through dispatch_full_attention
+// at modeling/gemma_4_moe.mojo:415-479).  Semantics: FlashPrefillFullKernel +
+// PrefillMergeKernel (kernels/flash_attention_prefill.mojo:117-248) at
+// degree 1, as in prefill_full_mfma_kernel -- every query token at position
+// p walks keys [0, p] in tiles of 16 from key 0 with the online softmax of
+// process_kv_tile (kernels/attention_ops.mojo:165-253), then its one-segment
+// merge (kernels/logsum_merge.mojo:28-122).
+//
+// A row is one (query token, q head).  A pair of waves owns 32 rows = 4
+// tokens x the 8 q heads of one kv head; wave 2p + h of the pair takes dims
+// 256h .. 256h + 255: it holds the Q^T fragments of those dims (64
+// registers) and the O^T accumulator of those output dims (128 registers),
+// the budget of the 256-dim kernel.  Per 32-key iteration each wave forms
+// its half of the scores, S_h^T = K[:, dims of h] . Q_h^T (16 x
+// v_mfma_f32_32x32x16_bf16), the two halves are exchanged through LDS and
+// added in the fixed order S_0 + S_1, so both waves of the pair hold the
+// same score bits, run the same softmax and fold, and each accumulates its
+// own output dims: O_h^T += V^T[dims of h] . P'^T (8 dim blocks x 2 tiles,
+// + lo).  A block of 4 waves (one per SIMD, one block per CU) owns 8 tokens;
+// a plan query block of 64 tokens is 8 such blocks.  Every K and V fragment
+// read from LDS feeds 32 rows, as in the 256-dim kernel.
+//
+// The C layout, the per-tile softmax (softmax_tile), the folded rescales
+// with the per-row scale S, the hi + lo bf16 parts of P under the kLoShare
+// gate, the fused-FMA biased exp, the swizzled K/V rows staged straight
+// into LDS (32 keys of 1 KiB rows, double-buffered) and the transposing
+// V^T reads are those of prefill_full_mfma_kernel (prefill.hip).
+//
+// Blocks run in an XCD-aware order: launch block b runs work item
+// (b % 8) * per_xcd + b / 8, so the consecutive items of one plan query
+// block (its 8 sub-blocks x kv heads) run on one XCD and share its L2.
+#include <type_traits>
+
+#include "common.hpp"
+#include "launch.hpp"
+#include "prefill_common.hpp"
+
+namespace ifr {
+namespace {
+
+using namespace prefill;
+
+constexpr int kWD = 512;                   // head_dim
+constexpr int kWHalf = kWD / 2;            // dims per wave of a pair
+constexpr int kWG = 8;                     // q heads per kv head
+constexpr int kWTokensPerPair = 32 / kWG;  // 4 tokens x 8 heads = 32 rows
+constexpr int kWTokens = (kPWaves / 2) * kWTokensPerPair;  // 8 tokens per block
+constexpr int kWSub = kPrefillTokens / kWTokens;            // blocks per plan query block
+constexpr int kWKeys = 32;                 // keys per iteration (one S block, two tiles)
+constexpr int kWRowBytes = kWD * 2;        // one key row of K or V in LDS
+constexpr int kWTileBytes = kWKeys * kWRowBytes;  // 32 KiB
+constexpr int kWDimBlocks = kWHalf / 32;   // 32-dim blocks of a wave's O^T
+constexpr int kWStageRows = kWKeys / kPWaves;  // key rows each wave stages
+constexpr int kWXBytes = 64 * 16 * 4;      // one wave's score half (16 floats per lane)
+constexpr int kWLdsPages = 2048;           // page-table entries held in LDS
+constexpr int kXcds = 8;
+static_assert(kPrefillTokens % kWTokens == 0, "plan query blocks split into kernel blocks");
+static_assert(4 * kWTileBytes + kPWaves * kWXBytes + 4 * kWLdsPages <= 160 * 1024,
+              "LDS budget");
+
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_wide_mfma_kernel(
+    const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride, int shift,
+    int row_mask, int num_items, int per_xcd) {
+  __shared__ __align__(16) uint8_t kbuf0[kWTileBytes];
+  __shared__ __align__(16) uint8_t kbuf1[kWTileBytes];
+  __shared__ __align__(16) uint8_t vbuf0[kWTileBytes];
+  __shared__ __align__(16) uint8_t vbuf1[kWTileBytes];
+  __shared__ __align__(16) uint8_t xbuf[kPWaves * kWXBytes];
+  __shared__ int32_t page_rows[kWLdsPages];
+  const int item = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (item >= num_items) return;  // block-uniform, before any barrier
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pair = wave >> 1;
+  const int dh = wave & 1;  // dim half of this wave
+  const int lane = tid & 63;
+  const int half = lane >> 5;
+  const int row = lane & 31;
+  const int g = item % num_kv;
+  const int sub = (item / num_kv) % kWSub;
+  const int qb = item / (num_kv * kWSub);
+
+  const int32_t* blk = image + image[kHdrOffQBlocks] + qb * kQBlockWords;
+  const int run = blk[0];
+  const int t0 = blk[1] + sub * kWTokens;
+  const int ntok = min(kWTokens, blk[2] - sub * kWTokens);
+  if (ntok <= 0) return;  // block-uniform
+  const int32_t* rp = image + image[kHdrOffRuns] + run * 4;
+  const int buf_start = rp[0];
+  const int base_pos = rp[1];
+  const int32_t* rows = image + image[kHdrOffRows] + rp[2];
+
+  // Keys the block needs: [0, count_max).
+  const int count_max = base_pos + (t0 + ntok - 1 - buf_start) + 1;
+  const int n_iters = (count_max + kWKeys - 1) / kWKeys;
+
+  // This lane's row: token 4*pair + (l%32)/8, q head 8g + (l%32)%8.
+  const int tok_local = pair * kWTokensPerPair + (row >> 3);
+  const int head = g * kWG + (row & 7);
+  const bool row_live = tok_local < ntok;
+  const int tok = t0 + tok_local;
+  const int count = row_live ? base_pos + (tok - buf_start) + 1 : 0;
+  const int pair_first = pair * kWTokensPerPair;
+  const int pair_last = min(ntok, pair_first + kWTokensPerPair) - 1;
+  const int pair_count = pair_first < ntok ? base_pos + (t0 + pair_last - buf_start) + 1 : 0;
+  // Keys below pair_min are valid for every row of the pair.
+  const int pair_min = pair_first + kWTokensPerPair <= ntok
+                           ? base_pos + (t0 + pair_first - buf_start) + 1
+                           : 0;
+
+  // Q^T fragments of this wave's dims: lane holds
+  // Q[row][256*dh + 16*d + 8*half .. +7] for 16-dim steps d.  In AGPRs, as in
+  // the 256-dim kernel.
+  bf16x8_t qf[kWHalf / 16];
+  {
+    const uint16_t* qr = q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kWD +
+                         kWHalf * dh + 8 * half;
+#pragma unroll
+    for (int d = 0; d < kWHalf / 16; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
+      qf[d] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < kWHalf / 16; ++d) asm volatile("" : "+a"(qf[d]));
+
+  // acc = acc_stored * S (prefill_full_mfma_kernel's scheme).
+  f32x16_t acc[kWDimBlocks];
+#pragma unroll
+  for (int b = 0; b < kWDimBlocks; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+  float m = kNegBig, l = 0.0f, S = 1.0f;
+
+  const int n_pages = count_max > 0 ? ((count_max - 1) >> shift) + 1 : 0;
+  for (int i = tid; i < n_pages; i += kPThreads) page_rows[i] = rows[i];
+  __syncthreads();
+
+  // Staging: wave w moves key rows kWStageRows*w .. +7 of K and of V, one
+  // 1 KiB row per load (lane p: 16 bytes).  Lane p writes LDS chunk p; for K
+  // it holds global chunk p ^ (key & 15), for V chunk p ^ 2*(key & 3).  Keys
+  // past count_max read the last key (in bounds); their V rows are zeroed
+  // once the loads have landed.
+  const uint16_t* kbase = kc + static_cast<int64_t>(g) * kWD;
+  const uint16_t* vbase = vc + static_cast<int64_t>(g) * kWD;
+  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+#pragma unroll
+    for (int i = 0; i < kWStageRows; ++i) {
+      const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
+      const int key = min(it * kWKeys + r, count_max - 1);
+      const int prow = __builtin_amdgcn_readfirstlane(page_rows[key >> shift]);
+      const int64_t off = (static_cast<int64_t>(prow) + (key & row_mask)) * kv_stride;
+      __builtin_amdgcn_global_load_lds(kbase + off + 8 * (lane ^ (r & 15)),
+                                       (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + off + 8 * (lane ^ (2 * (r & 3))),
+                                       (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
+    }
+  };
+  auto zero_tail = [&](int it, uint8_t* vdst) {
+    if ((it + 1) * kWKeys <= count_max) return;  // block-uniform
+#pragma unroll
+    for (int i = 0; i < kWStageRows; ++i) {
+      const int r = wave * kWStageRows + i;
+      if (it * kWKeys + r >= count_max)
+        *reinterpret_cast<uint4*>(vdst + r * kWRowBytes + 16 * lane) =
+            make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+
+  if (n_iters > 0) stage(0, kbuf0, vbuf0);
+  __builtin_amdgcn_s_waitcnt(0);
+  if (n_iters > 0) zero_tail(0, vbuf0);
+  __syncthreads();
+
+  // QK operand reads: chunk 32*dh + 2d + half of key row (row & 31), stored
+  // at chunk (32*dh + 2d + half) ^ (row & 15): byte address k_lane ^ 32d.
+  const int k_lane = row * kWRowBytes + 512 * dh + 16 * ((row & 15) ^ half);
+  // Transposing V^T reads, as in prefill_full_mfma_kernel at 1 KiB rows,
+  // offset to this wave's dims.
+  const int vj = lane & 15;
+  const int v_row = (4 * half + (vj >> 2)) * kWRowBytes + 512 * dh +
+                    32 * (((lane >> 4) & 1) ^ ((vj >> 2) & 1)) + 8 * (vj & 3);
+  const int v_even = v_row + 64 * (vj >> 3);
+  const int v_odd = v_row - 64 * (vj >> 3);
+  // Score halves: chunk c of lane l at byte 1024*c + 16*l of the wave's slot.
+  uint8_t* x_own = xbuf + wave * kWXBytes + 16 * lane;
+  const uint8_t* x_s0 = xbuf + (wave & ~1) * kWXBytes + 16 * lane;
+  const uint8_t* x_s1 = xbuf + (wave | 1) * kWXBytes + 16 * lane;
+
+  constexpr int kKAhead = 6;
+  auto qk = [&](const uint8_t* kl) {
+    f32x16_t sblk;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
+    uint4 kf[kWHalf / 16];
+#pragma unroll
+    for (int d = 0; d < kKAhead; ++d)
+      kf[d] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * d)));
+#pragma unroll
+    for (int d = 0; d < kWHalf / 16; ++d) {
+      if (d + kKAhead < kWHalf / 16)
+        kf[d + kKAhead] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * (d + kKAhead))));
+      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]), qf[d],
+                                                     sblk, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+    for (int d = 0; d < kWHalf / 16 - kKAhead; ++d) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
+    return sblk;
+  };
+  // The pair's full scores: own half out, barrier, the other half in, added
+  // as S_0 + S_1 in both waves.
+  auto exchange = [&](const f32x16_t& own) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<float4*>(x_own + 1024 * c) =
+          make_float4(own[4 * c], own[4 * c + 1], own[4 * c + 2], own[4 * c + 3]);
+    __syncthreads();
+    f32x16_t sfull;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 a = *reinterpret_cast<const float4*>(x_s0 + 1024 * c);
+      const float4 b = *reinterpret_cast<const float4*>(x_s1 + 1024 * c);
+      sfull[4 * c] = a.x + b.x;
+      sfull[4 * c + 1] = a.y + b.y;
+      sfull[4 * c + 2] = a.z + b.z;
+      sfull[4 * c + 3] = a.w + b.w;
+    }
+    return sfull;
+  };
+  auto softmax_pair = [&](const f32x16_t& sblk, int tile_key0, bool masked, float (&w)[2][8],
+                          float (&corr)[2], bool (&big)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = sblk[8 * u + i];
+      if (!masked) {
+        softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u], big[u]);
+      } else {
+        corr[u] = 1.0f;
+        big[u] = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[u][i] = 0.0f;
+        const int tk = tile_key0 + 16 * u;
+        if (tk < pair_count) {  // wave-uniform (the same in both waves of the pair)
+          if (tk + 16 <= pair_min) {
+            softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u], big[u]);
+          } else {
+            const int valid = min(16, max(0, count - tk));
+            softmax_tile<true>(sv, valid, half, m, l, corr[u], w[u], big[u]);
+          }
+        }
+      }
+    }
+  };
+  // Fold of the two tiles and acc_stored += V^T P''^T (prefill.hip's fold_pv
+  // on one 32-key block).
+  auto fold_pv = [&](const uint8_t* vl, const float (&w)[2][8], const float (&corr)[2],
+                     const bool (&big)[2]) {
+    float S_new = S * (corr[0] * corr[1]);
+    if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
+#pragma unroll
+      for (int b = 0; b < kWDimBlocks; ++b) {
+        f32x16_t t = acc[b];
+        asm volatile("" : "+v"(t));
+        acc[b] = t * S_new;
+        asm volatile("" : "+a"(acc[b]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      S_new = 1.0f;
+    }
+    S = S_new;
+    const float inv_s = __builtin_amdgcn_rcpf(S_new);
+    const float fs[2] = {corr[1] * inv_s, inv_s};
+    bf16x8_t phi[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const bf16x2_t hb =
+            __builtin_convertvector(f32x2_t{w[u][i] * fs[u], w[u][i + 1] * fs[u]}, bf16x2_t);
+        phi[u][i] = hb[0];
+        phi[u][i + 1] = hb[1];
+      }
+    }
+    // V^T operands of tile u, dim blocks b0 .. b0+3 (8 transposing reads).
+    auto read_group = [&](int u, int b0, bf16x8_t (&av)[4]) {
+      const uint8_t* vt = vl + 16 * u * kWRowBytes;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint8_t* vb = vt + (((b0 + b) & 1) ? v_odd : v_even) + 64 * (b0 + b);
+        const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
+        const s16x4_t v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kWRowBytes));
+        av[b] = __builtin_bit_cast(bf16x8_t,
+                                   __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    auto mfma_group = [&](const bf16x8_t& p, int b0, const bf16x8_t (&av)[4]) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], p, acc[b0 + b], 0, 0, 0);
+    };
+    {
+      bf16x8_t ga[4], gb[4];
+      read_group(0, 0, ga);
+      read_group(0, 4, gb);
+      mfma_group(phi[0], 0, ga);
+      read_group(1, 0, ga);
+      mfma_group(phi[0], 4, gb);
+      read_group(1, 4, gb);
+      mfma_group(phi[1], 0, ga);
+      mfma_group(phi[1], 4, gb);
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (__builtin_amdgcn_ballot_w64(big[u]) != 0) {  // wave-uniform
+        bf16x8_t plo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
+        bf16x8_t ga[4], gb[4];
+        read_group(u, 0, ga);
+        read_group(u, 4, gb);
+        mfma_group(plo, 0, ga);
+        mfma_group(plo, 4, gb);
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
+    }
+  };
+
+  auto iteration_end = [&](int it, uint8_t* vnext) {
+#pragma unroll
+    for (int b = 0; b < kWDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
+#pragma unroll
+    for (int d = 0; d < kWHalf / 16; ++d) asm volatile("" : "+a"(qf[d]));
+    __builtin_amdgcn_s_waitcnt(0);
+    if (it + 1 < n_iters) zero_tail(it + 1, vnext);
+    __syncthreads();
+  };
+  // An iteration whose keys are valid for every row of the block.  The
+  // next iteration's rows are staged unconditionally (past the last
+  // iteration they are clamped, in-bounds rows of an unused buffer).
+  auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
+                            uint8_t* vnext) {
+    stage(it + 1, knext, vnext);
+    float w[2][8], corr[2];
+    bool big[2];
+    const f32x16_t s = exchange(qk(kl));
+    softmax_pair(s, 0, false, w, corr, big);
+    fold_pv(vl, w, corr, big);
+    iteration_end(it, vnext);
+  };
+  // An iteration on the causal diagonal: per-tile masks; a pair whose rows
+  // all end before the iteration skips its work but not the barriers.
+  auto masked_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
+                              uint8_t* vnext) {
+    const int key_base = it * kWKeys;
+    if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+    const bool work = key_base < pair_count;  // wave-uniform
+    f32x16_t own;
+    if (work) {
+      own = qk(kl);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) own[v] = 0.0f;
+    }
+    const f32x16_t s = exchange(own);
+    if (work) {
+      float w[2][8], corr[2];
+      bool big[2];
+      softmax_pair(s, key_base, true, w, corr, big);
+      fold_pv(vl, w, corr, big);
+    }
+    iteration_end(it, vnext);
+  };
+
+  // Iterations whose keys are valid for every row of the block run the
+  // unmasked code, in pairs so that each buffer is a fixed LDS object; the
+  // rest (the causal diagonal, and an odd one left over) the masked code.
+  // All waves of the block run the same iterations and barriers.
+  const int block_min = ntok == kWTokens ? base_pos + (t0 - buf_start) + 1 : 0;
+  const int it_full = min(n_iters, block_min / kWKeys) & ~1;
+  int it = 0;
+  for (; it < it_full; it += 2) {
+    full_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
+    full_iteration(it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
+  }
+  for (; it < n_iters; ++it) {
+    if (it & 1)
+      masked_iteration(it, kbuf1, vbuf1, kbuf0, vbuf0);
+    else
+      masked_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
+  }
+
+  // ---- one-segment merge and bf16 store (PrefillMergeKernel) ----
+  // Lane l holds dims 256*dh + 32*b + 8*j + 4*half + i (value 4*j + i of
+  // block b).
+  if (row_live) {
+    const float c0 = l > 0.0f ? fexp(max_ref(-87.0f, m - m)) : 0.0f;
+    const float gl = l * c0;
+    const bool live = gl > 0.0f;
+    const float inv_l = live ? 1.0f / gl : 0.0f;
+    uint16_t* dst =
+        out + (static_cast<int64_t>(tok) * num_q + head) * kWD + kWHalf * dh + 4 * half;
+#pragma unroll
+    for (int b = 0; b < kWDimBlocks; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float av = (acc[b][4 * j + i] * S) * c0;
+          e[i] = live ? f32_to_bf16_bits(av * inv_l) : 0u;
+        }
+        *reinterpret_cast<uint2*>(dst + 32 * b + 8 * j) =
+            make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int prefill_wide_max_pages() { return kWLdsPages; }
+
+hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const void* q,
+                                    const void* k, const void* v, void* output, int num_q,
+                                    int num_kv, int64_t kv_stride, PagedGeom geom,
+                                    hipStream_t stream) {
+  if (num_qblocks <= 0) return hipSuccess;
+  const int items = num_qblocks * kWSub * num_kv;
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  hipLaunchKernelGGL(prefill_wide_mfma_kernel, dim3(per_xcd * kXcds), dim3(kPThreads), 0,
+                     stream, image, static_cast<const uint16_t*>(q),
+                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                     static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
+                     geom.row_mask, items, per_xcd);
+  return hipGetLastError();
+}
+
+}  // namespace ifr

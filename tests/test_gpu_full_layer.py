@@ -7,8 +7,8 @@ dispatch_bq_full_attention_qkv call the path (modeling/gemma_4_moe.mojo:
 - append (rope_cache_write) bit-exact, and the fused head norm + append with
   V taken from the raw K projection (the full layer's V, gemma_4_moe.mojo:
   441-448), bit-exact;
-- bf16 decode (batched, all merge routes) and the token-partitioned prefill
-  within 1e-2 of the oracle (one bf16 spacing where |x| >= 2);
+- bf16 decode (batched, all merge routes) and a prefill chunk within 1e-2
+  of the oracle (one bf16 spacing where |x| >= 2);
 - bq prep (codes, scales, q bias and f_q) bit-exact with partial RoPE and
   gains, and bq attention outputs bit-exact (integer MFMA scores, the
   reference's softmax and per-element P.V order), with the o_proj block
@@ -148,7 +148,8 @@ def test_full_layer_single_sequence():
 
 
 def test_full_layer_token_prefill():
-    """A prefill chunk takes the token-partitioned route at this shape."""
+    """A short prefill chunk at this shape (the MFMA prefill route;
+    test_gpu_prefill_wide.py covers it in depth)."""
     announce("full layer token prefill")
     case = make_prefill_case(9, [0, 300, 77], [20, 45, 33])
     r = _bf16_attention(case, 98, 16, 80)
