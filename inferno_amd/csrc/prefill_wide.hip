@@ -155,10 +155,12 @@ void prefill_wide_mfma_kernel(
       const int key = min(it * kWKeys + r, count_max - 1);
       const int prow = __builtin_amdgcn_readfirstlane(page_rows[key >> shift]);
       const int64_t off = (static_cast<int64_t>(prow) + (key & row_mask)) * kv_stride;
-      __builtin_amdgcn_global_load_lds(kbase + off + 8 * (lane ^ (r & 15)),
-                                       (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + off + 8 * (lane ^ (2 * (r & 3))),
-                                       (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
+      const uint8_t* krow = reinterpret_cast<const uint8_t*>(kbase + off);  // uniform
+      const uint8_t* vrow = reinterpret_cast<const uint8_t*>(vbase + off);
+      const uint32_t lk = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
+      const uint32_t lv = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+      __builtin_amdgcn_global_load_lds(krow + lk, (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vrow + lv, (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
     }
   };
   auto zero_tail = [&](int it, uint8_t* vdst) {
@@ -368,30 +370,21 @@ void prefill_wide_mfma_kernel(
     fold_pv(vl, w, corr, big);
     iteration_end(it, vnext);
   };
-  // An iteration on the causal diagonal: per-tile masks; a pair whose rows
-  // all end before the iteration skips its work but not the barriers.
+  // An iteration on the causal diagonal: per-tile masks (a pair whose rows
+  // all end before a tile gets corr 1 and zero weights for it).  One call
+  // site with the buffers chosen at run time keeps the register allocation
+  // of the whole kernel within the register file.
   auto masked_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                               uint8_t* vnext) {
     const int key_base = it * kWKeys;
     if (it + 1 < n_iters) stage(it + 1, knext, vnext);
-    const bool work = key_base < pair_count;  // wave-uniform
-    f32x16_t own;
-    if (work) {
-      own = qk(kl);
-    } else {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) own[v] = 0.0f;
-    }
-    const f32x16_t s = exchange(own);
-    if (work) {
-      float w[2][8], corr[2];
-      bool big[2];
-      softmax_pair(s, key_base, true, w, corr, big);
-      fold_pv(vl, w, corr, big);
-    }
+    float w[2][8], corr[2];
+    bool big[2];
+    const f32x16_t s = exchange(qk(kl));
+    softmax_pair(s, key_base, true, w, corr, big);
+    fold_pv(vl, w, corr, big);
     iteration_end(it, vnext);
   };
-
   // Iterations whose keys are valid for every row of the block run the
   // unmasked code, in pairs so that each buffer is a fixed LDS object; the
   // rest (the causal diagonal, and an odd one left over) the masked code.
@@ -403,11 +396,11 @@ void prefill_wide_mfma_kernel(
     full_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
     full_iteration(it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
   }
+#pragma unroll 1
   for (; it < n_iters; ++it) {
-    if (it & 1)
-      masked_iteration(it, kbuf1, vbuf1, kbuf0, vbuf0);
-    else
-      masked_iteration(it, kbuf0, vbuf0, kbuf1, vbuf1);
+    const bool odd = it & 1;
+    masked_iteration(it, odd ? kbuf1 : kbuf0, odd ? vbuf1 : vbuf0, odd ? kbuf0 : kbuf1,
+                     odd ? vbuf0 : vbuf1);
   }
 
   // ---- one-segment merge and bf16 store (PrefillMergeKernel) ----
