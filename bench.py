@@ -952,22 +952,32 @@ class PrefillSliding:
     sequence on its own 64-page ring (4096 positions, enough for the chunk
     and its window), then the sliding prefill over window 1024
     (FlashPrefillSlidingKernel, kernels/flash_attention_prefill.mojo:18-114),
-    on MFMA when the window is a multiple of 16."""
+    on MFMA when the window is a multiple of 16.  --kv bq: the butterquant
+    layer (BqFlashPrefillSlidingKernel, butterquant_kernels/attention.mojo:
+    170-264), the append being bq prep (codes and scales of the chunk into
+    the ring, q codes)."""
 
-    dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
     phases = ("append", "attention")
-    dominant = "prefill_sliding_mfma_kernel"
     dominant_phase = "attention"
     bound = "mfma"
     RING = 64
 
-    def __init__(self, seed: int, window: int):
-        self.seed, self.window = seed, window
+    def __init__(self, seed: int, window: int, kv: str = "bf16"):
+        self.seed, self.window, self.bq = seed, window, kv == "bq"
         self.prefix = uniform_ints(seed, 8, 0, 16384)
         self.new = 2048
+        if self.bq:
+            self.dtype = "int8 KV (f32 scales): int8 MFMA scores, bf16 MFMA P.V, f32 accumulate"
+            self.dominant = "prefill_sliding_mfma_kernel<bq>"
+            kind = ("butterquant int8 KV (f32 scales per position and kv head), bq prep + "
+                    "causal sliding prefill")
+        else:
+            self.dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
+            self.dominant = "prefill_sliding_mfma_kernel"
+            kind = "bf16, append + causal sliding prefill"
         self.name = (f"config11 (widening): sliding-window chunked prefill, 8 sequences x 2048 "
                      f"new tokens on prefixes ~ U[0,16384], window {window}, 64-page rings of "
-                     f"64-token pages, 16q/8kv hd256 bf16, append + causal sliding prefill")
+                     f"64-token pages, 16q/8kv hd256 {kind}")
 
     def setup(self, dev, a):
         import torch
@@ -988,28 +998,50 @@ class PrefillSliding:
         self.table, self.n = table, n
         self.stream = torch.cuda.current_stream()
         sid = int(self.stream.cuda_stream)
-        self.k = torch.empty(rows * KV_STRIDE, dtype=torch.int16, device=dev)
+        cdt = torch.int8 if self.bq else torch.int16
+        self.k = torch.empty(rows * KV_STRIDE, dtype=cdt, device=dev)
         self.v = torch.empty_like(self.k)
         self.q = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
         self.ks = torch.empty(n * KV_STRIDE, dtype=torch.int16, device=dev)
         self.vs = torch.empty_like(self.ks)
         for i, t in enumerate((self.k, self.v, self.q, self.ks, self.vs)):
             _fill(t, self.seed * 16 + i, sid)
+        if self.bq:
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(self.seed)
+            self.ksc = torch.rand(rows * NUM_KV, device=dev, generator=gen) * 4 + 0.5
+            self.vsc = torch.rand(rows * NUM_KV, device=dev, generator=gen) * 4 + 0.5
+            self.gain = torch.full((HEAD_DIM,), 0x3F80, dtype=torch.int16, device=dev)
+            self.q_i8 = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int8, device=dev)
+            self.qb = torch.empty(n * NUM_Q, dtype=torch.float32, device=dev)
+            self.fq = torch.empty_like(self.qb)
         cos, sin = rope_tables(max(self.prefix) + self.new + 1)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.plan = AttentionPlan(table, n, kind=0, window=self.window,
                                   cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN,
-                                  cache_rows=rows, cap=a.cap, kv_row_bytes=KV_STRIDE * 2,
-                                  device=dev)
+                                  cache_rows=rows, cap=a.cap,
+                                  kv_row_bytes=KV_STRIDE * (1 if self.bq else 2), device=dev)
         self.partials, self.ps = A.partials_buffer(self.plan, NUM_Q, HEAD_DIM)
         self.out = torch.empty(n * NUM_Q * HEAD_DIM, dtype=torch.int16, device=dev)
         self.cap = a.cap
         if int(self.plan.info[14]) == 0:
-            self.dominant = "flash_partial_bf16_kernel (token route) + merge_kernel"
+            self.dominant = ("bq_partial_kernel (token route) + merge_kernel" if self.bq else
+                             "flash_partial_bf16_kernel (token route) + merge_kernel")
 
     def launch(self, phase):
         A, p = self.A, self.plan
-        if phase == "append":
+        if self.bq and phase == "append":
+            A.dispatch_bq_attn_prep(p, self.q, self.ks, self.vs, self.gain, self.gain,
+                                    self.q_i8, self.qb, self.fq, self.k, self.ksc, self.v,
+                                    self.vsc, self.cos, self.sin, num_q=NUM_Q, num_kv=NUM_KV,
+                                    head_dim=HEAD_DIM, rope_half=128, pair_stride=128,
+                                    sqrt_n=float(np.sqrt(np.float32(HEAD_DIM))),
+                                    n_eps=float(np.float32(HEAD_DIM) * np.float32(1e-6)))
+        elif self.bq:
+            A.bq_attention(p, self.q_i8, self.qb, self.fq, self.k, self.ksc, self.v, self.vsc,
+                           self.out, self.partials, self.ps, num_q=NUM_Q, num_kv=NUM_KV,
+                           head_dim=HEAD_DIM, kv_stride=KV_STRIDE)
+        elif phase == "append":
             A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
                                         self.sin, num_q=NUM_Q, num_kv=NUM_KV, half=128,
                                         pair_stride=128, head_dim=HEAD_DIM)
@@ -1025,6 +1057,8 @@ class PrefillSliding:
         return 4 * HEAD_DIM * NUM_Q * keys
 
     def step_bytes(self) -> int:
+        if self.bq:  # bf16 q/k/v in, codes out; bf16 output
+            return self.n * ((NUM_Q + 2 * NUM_KV) * HEAD_DIM * 3 + NUM_Q * HEAD_DIM * 2)
         return self.n * (KV_STRIDE * 2 * 2 * 2 + NUM_Q * HEAD_DIM * 2 * 3)
 
     def dominant_bytes(self) -> int:
@@ -1049,6 +1083,8 @@ class PrefillSliding:
         p0 = self.prefix[0]
         pages = np.asarray(self.table.base_rows[:self.RING], dtype=np.int64) // PAGE_LEN
         idx = torch.from_numpy(pages).to(self.k.device)
+        if self.bq:
+            return self._cpu_baseline_bq(budget_s, hc, p0, idx)
         kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
         vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
         kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
@@ -1076,6 +1112,47 @@ class PrefillSliding:
                                                       "affinity_cpus")},
                 "sample": (f"last {n_s} query tokens of the first sequence ({keys} query-key "
                            f"pairs), the reference's sliding token route at cap={threads} "
+                           f"workers, median of {len(times)}")}
+
+    def _cpu_baseline_bq(self, budget_s, hc, p0, idx):
+        """The oracle's bq sliding token route (BqFlashPrefillSlidingKernel) on
+        the last 16 query tokens of the first sequence."""
+        import oracle
+
+        threads = hc["threads"]
+
+        def pages_of(t, per_row):
+            return np.ascontiguousarray(
+                t.view(-1, PAGE_LEN * per_row).index_select(0, idx).cpu().numpy()).reshape(-1)
+
+        kp, vp = pages_of(self.k, KV_STRIDE), pages_of(self.v, KV_STRIDE)
+        ksp, vsp = pages_of(self.ksc, NUM_KV), pages_of(self.vsc, NUM_KV)
+        n_s = 16
+        first = self.new - n_s
+        runs = np.asarray([[0, p0 + first, 0, self.RING]], dtype=np.int32)
+        base = np.arange(self.RING, dtype=np.int32) * PAGE_LEN
+        qh = np.ascontiguousarray(
+            self.q_i8.view(-1, NUM_Q * HEAD_DIM)[first:self.new].cpu().numpy()).reshape(-1)
+        qb = np.ascontiguousarray(self.qb.view(-1, NUM_Q)[first:self.new].cpu().numpy())
+        fq = np.ascontiguousarray(self.fq.view(-1, NUM_Q)[first:self.new].cpu().numpy())
+        keys = sum(min(p0 + first + t + 1, self.window) for t in range(n_s))
+        fl = 4 * HEAD_DIM * NUM_Q * keys
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.bq_attention(0, runs, base, qh, qb.reshape(-1), fq.reshape(-1), kp, ksp, vp,
+                                vsp, num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
+                                kv_stride=KV_STRIDE, window=self.window,
+                                cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN,
+                                seq_len=n_s, cap=threads, threads=threads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
+                "sample": (f"last {n_s} query tokens of the first sequence ({keys} query-key "
+                           f"pairs), the reference's bq sliding token route at cap={threads} "
                            f"workers, median of {len(times)}")}
 
 
@@ -1295,7 +1372,7 @@ def main() -> None:
                     help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
                          "own pass or fused into the append kernel")
     ap.add_argument("--kv", choices=("bf16", "bq"), default="bf16",
-                    help="config 6: bf16 or butterquant int8 KV for the sparse attention")
+                    help="configs 6 and 11: bf16 or butterquant int8 KV")
     ap.add_argument("--oproj", action="store_true",
                     help="configs 1-3: the bf16 o_proj GEMM after the merge")
     ap.add_argument("--oquant", choices=("none", "separate", "fused"), default="none",
@@ -1330,7 +1407,7 @@ def main() -> None:
     elif a.config == 10:
         w = GatherBench(a.seed)
     elif a.config == 11:
-        w = PrefillSliding(a.seed, a.window)
+        w = PrefillSliding(a.seed, a.window, a.kv)
     else:
         w = DecodeBf16(a.config, a.seed)
     w.setup(dev, a)
@@ -1381,7 +1458,7 @@ def main() -> None:
         res["pct_mfma_peak"] = round(100 * value_override / MFMA_BF16_PEAK_TFLOPS, 2)
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 "traffic.json")
-    key = f"config{a.config}_cap{a.cap}"
+    key = f"config{a.config}_cap{a.cap}" + ("_bq" if a.kv == "bq" and a.config in (6, 11) else "")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
             measured = json.load(f).get(key)

@@ -1071,6 +1071,23 @@ int32_t bq_attention(const void* image_dev, const int64_t* info, const void* q_i
     return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
   ifr::PagedGeom g{static_cast<int>(pow2_shift(page_len)), static_cast<int>(page_len - 1),
                    static_cast<int>(page_mask)};
+  if (info[2] == IFR_PLAN_TOKEN_DIRECT && info[14] > 0 && head_dim == 256 &&
+      num_q == 2 * num_kv && page_mask >= 0) {
+    // Prefill chunk of a sliding-window layer: MFMA query blocks; the o_proj
+    // block quant, if asked for, as its own pass over the finished rows.
+    IFR_HIP(ifr::launch_prefill_sliding_mfma_bq(
+                static_cast<const int32_t*>(image_dev), static_cast<int>(info[14]), q_i8,
+                qi_bias, f_q, k_base, k_scale, v_base, v_scale, output,
+                static_cast<int>(num_q), static_cast<int>(num_kv), kv_stride, g,
+                static_cast<int>(info[12]), as_stream(stream)),
+            "prefill_sliding_mfma_bq");
+    if (o_i8)
+      IFR_HIP(ifr::launch_bq_block_quant(output, o_i8, o_sa, num_q * head_dim,
+                                         static_cast<int>(head_dim), info[5],
+                                         as_stream(stream)),
+              "bq_block_quant");
+    return ok();
+  }
   IFR_HIP(ifr::launch_bq_attention(static_cast<const int32_t*>(image_dev),
                                    static_cast<int>(info[0]), static_cast<int>(info[1]),
                                    static_cast<int>(info[2]), q_i8, qi_bias, f_q, k_base,

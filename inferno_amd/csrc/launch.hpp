@@ -63,6 +63,14 @@ hipError_t launch_prefill_sliding_mfma(const int32_t* image_dev, int num_qblocks
                                        const void* q, const void* k_base, const void* v_base,
                                        void* output, int num_q, int num_kv, int64_t kv_stride,
                                        PagedGeom geom, int window, hipStream_t stream);
+// The same over butterquant int8 KV (f32 scales per row and kv head).
+hipError_t launch_prefill_sliding_mfma_bq(const int32_t* image_dev, int num_qblocks,
+                                          const void* q_i8, const float* qi_bias,
+                                          const float* f_q, const void* k_base,
+                                          const float* k_scale, const void* v_base,
+                                          const float* v_scale, void* output, int num_q,
+                                          int num_kv, int64_t kv_stride, PagedGeom geom,
+                                          int window, hipStream_t stream);
 
 hipError_t launch_bq_attention(const int32_t* image_dev, int num_items,
                                int num_units, int mode, const void* q_i8,

@@ -32,6 +32,18 @@
 // bf16 hi parts plus, for tiles that hold a large share of some row's l, the
 // lo parts (the full kernel's gate), and the biased exp is the fused-FMA form
 // (about 2e-5 relative from the reference's separately rounded steps).
+//
+// kBq: the butterquant variant (BqFlashPrefillSlidingKernel, butterquant_
+// kernels/attention.mojo:170-264; bq_process_kv_tile :27-102).  K codes are
+// staged straight into LDS (256-byte rows, the same XOR swizzle) and the
+// scores come from v_mfma_i32_32x32x32_i8: sum k*q is exact, plus 128 *
+// sum q it is the reference's VNNI raw dot, and each score is then formed in
+// the reference's order, ((raw - qi_bias) * f_q) * k_scale / 127^2, so the
+// scores equal the oracle's bit for bit.  V codes pass through registers on
+// their way to LDS, converted to bf16 (exact for int8), so P.V is the bf16
+// path above; a weight enters it as (w * v_scale) / 127.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "prefill_common.hpp"
@@ -41,17 +53,29 @@ namespace {
 
 using namespace prefill;
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+
+// Bytes of one head's row of int8 codes.
+constexpr int kBqRowBytes = kPD;
+
+template <bool kBq>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_sliding_mfma_kernel(
-    const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
-    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int32_t* __restrict__ image, const void* __restrict__ qp,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const void* __restrict__ kcp, const float* __restrict__ k_scale,
+    const void* __restrict__ vcp, const float* __restrict__ v_scale,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride, int shift,
     int row_mask, int page_mask, int window) {
-  __shared__ __align__(16) uint8_t kbuf0[kTileBytes];
-  __shared__ __align__(16) uint8_t kbuf1[kTileBytes];
+  __shared__ __align__(16) uint8_t kbuf0[kBq ? kKeys * kBqRowBytes : kTileBytes];
+  __shared__ __align__(16) uint8_t kbuf1[kBq ? kKeys * kBqRowBytes : kTileBytes];
   __shared__ __align__(16) uint8_t vbuf0[kTileBytes];
   __shared__ __align__(16) uint8_t vbuf1[kTileBytes];
   __shared__ int32_t page_rows[kPrefillLdsPages];
+  // bq: K and V scales of the staged keys, per buffer.
+  __shared__ __align__(16) float kscl[2][kBq ? kKeys : 1];
+  __shared__ __align__(16) float vscl[2][kBq ? kKeys : 1];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -90,18 +114,44 @@ void prefill_sliding_mfma_kernel(
   const int t_first = row_live ? (lo >> 4) : (1 << 30);
   const int t_end = row_live ? (p >> 4) + (r == 0 ? 1 : 0) : -1;
 
-  bf16x8_t qf[kPD / 16];
-  {
-    const uint16_t* qr =
-        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * half;
+  // Q^T fragments.  bf16: lane holds Q[row][16*d + 8*half .. +7]; bq: the
+  // codes Q[row][32*d + 16*half .. +15], with the row's 128 * sum q, bias
+  // and f_q.
+  constexpr int kQFrags = kBq ? kPD / 32 : kPD / 16;
+  using QFrag = typename std::conditional<kBq, i32x4_t, bf16x8_t>::type;
+  QFrag qf[kQFrags];
+  int qs128 = 0;
+  float qb_row = 0.0f, fq_row = 0.0f;
+  const int64_t q_off = (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD;
+  if constexpr (kBq) {
+    const int8_t* qr = static_cast<const int8_t*>(qp) + q_off + 16 * half;
+    int qs = 0;
 #pragma unroll
-    for (int d = 0; d < kPD / 16; ++d) {
+    for (int d = 0; d < kQFrags; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * d);
+      qf[d] = __builtin_bit_cast(i32x4_t, v);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.x), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, qs, false);
+    }
+    // The row's other 128 codes are in lane ^ 32.
+    const auto sw = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(qs),
+                                                    static_cast<uint32_t>(qs), false, false);
+    qs128 = 128 * (static_cast<int>(sw[0]) + static_cast<int>(sw[1]));
+    const int64_t qh = static_cast<int64_t>(row_live ? tok : t0) * num_q + head;
+    qb_row = qi_bias[qh];
+    fq_row = f_q[qh];
+  } else {
+    const uint16_t* qr = static_cast<const uint16_t*>(qp) + q_off + 8 * half;
+#pragma unroll
+    for (int d = 0; d < kQFrags; ++d) {
       const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
       qf[d] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
 #pragma unroll
-  for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
+  for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
 
   f32x16_t acc[kDimBlocks];
 #pragma unroll
@@ -118,39 +168,98 @@ void prefill_sliding_mfma_kernel(
 
   // Staging of one iteration (as the full kernel's): keys clamped into
   // [k_lo, p_last]; V rows of keys outside it are zeroed after landing.
-  const uint16_t* kbase = kc + static_cast<int64_t>(g) * kPD;
-  const uint16_t* vbase = vc + static_cast<int64_t>(g) * kPD;
+  const uint16_t* kbase = static_cast<const uint16_t*>(kcp) + static_cast<int64_t>(g) * kPD;
+  const uint16_t* vbase = static_cast<const uint16_t*>(vcp) + static_cast<int64_t>(g) * kPD;
+  const int8_t* kbase8 = static_cast<const int8_t*>(kcp) + static_cast<int64_t>(g) * kPD;
+  const int8_t* vbase8 = static_cast<const int8_t*>(vcp) + static_cast<int64_t>(g) * kPD;
   const int stage_row0 = wave * kStageRows + half;
-  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+  auto slot_of = [&](int key) -> int64_t {
+    return static_cast<int64_t>(page_rows[(key >> shift) & page_mask]) + (key & row_mask);
+  };
+  // bq: V codes of the wave's kStageRows rows, 4 rows per 64 lanes (lane p:
+  // row p / 16, 16 codes from 16 * (p % 16)), held until converted.
+  uint4 vcodes[kBq ? kStageRows / 4 : 1];
+  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst, int buf) {
+    if constexpr (kBq) {
 #pragma unroll
-    for (int i = 0; i < kStageRows / 2; ++i) {
-      const int rr = stage_row0 + 2 * i;
-      const int key = min(max(kb0 + it * kKeys + rr, k_lo), p_last);
-      const int64_t slot =
-          static_cast<int64_t>(page_rows[(key >> shift) & page_mask]) + (key & row_mask);
-      const int64_t off = slot * kv_stride;
-      const int lds_row = wave * kStageRows + 2 * i;
-      __builtin_amdgcn_global_load_lds(kbase + off + 8 * (row ^ (rr & 15)),
-                                       (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + off + 8 * (row ^ (2 * (rr & 3))),
-                                       (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+      for (int i = 0; i < kStageRows / 4; ++i) {
+        const int rr = wave * kStageRows + 4 * i + (lane >> 4);
+        const int key = min(max(kb0 + it * kKeys + rr, k_lo), p_last);
+        const int64_t off = slot_of(key) * kv_stride;
+        const int c = lane & 15;
+        __builtin_amdgcn_global_load_lds(
+            kbase8 + off + 16 * (c ^ (rr & 15)),
+            (lds_void_t*)(kdst + (wave * kStageRows + 4 * i) * kBqRowBytes), 16, 0, 0);
+        vcodes[i] = *reinterpret_cast<const uint4*>(vbase8 + off + 16 * c);
+      }
+      if (wave == 0) {
+        // The staged keys' scales, lane p: key p of the iteration.
+        const int key = min(max(kb0 + it * kKeys + lane, k_lo), p_last);
+        const int64_t si = slot_of(key) * num_kv + g;
+        __builtin_amdgcn_global_load_lds(k_scale + si, (lds_void_t*)(&kscl[buf][0]), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(v_scale + si, (lds_void_t*)(&vscl[buf][0]), 4, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kStageRows / 2; ++i) {
+        const int rr = stage_row0 + 2 * i;
+        const int key = min(max(kb0 + it * kKeys + rr, k_lo), p_last);
+        const int64_t off = slot_of(key) * kv_stride;
+        const int lds_row = wave * kStageRows + 2 * i;
+        __builtin_amdgcn_global_load_lds(kbase + off + 8 * (row ^ (rr & 15)),
+                                         (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vbase + off + 8 * (row ^ (2 * (rr & 3))),
+                                         (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+      }
     }
   };
-  auto zero_outside = [&](int it, uint8_t* vdst) {
+  // After the wave's loads have landed: bf16 keeps the staged V rows and
+  // zeroes those outside [k_lo, p_last]; bq writes its V codes as bf16 (the
+  // bf16 swizzle: 16-byte chunk c of row rr at c ^ 2*(rr & 3)), zeros for
+  // keys outside the range.
+  auto land_v = [&](int it, uint8_t* vdst) {
     const int first = kb0 + it * kKeys;
-    if (first >= k_lo && first + kKeys <= p_last + 1) return;  // block-uniform
+    if constexpr (kBq) {
 #pragma unroll
-    for (int i = 0; i < kStageRows / 2; ++i) {
-      const int rr = stage_row0 + 2 * i;
-      const int key = first + rr;
-      if (key < k_lo || key > p_last)
-        *reinterpret_cast<uint4*>(vdst + rr * kRowBytes + 16 * row) = make_uint4(0u, 0u, 0u, 0u);
+      for (int i = 0; i < kStageRows / 4; ++i) {
+        const int rr = wave * kStageRows + 4 * i + (lane >> 4);
+        const int key = first + rr;
+        const bool in = key >= k_lo && key <= p_last;
+        const uint32_t w[4] = {vcodes[i].x, vcodes[i].y, vcodes[i].z, vcodes[i].w};
+        uint32_t bf[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int b = 0; b < 4; b += 2) {
+            const float f0 = static_cast<float>(static_cast<int8_t>(w[j] >> (8 * b)));
+            const float f1 = static_cast<float>(static_cast<int8_t>(w[j] >> (8 * b + 8)));
+            bf[2 * j + b / 2] = in ? ((__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u))
+                                   : 0u;
+          }
+        }
+        const int c0 = 2 * (lane & 15);
+        uint8_t* vr = vdst + rr * kRowBytes;
+        *reinterpret_cast<uint4*>(vr + 16 * (c0 ^ (2 * (rr & 3)))) =
+            make_uint4(bf[0], bf[1], bf[2], bf[3]);
+        *reinterpret_cast<uint4*>(vr + 16 * ((c0 + 1) ^ (2 * (rr & 3)))) =
+            make_uint4(bf[4], bf[5], bf[6], bf[7]);
+      }
+    } else {
+      if (first >= k_lo && first + kKeys <= p_last + 1) return;  // block-uniform
+#pragma unroll
+      for (int i = 0; i < kStageRows / 2; ++i) {
+        const int rr = stage_row0 + 2 * i;
+        const int key = first + rr;
+        if (key < k_lo || key > p_last)
+          *reinterpret_cast<uint4*>(vdst + rr * kRowBytes + 16 * row) =
+              make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
 
-  if (n_iters > 0) stage(0, kbuf0, vbuf0);
+  if (n_iters > 0) stage(0, kbuf0, vbuf0, 0);
   __builtin_amdgcn_s_waitcnt(0);
-  if (n_iters > 0) zero_outside(0, vbuf0);
+  if (n_iters > 0) land_v(0, vbuf0);
   __syncthreads();
 
   const int k_lane = row * kRowBytes + 16 * ((row & 15) ^ half);
@@ -160,8 +269,46 @@ void prefill_sliding_mfma_kernel(
   const int v_even = v_row + 64 * (vj >> 3);
   const int v_odd = v_row - 64 * (vj >> 3);
 
+  // bq K operand reads: chunk 2d + half of key row (row & 31) of 256 bytes,
+  // stored at (2d + half) ^ (row & 15): byte address kq_lane ^ 32d.
+  const int kq_lane = row * kBqRowBytes + 16 * ((row & 15) ^ half);
+  constexpr float kInv127 = 1.0f / 127.0f;
+  constexpr float kInv127Sq = kInv127 * kInv127;
+
   constexpr int kKAhead = 6;
-  auto qk = [&](const uint8_t* kl, int h) {
+  // Scores of 32-key block h of the staged iteration (buffer buf).
+  auto qk = [&](const uint8_t* kl, int h, int buf) {
+    if constexpr (kBq) {
+      i32x16_t si;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) si[v] = 0;
+      const uint8_t* kh = kl + 32 * h * kBqRowBytes;
+      uint4 kf[kQFrags];
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d)
+        kf[d] = *reinterpret_cast<const uint4*>(kh + (kq_lane ^ (32 * d)));
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d)
+        si = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, kf[d]), qf[d],
+                                                   si, 0, 0, 0);
+      // ((raw - qi_bias) * f_q) * k_scale / 127^2 per (row, key); value
+      // 4j + i holds key 8j + 4*half + i of the block.
+      f32x16_t sblk;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 ks4 =
+            *reinterpret_cast<const float4*>(&kscl[buf][32 * h + 8 * j + 4 * half]);
+        const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float sc = static_cast<float>(si[4 * j + i] + qs128) - qb_row;
+          sc = sc * fq_row;
+          sc = sc * ks[i];
+          sblk[4 * j + i] = sc * kInv127Sq;
+        }
+      }
+      return sblk;
+    } else {
     f32x16_t sblk;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
@@ -185,6 +332,7 @@ void prefill_sliding_mfma_kernel(
     }
     __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
     return sblk;
+    }
   };
 
   // acc_stored += V^T P^T for the 16-key tile at rows tile_row .. +15 of vl:
@@ -193,7 +341,23 @@ void prefill_sliding_mfma_kernel(
   // reference tile with weights in this tile (the full kernel's gate: the
   // lo parts of a smaller share move that row's output by at most
   // 2^-9 * kLoShare * max|v|).
-  auto pv = [&](const uint8_t* vl, int tile_row, const float (&pw)[8], bool need_lo) {
+  auto pv = [&](const uint8_t* vl, int tile_row, const float (&pw0)[8], bool need_lo,
+                int buf) {
+    float pw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pw[i] = pw0[i];
+    if constexpr (kBq) {
+      // Lane value i is key tile_row + 8*(i/4) + 4*half + i%4.
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float4 vs4 =
+            *reinterpret_cast<const float4*>(&vscl[buf][tile_row + 8 * j + 4 * half]);
+        pw[4 * j] = (pw[4 * j] * vs4.x) * kInv127;
+        pw[4 * j + 1] = (pw[4 * j + 1] * vs4.y) * kInv127;
+        pw[4 * j + 2] = (pw[4 * j + 2] * vs4.z) * kInv127;
+        pw[4 * j + 3] = (pw[4 * j + 3] * vs4.w) * kInv127;
+      }
+    }
     bf16x8_t phi;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
@@ -238,7 +402,7 @@ void prefill_sliding_mfma_kernel(
   // tile (high part of t - 1, low part of t) when t_first < t <= t_end, then
   // P.V of tile t - 1 (vprev, rows prev_row ..) unless do_pv is false.
   auto step = [&](int t, const float (&st)[8], const uint8_t* vprev, int prev_row,
-                  bool do_pv) {
+                  bool do_pv, int prev_buf) {
     const bool fin = t > t_first && t <= t_end;
     float sel[8];
     bool low[8];
@@ -295,7 +459,7 @@ void prefill_sliding_mfma_kernel(
     }
     const bool need_lo = pend_big || big;
     pend_big = big && r != 0;
-    if (do_pv) pv(vprev, prev_row, pw, need_lo);
+    if (do_pv) pv(vprev, prev_row, pw, need_lo, prev_buf);
   };
 
   for (int it = 0; it < n_iters; ++it) {
@@ -303,32 +467,33 @@ void prefill_sliding_mfma_kernel(
     uint8_t* vl = (it & 1) ? vbuf1 : vbuf0;
     uint8_t* kn = (it & 1) ? kbuf0 : kbuf1;
     uint8_t* vn = (it & 1) ? vbuf0 : vbuf1;
+    const int cb = it & 1, nb = cb ^ 1;
     const int tb = tile0 + 4 * it;
     float st[8];
-    const f32x16_t s0 = qk(kl, 0);
+    const f32x16_t s0 = qk(kl, 0, cb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s0[i];
     // Tile tb - 1 lies in the other buffer (the previous iteration's last
     // tile); it is read before that buffer is restaged.
-    step(tb, st, vn, 48, it > 0);
+    step(tb, st, vn, 48, it > 0, nb);
     __syncthreads();
-    if (it + 1 < n_iters) stage(it + 1, kn, vn);
+    if (it + 1 < n_iters) stage(it + 1, kn, vn, nb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s0[8 + i];
-    step(tb + 1, st, vl, 0, true);
-    const f32x16_t s1 = qk(kl, 1);
+    step(tb + 1, st, vl, 0, true, cb);
+    const f32x16_t s1 = qk(kl, 1, cb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s1[i];
-    step(tb + 2, st, vl, 16, true);
+    step(tb + 2, st, vl, 16, true, cb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s1[8 + i];
-    step(tb + 3, st, vl, 32, true);
+    step(tb + 3, st, vl, 32, true, cb);
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
 #pragma unroll
-    for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
+    for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
     __builtin_amdgcn_s_waitcnt(0);
-    if (it + 1 < n_iters) zero_outside(it + 1, vn);
+    if (it + 1 < n_iters) land_v(it + 1, vn);
     __syncthreads();
   }
   // The step past the last staged tile: completes the last reference tile of
@@ -337,7 +502,8 @@ void prefill_sliding_mfma_kernel(
     float st[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = kNegBig;
-    step(tile0 + 4 * n_iters, st, ((n_iters - 1) & 1) ? vbuf1 : vbuf0, 48, true);
+    const int lb = (n_iters - 1) & 1;
+    step(tile0 + 4 * n_iters, st, lb ? vbuf1 : vbuf0, 48, true, lb);
   }
 
   // Finalisation of the sliding prefill: acc * (1/l).
@@ -369,11 +535,25 @@ hipError_t launch_prefill_sliding_mfma(const int32_t* image, int num_qblocks, co
                                        int num_kv, int64_t kv_stride, PagedGeom geom,
                                        int window, hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(prefill_sliding_mfma_kernel, dim3(num_qblocks * num_kv), dim3(kPThreads),
-                     0, stream, image, static_cast<const uint16_t*>(q),
-                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                     static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
-                     geom.row_mask, geom.page_mask, window);
+  hipLaunchKernelGGL(prefill_sliding_mfma_kernel<false>, dim3(num_qblocks * num_kv),
+                     dim3(kPThreads), 0, stream, image, q, nullptr, nullptr, k, nullptr, v,
+                     nullptr, static_cast<uint16_t*>(output), num_q, num_kv, kv_stride,
+                     geom.shift, geom.row_mask, geom.page_mask, window);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_sliding_mfma_bq(const int32_t* image, int num_qblocks,
+                                          const void* q_i8, const float* qi_bias,
+                                          const float* f_q, const void* k,
+                                          const float* k_scale, const void* v,
+                                          const float* v_scale, void* output, int num_q,
+                                          int num_kv, int64_t kv_stride, PagedGeom geom,
+                                          int window, hipStream_t stream) {
+  if (num_qblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(prefill_sliding_mfma_kernel<true>, dim3(num_qblocks * num_kv),
+                     dim3(kPThreads), 0, stream, image, q_i8, qi_bias, f_q, k, k_scale, v,
+                     v_scale, static_cast<uint16_t*>(output), num_q, num_kv, kv_stride,
+                     geom.shift, geom.row_mask, geom.page_mask, window);
   return hipGetLastError();
 }
 

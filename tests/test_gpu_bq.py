@@ -106,7 +106,10 @@ def _prep_and_attend(state, runs, rows, q, k, v, norm_q, norm_k, cos, sin, *, ki
 def test_reference_parity_schedule():
     """tests/test_sliding_attention_degree_parity.mojo at degree 1 on the GPU:
     the 10-step prefill/decode schedule over 2-page rings (cap 4 exercises
-    the token, batched-split and single-token routes)."""
+    the token, batched-split and single-token routes).  Decode steps are
+    bit-exact; prefill chunks take the MFMA sliding prefill (query blocks in
+    the plan) and are held to 1e-2 of the oracle (one bf16 spacing where
+    |x| >= 2) and the reference harness's 0.05."""
     cos, sin, norm = bq.constant_tables()
     state = BqState(bq.CACHE_ROWS)
     worst_ref, worst_or = 0.0, 0.0
@@ -120,7 +123,8 @@ def test_reference_parity_schedule():
             pair_stride=bq.PAIR_STRIDE)
         r = compare_bf16(got, ref)
         assert r["n_fail"] == 0 and r["n_nan"] == 0, (step, r)
-        assert np.array_equal(got, ref), (step, r)  # bit-exact, as in the batched test
+        if not (plan.summary.mode == 1 and int(plan.info[14]) > 0):
+            assert np.array_equal(got, ref), (step, r)  # bit-exact off the MFMA route
         worst_or = max(worst_or, r["max_abs"])
         worst_ref = max(worst_ref, bq.check_step(tok_seq, tok_pos, spec, q_i8, fq, state.k,
                                                  state.ks, state.v, state.vs, got))

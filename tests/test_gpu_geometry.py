@@ -92,7 +92,7 @@ def test_page1024_sliding_ring_decode(layer):
 
 
 def test_page1024_sliding_prefill():
-    """A sliding prefill chunk over 2-page rings (token-partitioned route)."""
+    """A sliding prefill chunk over 2-page rings (the MFMA sliding prefill)."""
     announce("page 1024 sliding prefill")
     runs, rows, cache_rows = _ring_case(4, [0, 1500, 6000], new=40)
     _attend(SLIDING, runs, rows, cache_rows, 120, SHAPES["sliding"], 16, 80)
