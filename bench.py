@@ -762,15 +762,19 @@ class PrefillBf16:
     cache write), then causal full-attention prefill over the paged prefix +
     chunk (MFMA).  Config 12 (widening): the same at Gemma-4's full-attention
     layer shape (16 q / 2 kv heads x 512, partial RoPE over 64 pairs at
-    pair_stride 256; modeling/gemma4_common.mojo:14-20)."""
+    pair_stride 256; modeling/gemma4_common.mojo:14-20).  --kv bq: butterquant
+    int8 KV (BqFlashPrefillFullKernel, butterquant_kernels/attention.mojo:
+    267-351), the append being bq prep and the copy-on-write moving codes
+    and scales."""
 
-    dtype = "bf16 (MFMA bf16 in, f32 accumulate)"
     phases = ("cow", "append", "attention")
     dominant_phase = "attention"
     bound = "mfma"
 
-    def __init__(self, seed: int, config: int = 4):
-        self.seed = seed
+    def __init__(self, seed: int, config: int = 4, kv: str = "bf16"):
+        self.seed, self.cfg, self.bq = seed, config, kv == "bq"
+        self.dtype = ("int8 KV (f32 scales): int8 MFMA scores, bf16 MFMA P.V, f32 accumulate"
+                      if self.bq else "bf16 (MFMA bf16 in, f32 accumulate)")
         shared = uniform_ints(seed, 4, 0, 16384)
         self.prefix = [p for p in shared for _ in range(2)]
         self.new = 2048
@@ -788,6 +792,9 @@ class PrefillBf16:
                      "~ U[0,16384] shared by sequence pairs (sealed pages shared, the partial "
                      "page copied on write), 16q/8kv hd256 bf16")
         self.kvs = self.nkv * self.hd
+        if self.bq:
+            self.dominant += "<bq>"
+            label = label.replace(" bf16", " butterquant int8 KV (f32 scales)")
         self.name = label + (", 64-token pages, COW copy + append + causal MFMA prefill "
                              "over the paged prefix and chunk")
 
@@ -832,9 +839,21 @@ class PrefillBf16:
         sid = int(self.stream.cuda_stream)
         # K and V share one arena, as the reference's KV mirror lays the
         # components out, so the copy jobs address both with byte offsets.
-        self.arena = torch.empty(2 * rows * self.kvs, dtype=torch.int16, device=dev)
+        cdt = torch.int8 if self.bq else torch.int16
+        self.arena = torch.empty(2 * rows * self.kvs, dtype=cdt, device=dev)
         self.k = self.arena[:rows * self.kvs]
         self.v = self.arena[rows * self.kvs:]
+        if self.bq:
+            # Scales [row][kv head] of K then V, one arena for their COW copies.
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(self.seed)
+            self.sarena = torch.rand(2 * rows * self.nkv, device=dev, generator=gen) * 4 + 0.5
+            self.ksc = self.sarena[:rows * self.nkv]
+            self.vsc = self.sarena[rows * self.nkv:]
+            self.gain = torch.full((self.hd,), 0x3F80, dtype=torch.int16, device=dev)
+            self.q_i8 = torch.empty(n * self.nq * self.hd, dtype=torch.int8, device=dev)
+            self.qb = torch.empty(n * self.nq, dtype=torch.float32, device=dev)
+            self.fq = torch.empty_like(self.qb)
         self.q = torch.empty(n * self.nq * self.hd, dtype=torch.int16, device=dev)
         self.ks = torch.empty(n * self.kvs, dtype=torch.int16, device=dev)
         self.vs = torch.empty_like(self.ks)
@@ -843,9 +862,9 @@ class PrefillBf16:
         # COW jobs: rows [0, p % 64) of the first's partial prefix page into the
         # second's own page at the same ordinal, for K and V
         # (append_prefix_copy_jobs, modeling/kv_policy.mojo:59-78).
-        row_bytes = self.kvs * 2
+        row_bytes = self.kvs * (1 if self.bq else 2)
         v_base = rows * row_bytes
-        jobs = []
+        jobs, sjobs = [], []
         for i in range(1, n_seq, 2):
             p = self.prefix[i]
             if p % PAGE_LEN == 0:
@@ -855,13 +874,20 @@ class PrefillBf16:
             nb = (p % PAGE_LEN) * row_bytes
             for base in (0, v_base):
                 jobs.append([base + src * row_bytes, base + dst * row_bytes, nb])
-        self.jobs = np.asarray(jobs, dtype=np.int64).reshape(-1, 3)
-        self.cow = CopyStager(self.jobs, dev) if len(jobs) else None
+            if self.bq:
+                sb = self.nkv * 4
+                for base in (0, rows * sb):
+                    sjobs.append([base + src * sb, base + dst * sb, (p % PAGE_LEN) * sb])
+        self.jobs = np.asarray(jobs + sjobs, dtype=np.int64).reshape(-1, 3)
+        self.cow = CopyStager(np.asarray(jobs, dtype=np.int64).reshape(-1, 3), dev) \
+            if len(jobs) else None
+        self.scow = CopyStager(np.asarray(sjobs, dtype=np.int64).reshape(-1, 3), dev) \
+            if len(sjobs) else None
         cos, sin = rope_tables(max(self.prefix) + self.new + 1, self.half)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.plan = AttentionPlan(table, n, kind=1, window=0, cache_size=PAGE_LEN,
                                   page_len=PAGE_LEN, cache_rows=rows, cap=a.cap,
-                                  kv_row_bytes=self.kvs * 2, device=dev)
+                                  kv_row_bytes=self.kvs * (1 if self.bq else 2), device=dev)
         self.partials, self.ps = A.partials_buffer(self.plan, self.nq, self.hd)
         self.out = torch.empty(n * self.nq * self.hd, dtype=torch.int16, device=dev)
         self.cap = a.cap
@@ -871,6 +897,22 @@ class PrefillBf16:
         if phase == "cow":
             if self.cow is not None:
                 self.cow(self.arena, self.stream)
+            if self.bq and self.scow is not None:
+                self.scow(self.sarena, self.stream)
+        elif self.bq and phase == "append":
+            # The full layer's V is its raw K projection (gemma_4_moe_bq.mojo:566-573).
+            vsrc = self.ks if self.cfg == 12 else self.vs
+            A.dispatch_bq_attn_prep(p, self.q, self.ks, vsrc, self.gain, self.gain, self.q_i8,
+                                    self.qb, self.fq, self.k, self.ksc, self.v, self.vsc,
+                                    self.cos, self.sin, num_q=self.nq, num_kv=self.nkv,
+                                    head_dim=self.hd, rope_half=self.half,
+                                    pair_stride=self.pair,
+                                    sqrt_n=float(np.sqrt(np.float32(self.hd))),
+                                    n_eps=float(np.float32(self.hd) * np.float32(1e-6)))
+        elif self.bq:
+            A.bq_attention(p, self.q_i8, self.qb, self.fq, self.k, self.ksc, self.v, self.vsc,
+                           self.out, self.partials, self.ps, num_q=self.nq, num_kv=self.nkv,
+                           head_dim=self.hd, kv_stride=self.kvs)
         elif phase == "append":
             A.dispatch_rope_cache_write(p, self.q, self.ks, self.vs, self.k, self.v, self.cos,
                                         self.sin, num_q=self.nq, num_kv=self.nkv,
@@ -887,6 +929,9 @@ class PrefillBf16:
 
     def step_bytes(self) -> int:
         cow = 2 * int(self.jobs[:, 2].sum()) if self.jobs.size else 0
+        if self.bq:  # bf16 q/k/v in, codes out; bf16 output
+            return self.n * ((self.nq + 2 * self.nkv) * self.hd * 3 +
+                             self.nq * self.hd * 2) + cow
         return self.n * (self.kvs * 2 * 2 * 2 + self.nq * self.hd * 2 * 3) + cow
 
     def dominant_bytes(self) -> int:
@@ -916,6 +961,8 @@ class PrefillBf16:
         pages = np.asarray(self.tables[i], dtype=np.int64)
         npage = pages.size
         idx = torch.from_numpy(pages).to(self.k.device)
+        if self.bq:
+            return self._cpu_baseline_bq(budget_s, hc, i, p0, idx, npage)
         kp = self.k.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
         vp = self.v.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
         kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
@@ -945,6 +992,46 @@ class PrefillBf16:
                            f"({keys} query-key pairs), the reference's token route at "
                            f"cap={threads} workers, median of {len(times)}")}
 
+    def _cpu_baseline_bq(self, budget_s, hc, i, p0, idx, npage):
+        """The oracle's bq token route (BqFlashPrefillFullKernel) on the last
+        16 query tokens of the longest sequence."""
+        import oracle
+
+        threads = hc["threads"]
+
+        def pages_of(t, per_row):
+            return np.ascontiguousarray(
+                t.view(-1, PAGE_LEN * per_row).index_select(0, idx).cpu().numpy()).reshape(-1)
+
+        kp, vp = pages_of(self.k, self.kvs), pages_of(self.v, self.kvs)
+        ksp, vsp = pages_of(self.ksc, self.nkv), pages_of(self.vsc, self.nkv)
+        n_s = 16
+        first = self.new - n_s
+        runs = np.asarray([[0, p0 + first, 0, npage]], dtype=np.int32)
+        base = np.arange(npage, dtype=np.int32) * PAGE_LEN
+        t0_, t1_ = i * self.new + first, (i + 1) * self.new
+        qh = np.ascontiguousarray(
+            self.q_i8.view(-1, self.nq * self.hd)[t0_:t1_].cpu().numpy()).reshape(-1)
+        qb = np.ascontiguousarray(self.qb.view(-1, self.nq)[t0_:t1_].cpu().numpy()).reshape(-1)
+        fq = np.ascontiguousarray(self.fq.view(-1, self.nq)[t0_:t1_].cpu().numpy()).reshape(-1)
+        keys = sum(p0 + first + t + 1 for t in range(n_s))
+        fl = 4 * self.hd * self.nq * keys
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            oracle.bq_attention(1, runs, base, qh, qb, fq, kp, ksp, vp, vsp, num_q=self.nq,
+                                num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs,
+                                window=0, cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
+                                cap=threads, threads=threads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
+                                                      "affinity_cpus")},
+                "sample": (f"last {n_s} query tokens of the longest sequence ({keys} query-key "
+                           f"pairs), the reference's bq token route at cap={threads} workers, "
+                           f"median of {len(times)}")}
 
 class PrefillSliding:
     """Config 11 (widening): chunked prefill of a sliding-window layer --
@@ -1372,7 +1459,7 @@ def main() -> None:
                     help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
                          "own pass or fused into the append kernel")
     ap.add_argument("--kv", choices=("bf16", "bq"), default="bf16",
-                    help="configs 6 and 11: bf16 or butterquant int8 KV")
+                    help="configs 4, 6, 11 and 12: bf16 or butterquant int8 KV")
     ap.add_argument("--oproj", action="store_true",
                     help="configs 1-3: the bf16 o_proj GEMM after the merge")
     ap.add_argument("--oquant", choices=("none", "separate", "fused"), default="none",
@@ -1401,7 +1488,7 @@ def main() -> None:
     elif a.config in (5, 8):
         w = DecodeBq(a.config, a.seed)
     elif a.config in (4, 12):
-        w = PrefillBf16(a.seed, a.config)
+        w = PrefillBf16(a.seed, a.config, a.kv)
     elif a.config == 9:
         w = PageCopyBench(a.seed)
     elif a.config == 10:
@@ -1458,7 +1545,8 @@ def main() -> None:
         res["pct_mfma_peak"] = round(100 * value_override / MFMA_BF16_PEAK_TFLOPS, 2)
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 "traffic.json")
-    key = f"config{a.config}_cap{a.cap}" + ("_bq" if a.kv == "bq" and a.config in (6, 11) else "")
+    key = f"config{a.config}_cap{a.cap}" + ("_bq" if a.kv == "bq" and a.config in (4, 6, 11, 12)
+                                            else "")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
             measured = json.load(f).get(key)

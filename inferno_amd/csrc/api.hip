@@ -1088,6 +1088,23 @@ int32_t bq_attention(const void* image_dev, const int64_t* info, const void* q_i
               "bq_block_quant");
     return ok();
   }
+  if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 512 &&
+      num_q == 8 * num_kv && page_mask < 0 &&
+      (info[13] >> g.shift) + 1 <= ifr::prefill_wide_max_pages()) {
+    // Prefill chunk of a full-attention layer at head_dim 512 / GQA 8.
+    IFR_HIP(ifr::launch_prefill_wide_mfma_bq(
+                static_cast<const int32_t*>(image_dev), static_cast<int>(info[14]), q_i8,
+                qi_bias, f_q, k_base, k_scale, v_base, v_scale, output,
+                static_cast<int>(num_q), static_cast<int>(num_kv), kv_stride, g,
+                as_stream(stream)),
+            "prefill_wide_mfma_bq");
+    if (o_i8)
+      IFR_HIP(ifr::launch_bq_block_quant(output, o_i8, o_sa, num_q * head_dim,
+                                         static_cast<int>(head_dim), info[5],
+                                         as_stream(stream)),
+              "bq_block_quant");
+    return ok();
+  }
   IFR_HIP(ifr::launch_bq_attention(static_cast<const int32_t*>(image_dev),
                                    static_cast<int>(info[0]), static_cast<int>(info[1]),
                                    static_cast<int>(info[2]), q_i8, qi_bias, f_q, k_base,

@@ -28,6 +28,16 @@
 // into LDS (32 keys of 1 KiB rows, double-buffered) and the transposing
 // V^T reads are those of prefill_full_mfma_kernel (prefill.hip).
 //
+// kBq: the butterquant variant (BqFlashPrefillFullKernel, butterquant_
+// kernels/attention.mojo:267-351, at Gemma-4's bq full layer, modeling/
+// gemma_4_moe_bq.mojo:527-553).  K codes (512-byte rows) are staged straight
+// into LDS; each wave's score half is sum k*q over its dims from
+// v_mfma_i32_32x32x32_i8 plus 128 * sum q over those dims, so the two halves
+// add (as integers, exactly) to the reference's VNNI raw dot, and the score
+// is formed in the reference's order, ((raw - qi_bias) * f_q) * k_scale /
+// 127^2.  V codes pass through registers to LDS as bf16 (exact for int8)
+// and the V scale enters the weight as (w * v_scale) / 127.
+//
 // Blocks run in an XCD-aware order: launch block b runs work item
 // (b % 8) * per_xcd + b / 8, so the consecutive items of one plan query
 // block (its 8 sub-blocks x kv heads) run on one XCD and share its L2.
@@ -60,18 +70,27 @@ static_assert(kPrefillTokens % kWTokens == 0, "plan query blocks split into kern
 static_assert(4 * kWTileBytes + kPWaves * kWXBytes + 4 * kWLdsPages <= 160 * 1024,
               "LDS budget");
 
+typedef int wi32x4_t __attribute__((ext_vector_type(4)));
+typedef int wi32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kWBqRowBytes = kWD;  // one kv head's row of int8 codes
+
+template <bool kBq>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_wide_mfma_kernel(
-    const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
-    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int32_t* __restrict__ image, const void* __restrict__ qp,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const void* __restrict__ kcp, const float* __restrict__ k_scale,
+    const void* __restrict__ vcp, const float* __restrict__ v_scale,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride, int shift,
     int row_mask, int num_items, int per_xcd) {
-  __shared__ __align__(16) uint8_t kbuf0[kWTileBytes];
-  __shared__ __align__(16) uint8_t kbuf1[kWTileBytes];
+  __shared__ __align__(16) uint8_t kbuf0[kBq ? kWKeys * kWBqRowBytes : kWTileBytes];
+  __shared__ __align__(16) uint8_t kbuf1[kBq ? kWKeys * kWBqRowBytes : kWTileBytes];
   __shared__ __align__(16) uint8_t vbuf0[kWTileBytes];
   __shared__ __align__(16) uint8_t vbuf1[kWTileBytes];
   __shared__ __align__(16) uint8_t xbuf[kPWaves * kWXBytes];
   __shared__ int32_t page_rows[kWLdsPages];
+  // bq: the staged keys' K scales (0 .. 31) and V scales (32 .. 63), per buffer.
+  __shared__ __align__(16) float scl[2][kBq ? 2 * kWKeys : 1];
   const int item = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
   if (item >= num_items) return;  // block-uniform, before any barrier
   const int tid = threadIdx.x;
@@ -116,18 +135,42 @@ void prefill_wide_mfma_kernel(
   // Q^T fragments of this wave's dims: lane holds
   // Q[row][256*dh + 16*d + 8*half .. +7] for 16-dim steps d.  In AGPRs, as in
   // the 256-dim kernel.
-  bf16x8_t qf[kWHalf / 16];
-  {
-    const uint16_t* qr = q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kWD +
-                         kWHalf * dh + 8 * half;
+  // bq: the codes Q[row][256*dh + 32*d + 16*half .. +15], 128 * sum of the
+  // wave's 256 codes of the row, and the row's bias and f_q.
+  constexpr int kQFrags = kBq ? kWHalf / 32 : kWHalf / 16;
+  using QFrag = typename std::conditional<kBq, wi32x4_t, bf16x8_t>::type;
+  QFrag qf[kQFrags];
+  int qs128 = 0;
+  float qb_row = 0.0f, fq_row = 0.0f;
+  const int64_t q_row = static_cast<int64_t>(row_live ? tok : t0) * num_q + head;
+  if constexpr (kBq) {
+    const int8_t* qr = static_cast<const int8_t*>(qp) + q_row * kWD + kWHalf * dh + 16 * half;
+    int qs = 0;
 #pragma unroll
-    for (int d = 0; d < kWHalf / 16; ++d) {
+    for (int d = 0; d < kQFrags; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * d);
+      qf[d] = __builtin_bit_cast(wi32x4_t, v);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.x), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, qs, false);
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(qs),
+                                                    static_cast<uint32_t>(qs), false, false);
+    qs128 = 128 * (static_cast<int>(sw[0]) + static_cast<int>(sw[1]));
+    qb_row = qi_bias[q_row];
+    fq_row = f_q[q_row];
+  } else {
+    const uint16_t* qr =
+        static_cast<const uint16_t*>(qp) + q_row * kWD + kWHalf * dh + 8 * half;
+#pragma unroll
+    for (int d = 0; d < kQFrags; ++d) {
       const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
       qf[d] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
 #pragma unroll
-  for (int d = 0; d < kWHalf / 16; ++d) asm volatile("" : "+a"(qf[d]));
+  for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
 
   // acc = acc_stored * S (prefill_full_mfma_kernel's scheme).
   f32x16_t acc[kWDimBlocks];
@@ -141,42 +184,103 @@ void prefill_wide_mfma_kernel(
   for (int i = tid; i < n_pages; i += kPThreads) page_rows[i] = rows[i];
   __syncthreads();
 
-  // Staging: wave w moves key rows kWStageRows*w .. +7 of K and of V, one
-  // 1 KiB row per load (lane p: 16 bytes).  Lane p writes LDS chunk p; for K
-  // it holds global chunk p ^ (key & 15), for V chunk p ^ 2*(key & 3).  Keys
+  // Staging: wave w moves key rows kWStageRows*w .. +7 of K and of V.  bf16:
+  // one 1 KiB row per load (lane p: 16 bytes); lane p writes LDS chunk p, for
+  // K holding global chunk p ^ (key & 15), for V chunk p ^ 2*(key & 3).  Keys
   // past count_max read the last key (in bounds); their V rows are zeroed
-  // once the loads have landed.
-  const uint16_t* kbase = kc + static_cast<int64_t>(g) * kWD;
-  const uint16_t* vbase = vc + static_cast<int64_t>(g) * kWD;
-  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+  // once the loads have landed.  bq: K rows of 512 bytes, two per load (lane
+  // p: row p / 32, LDS chunk p % 32 holding global chunk (p % 32) ^ (key &
+  // 15)); V codes to registers (lane p: row 2i + p / 32, 16 codes from
+  // 16 * (p % 32)), written to LDS as bf16 rows once landed; wave 0 moves the
+  // 32 keys' K scales (lanes 0-31) and V scales (lanes 32-63).
+  const uint16_t* kbase = static_cast<const uint16_t*>(kcp) + static_cast<int64_t>(g) * kWD;
+  const uint16_t* vbase = static_cast<const uint16_t*>(vcp) + static_cast<int64_t>(g) * kWD;
+  const int8_t* kbase8 = static_cast<const int8_t*>(kcp) + static_cast<int64_t>(g) * kWD;
+  const int8_t* vbase8 = static_cast<const int8_t*>(vcp) + static_cast<int64_t>(g) * kWD;
+  uint4 vcodes[kBq ? kWStageRows / 2 : 1];
+  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst, int buf) {
+    if constexpr (kBq) {
 #pragma unroll
-    for (int i = 0; i < kWStageRows; ++i) {
-      const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
-      const int key = min(it * kWKeys + r, count_max - 1);
-      const int prow = __builtin_amdgcn_readfirstlane(page_rows[key >> shift]);
-      const int64_t off = (static_cast<int64_t>(prow) + (key & row_mask)) * kv_stride;
-      const uint8_t* krow = reinterpret_cast<const uint8_t*>(kbase + off);  // uniform
-      const uint8_t* vrow = reinterpret_cast<const uint8_t*>(vbase + off);
-      const uint32_t lk = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
-      const uint32_t lv = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
-      __builtin_amdgcn_global_load_lds(krow + lk, (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vrow + lv, (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
+      for (int i = 0; i < kWStageRows / 2; ++i) {
+        const int r = wave * kWStageRows + 2 * i + (lane >> 5);
+        const int key = min(it * kWKeys + r, count_max - 1);
+        const int64_t off =
+            (static_cast<int64_t>(page_rows[key >> shift]) + (key & row_mask)) * kv_stride;
+        const int c = lane & 31;
+        __builtin_amdgcn_global_load_lds(
+            kbase8 + off + 16 * (c ^ (r & 15)),
+            (lds_void_t*)(kdst + (wave * kWStageRows + 2 * i) * kWBqRowBytes), 16, 0, 0);
+        vcodes[i] = *reinterpret_cast<const uint4*>(vbase8 + off + 16 * c);
+      }
+      if (wave == 0) {
+        const int key = min(it * kWKeys + (lane & 31), count_max - 1);
+        const int64_t si =
+            (static_cast<int64_t>(page_rows[key >> shift]) + (key & row_mask)) * num_kv + g;
+        __builtin_amdgcn_global_load_lds((lane < 32 ? k_scale : v_scale) + si,
+                                         (lds_void_t*)(&scl[buf][0]), 4, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWStageRows; ++i) {
+        const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
+        const int key = min(it * kWKeys + r, count_max - 1);
+        const int prow = __builtin_amdgcn_readfirstlane(page_rows[key >> shift]);
+        const int64_t off = (static_cast<int64_t>(prow) + (key & row_mask)) * kv_stride;
+        const uint8_t* krow = reinterpret_cast<const uint8_t*>(kbase + off);  // uniform
+        const uint8_t* vrow = reinterpret_cast<const uint8_t*>(vbase + off);
+        const uint32_t lk =
+            static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
+        const uint32_t lv =
+            static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+        __builtin_amdgcn_global_load_lds(krow + lk, (lds_void_t*)(kdst + r * kWRowBytes), 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(vrow + lv, (lds_void_t*)(vdst + r * kWRowBytes), 16,
+                                         0, 0);
+      }
     }
   };
-  auto zero_tail = [&](int it, uint8_t* vdst) {
-    if ((it + 1) * kWKeys <= count_max) return;  // block-uniform
+  // After the wave's loads have landed: bf16 zeroes the V rows of keys past
+  // count_max; bq writes its V codes as bf16 rows (zeros past count_max).
+  auto land_v = [&](int it, uint8_t* vdst) {
+    if constexpr (kBq) {
 #pragma unroll
-    for (int i = 0; i < kWStageRows; ++i) {
-      const int r = wave * kWStageRows + i;
-      if (it * kWKeys + r >= count_max)
-        *reinterpret_cast<uint4*>(vdst + r * kWRowBytes + 16 * lane) =
-            make_uint4(0u, 0u, 0u, 0u);
+      for (int i = 0; i < kWStageRows / 2; ++i) {
+        const int r = wave * kWStageRows + 2 * i + (lane >> 5);
+        const bool in = it * kWKeys + r < count_max;
+        const uint32_t w[4] = {vcodes[i].x, vcodes[i].y, vcodes[i].z, vcodes[i].w};
+        uint32_t bf[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int b = 0; b < 4; b += 2) {
+            const float f0 = static_cast<float>(static_cast<int8_t>(w[j] >> (8 * b)));
+            const float f1 = static_cast<float>(static_cast<int8_t>(w[j] >> (8 * b + 8)));
+            bf[2 * j + b / 2] =
+                in ? ((__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u)) : 0u;
+          }
+        }
+        const int c0 = 2 * (lane & 31);
+        uint8_t* vr = vdst + r * kWRowBytes;
+        *reinterpret_cast<uint4*>(vr + 16 * (c0 ^ (2 * (r & 3)))) =
+            make_uint4(bf[0], bf[1], bf[2], bf[3]);
+        *reinterpret_cast<uint4*>(vr + 16 * ((c0 + 1) ^ (2 * (r & 3)))) =
+            make_uint4(bf[4], bf[5], bf[6], bf[7]);
+      }
+    } else {
+      if ((it + 1) * kWKeys <= count_max) return;  // block-uniform
+#pragma unroll
+      for (int i = 0; i < kWStageRows; ++i) {
+        const int r = wave * kWStageRows + i;
+        if (it * kWKeys + r >= count_max)
+          *reinterpret_cast<uint4*>(vdst + r * kWRowBytes + 16 * lane) =
+              make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
 
-  if (n_iters > 0) stage(0, kbuf0, vbuf0);
+  if (n_iters > 0) stage(0, kbuf0, vbuf0, 0);
   __builtin_amdgcn_s_waitcnt(0);
-  if (n_iters > 0) zero_tail(0, vbuf0);
+  if (n_iters > 0) land_v(0, vbuf0);
   __syncthreads();
 
   // QK operand reads: chunk 32*dh + 2d + half of key row (row & 31), stored
@@ -194,8 +298,33 @@ void prefill_wide_mfma_kernel(
   const uint8_t* x_s0 = xbuf + (wave & ~1) * kWXBytes + 16 * lane;
   const uint8_t* x_s1 = xbuf + (wave | 1) * kWXBytes + 16 * lane;
 
+  // bq K operand reads: chunk 16*dh + 2d + half of key row (row & 31) of
+  // 512 bytes, stored at (16*dh + 2d + half) ^ (row & 15): kq_lane ^ 32d.
+  const int kq_lane = row * kWBqRowBytes + 256 * dh + 16 * ((row & 15) ^ half);
+  constexpr float kInv127 = 1.0f / 127.0f;
+  constexpr float kInv127Sq = kInv127 * kInv127;
+
   constexpr int kKAhead = 6;
-  auto qk = [&](const uint8_t* kl) {
+  // This wave's half of the scores.  bq: the integer dot over its dims plus
+  // 128 * its sum q, carried as bits in the float vector.
+  auto qk = [&](const uint8_t* kl) -> f32x16_t {
+    if constexpr (kBq) {
+      wi32x16_t si;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) si[v] = 0;
+      uint4 kf[kQFrags];
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d)
+        kf[d] = *reinterpret_cast<const uint4*>(kl + (kq_lane ^ (32 * d)));
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d)
+        si = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(wi32x4_t, kf[d]), qf[d],
+                                                   si, 0, 0, 0);
+      f32x16_t bits;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) bits[v] = __int_as_float(si[v] + qs128);
+      return bits;
+    } else {
     f32x16_t sblk;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
@@ -218,10 +347,13 @@ void prefill_wide_mfma_kernel(
     }
     __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
     return sblk;
+    }
   };
   // The pair's full scores: own half out, barrier, the other half in, added
-  // as S_0 + S_1 in both waves.
-  auto exchange = [&](const f32x16_t& own) {
+  // as S_0 + S_1 in both waves.  bq: the integer halves add exactly to the
+  // raw dot; the score is then ((raw - qi_bias) * f_q) * k_scale / 127^2
+  // (value 4j + i holds key 8j + 4*half + i of the block).
+  auto exchange = [&](const f32x16_t& own, int buf) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       *reinterpret_cast<float4*>(x_own + 1024 * c) =
@@ -232,10 +364,24 @@ void prefill_wide_mfma_kernel(
     for (int c = 0; c < 4; ++c) {
       const float4 a = *reinterpret_cast<const float4*>(x_s0 + 1024 * c);
       const float4 b = *reinterpret_cast<const float4*>(x_s1 + 1024 * c);
-      sfull[4 * c] = a.x + b.x;
-      sfull[4 * c + 1] = a.y + b.y;
-      sfull[4 * c + 2] = a.z + b.z;
-      sfull[4 * c + 3] = a.w + b.w;
+      if constexpr (kBq) {
+        const float4 ks4 = *reinterpret_cast<const float4*>(&scl[buf][8 * c + 4 * half]);
+        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+        const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int raw = __float_as_int(av[i]) + __float_as_int(bv[i]);
+          float sc = static_cast<float>(raw) - qb_row;
+          sc = sc * fq_row;
+          sc = sc * ks[i];
+          sfull[4 * c + i] = sc * kInv127Sq;
+        }
+      } else {
+        sfull[4 * c] = a.x + b.x;
+        sfull[4 * c + 1] = a.y + b.y;
+        sfull[4 * c + 2] = a.z + b.z;
+        sfull[4 * c + 3] = a.w + b.w;
+      }
     }
     return sfull;
   };
@@ -267,8 +413,29 @@ void prefill_wide_mfma_kernel(
   };
   // Fold of the two tiles and acc_stored += V^T P''^T (prefill.hip's fold_pv
   // on one 32-key block).
-  auto fold_pv = [&](const uint8_t* vl, const float (&w)[2][8], const float (&corr)[2],
-                     const bool (&big)[2]) {
+  auto fold_pv = [&](const uint8_t* vl, const float (&w0)[2][8], const float (&corr)[2],
+                     const bool (&big)[2], int buf) {
+    // bq: the weights as (w * v_scale) / 127; lane value i of tile u is key
+    // 16u + 8*(i/4) + 4*half + i%4.
+    float w[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float vs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (kBq) {
+          const float4 v4 =
+              *reinterpret_cast<const float4*>(&scl[buf][kWKeys + 16 * u + 8 * j + 4 * half]);
+          vs[0] = v4.x;
+          vs[1] = v4.y;
+          vs[2] = v4.z;
+          vs[3] = v4.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[u][4 * j + i] = kBq ? (w0[u][4 * j + i] * vs[i]) * kInv127 : w0[u][4 * j + i];
+      }
+    }
     float S_new = S * (corr[0] * corr[1]);
     if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
 #pragma unroll
@@ -352,9 +519,9 @@ void prefill_wide_mfma_kernel(
 #pragma unroll
     for (int b = 0; b < kWDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
 #pragma unroll
-    for (int d = 0; d < kWHalf / 16; ++d) asm volatile("" : "+a"(qf[d]));
+    for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
     __builtin_amdgcn_s_waitcnt(0);
-    if (it + 1 < n_iters) zero_tail(it + 1, vnext);
+    if (it + 1 < n_iters) land_v(it + 1, vnext);
     __syncthreads();
   };
   // An iteration whose keys are valid for every row of the block.  The
@@ -362,12 +529,12 @@ void prefill_wide_mfma_kernel(
   // iteration they are clamped, in-bounds rows of an unused buffer).
   auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                             uint8_t* vnext) {
-    stage(it + 1, knext, vnext);
+    stage(it + 1, knext, vnext, (it + 1) & 1);
     float w[2][8], corr[2];
     bool big[2];
-    const f32x16_t s = exchange(qk(kl));
+    const f32x16_t s = exchange(qk(kl), it & 1);
     softmax_pair(s, 0, false, w, corr, big);
-    fold_pv(vl, w, corr, big);
+    fold_pv(vl, w, corr, big, it & 1);
     iteration_end(it, vnext);
   };
   // An iteration on the causal diagonal: per-tile masks (a pair whose rows
@@ -377,12 +544,12 @@ void prefill_wide_mfma_kernel(
   auto masked_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                               uint8_t* vnext) {
     const int key_base = it * kWKeys;
-    if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+    if (it + 1 < n_iters) stage(it + 1, knext, vnext, (it + 1) & 1);
     float w[2][8], corr[2];
     bool big[2];
-    const f32x16_t s = exchange(qk(kl));
+    const f32x16_t s = exchange(qk(kl), it & 1);
     softmax_pair(s, key_base, true, w, corr, big);
-    fold_pv(vl, w, corr, big);
+    fold_pv(vl, w, corr, big, it & 1);
     iteration_end(it, vnext);
   };
   // Iterations whose keys are valid for every row of the block run the
@@ -441,9 +608,24 @@ hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const
   if (num_qblocks <= 0) return hipSuccess;
   const int items = num_qblocks * kWSub * num_kv;
   const int per_xcd = (items + kXcds - 1) / kXcds;
-  hipLaunchKernelGGL(prefill_wide_mfma_kernel, dim3(per_xcd * kXcds), dim3(kPThreads), 0,
-                     stream, image, static_cast<const uint16_t*>(q),
-                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+  hipLaunchKernelGGL(prefill_wide_mfma_kernel<false>, dim3(per_xcd * kXcds), dim3(kPThreads), 0,
+                     stream, image, q, nullptr, nullptr, k, nullptr, v, nullptr,
+                     static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
+                     geom.row_mask, items, per_xcd);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_wide_mfma_bq(const int32_t* image, int num_qblocks, const void* q_i8,
+                                       const float* qi_bias, const float* f_q, const void* k,
+                                       const float* k_scale, const void* v,
+                                       const float* v_scale, void* output, int num_q,
+                                       int num_kv, int64_t kv_stride, PagedGeom geom,
+                                       hipStream_t stream) {
+  if (num_qblocks <= 0) return hipSuccess;
+  const int items = num_qblocks * kWSub * num_kv;
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  hipLaunchKernelGGL(prefill_wide_mfma_kernel<true>, dim3(per_xcd * kXcds), dim3(kPThreads), 0,
+                     stream, image, q_i8, qi_bias, f_q, k, k_scale, v, v_scale,
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
                      geom.row_mask, items, per_xcd);
   return hipGetLastError();

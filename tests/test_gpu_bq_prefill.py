@@ -1,6 +1,8 @@
-"""GPU parity of the butterquant MFMA sliding-window prefill
-(BqFlashPrefillSlidingKernel, butterquant_kernels/attention.mojo:170-264)
-against the oracle's bq token route: int8 K/V codes with f32 scales per row
+"""GPU parity of the butterquant MFMA prefill -- sliding windows at head_dim
+256 / GQA 2 (BqFlashPrefillSlidingKernel, butterquant_kernels/attention.mojo:
+170-264) and full attention at Gemma-4's full-layer shape, head_dim 512 /
+GQA 8 (BqFlashPrefillFullKernel, :267-351) -- against the oracle's bq token
+route: int8 K/V codes with f32 scales per row
 and kv head, int8 queries with their bias (128 * sum q) and f_q.  The scores
 come from an int8 MFMA and are formed in the reference's order, so they
 equal the oracle's; the outputs are held to 1e-2 (one bf16 spacing where
@@ -12,14 +14,15 @@ import pytest
 
 import oracle
 from inferno_amd import attention as A
-from inferno_amd.kv import SLIDING, AttentionPlan, KVRunTable
+from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16
+from tests.helpers import compare_bf16, make_prefill_case
 
 pytestmark = pytest.mark.gpu
 
 NQ, NKV, D = 16, 8, 256
 KVS = NKV * D
+WNQ, WNKV, WD = 16, 2, 512
 
 
 def _table(runs, rows) -> KVRunTable:
@@ -64,7 +67,7 @@ def _run(window, prefix, new, ring, page_len, seed, q_scale=1.0, quant=False):
     k = _codes(cache_rows * KVS, seed + 3, outliers=True)
     v = _codes(cache_rows * KVS, seed + 4)
     ks = rng.uniform(0.5, 1.5, cache_rows * NKV).astype(np.float32)
-    vs = rng.uniform(0.01, 0.05, cache_rows * NKV).astype(np.float32)
+    vs = rng.uniform(0.5, 2.0, cache_rows * NKV).astype(np.float32)
     plan = AttentionPlan(_table(runs, rows), n, kind=SLIDING, window=window,
                          cache_size=ring * page_len, page_len=page_len, cache_rows=cache_rows,
                          cap=16, kv_row_bytes=KVS)
@@ -119,4 +122,64 @@ def test_bq_sliding_prefill_page_sizes(page_len, ring):
     announce(f"bq mfma sliding prefill page_len={page_len}")
     r = _run(1024, [0, 900, 2500], [96, 129, 64], ring, page_len, 11)
     print(f"  page_len {page_len}: {r}", flush=True)
+    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+
+
+def _run_full(prefix, new, page_len, seed, quant=False):
+    """Full attention at head_dim 512 / GQA 8 over page lists (no ring)."""
+    case = make_prefill_case(seed, prefix, new, page_len=page_len)
+    runs, rows, cache_rows = case.runs, case.base_rows, case.cache_rows
+    kvs = WNKV * WD
+    n = sum(new)
+    rng = np.random.default_rng(seed + 1)
+    q = _codes(n * WNQ * WD, seed + 2)
+    qb = (128.0 * q.reshape(n * WNQ, WD).astype(np.int64).sum(axis=1)).astype(np.float32)
+    # A 512-dim dot has sqrt(2) times the spread of a 256-dim one.
+    fq = rng.uniform(0.35, 1.05, n * WNQ).astype(np.float32)
+    k = _codes(cache_rows * kvs, seed + 3, outliers=True)
+    v = _codes(cache_rows * kvs, seed + 4)
+    ks = rng.uniform(0.5, 1.5, cache_rows * WNKV).astype(np.float32)
+    vs = rng.uniform(0.5, 2.0, cache_rows * WNKV).astype(np.float32)
+    plan = AttentionPlan(_table(runs, rows), n, kind=FULL, window=0, cache_size=page_len,
+                         page_len=page_len, cache_rows=cache_rows, cap=16, kv_row_bytes=kvs)
+    assert plan.summary.mode == 2 and int(plan.info[14]) > 0, "no query blocks"
+    out = empty_dev(n * WNQ * WD, np.uint16)
+    partials, ps = A.partials_buffer(plan, WNQ, WD)
+    args = (plan, to_dev(q), to_dev(qb), to_dev(fq), to_dev(k), to_dev(ks), to_dev(v),
+            to_dev(vs))
+    kw = dict(num_q=WNQ, num_kv=WNKV, head_dim=WD, kv_stride=kvs)
+    A.bq_attention(*args, out, partials, ps, **kw)
+    got = from_dev(out, np.uint16)
+    if quant:
+        out2 = empty_dev(n * WNQ * WD, np.uint16)
+        o_i8 = empty_dev(n * WNQ * WD, np.int8)
+        o_sa = empty_dev(n * WNQ, np.float32)
+        A.bq_attention(*args, out2, partials, ps, **kw, o_i8=o_i8, o_sa=o_sa)
+        assert np.array_equal(from_dev(out2, np.uint16), got), "quant changed the output"
+        want_i8, want_sa = oracle.bq_block_quant(got, cols=WNQ * WD, block=WD)
+        assert np.array_equal(from_dev(o_i8, np.int8).reshape(n, WNQ * WD), want_i8)
+        assert np.array_equal(from_dev(o_sa, np.float32).view(np.uint32),
+                              want_sa.reshape(-1).view(np.uint32))
+    ref = oracle.bq_attention(FULL, runs, rows, q, qb, fq, k, ks, v, vs, num_q=WNQ,
+                              num_kv=WNKV, head_dim=WD, kv_stride=kvs, window=0,
+                              cache_size=page_len, page_len=page_len, seq_len=n, cap=16,
+                              threads=16)
+    return compare_bf16(got, ref)
+
+
+def test_bq_full_layer_prefill():
+    """Chunks from position 0, short and long prefixes, blocks of 1-8 live
+    tokens (pairs without live rows), a one-token chunk; the o_proj block
+    quant on top."""
+    announce("bq mfma full-layer prefill")
+    r = _run_full([0, 100, 1000, 3000, 63, 5], [40, 33, 100, 64, 1, 7], 64, 21, quant=True)
+    print(f"  full layer: {r}", flush=True)
+    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+
+
+@pytest.mark.parametrize("page_len", [8, 1024])
+def test_bq_full_layer_prefill_page_sizes(page_len):
+    announce(f"bq mfma full-layer prefill page_len={page_len}")
+    r = _run_full([0, 900, 2500], [96, 129, 64], page_len, 23)
+    print(f"  full layer page_len {page_len}: {r}", flush=True)
     assert r["n_fail"] == 0 and r["n_nan"] == 0, r
