@@ -1407,6 +1407,15 @@ def measure(w, steps: int, warmup: int):
         for ph in w.phases:
             w.launch(ph)
     torch.cuda.synchronize()
+    # Past the W warmup steps, keep stepping (untimed) until at least 0.2 s of
+    # work has run, so that a step of a few microseconds (config 1) is timed
+    # at steady clocks rather than on a GPU still leaving its idle state.
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < 0.2:
+        for _ in range(8):
+            for ph in w.phases:
+                w.launch(ph)
+        torch.cuda.synchronize()
     # Timed region 1: wall clock over K steps, nothing but the step's launches.
     t0 = time.perf_counter()
     for _ in range(steps):
