@@ -35,6 +35,60 @@ __device__ __forceinline__ float bpermute_f32(float v, int src_lane) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
 }
 
+// v[lane ^ M] for M = 1 .. 32 on the VALU: DPP inside 16-lane rows (xor 4 as
+// the rotate by 12 or by 4, picked by lane bit 2), the gfx950 lane swaps
+// across rows (with v as both operands the results are the pair's lower and
+// upper members).
+constexpr int kDppRowRor12 = 0x12C;  // lane i <- (i-12)%16 = (i+4)%16 within 16 lanes
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v, int lane) {
+  if constexpr (M == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppXor1, 0xF, 0xF, true);
+  } else if constexpr (M == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppXor2, 0xF, 0xF, true);
+  } else if constexpr (M == 4) {
+    // row_ror:n gives lane i the value of lane (i - n) mod 16.
+    const uint32_t a = __builtin_amdgcn_update_dpp(0, v, kDppRowRor4, 0xF, 0xF, true);
+    const uint32_t b = __builtin_amdgcn_update_dpp(0, v, kDppRowRor12, 0xF, 0xF, true);
+    return (lane & 4) ? a : b;
+  } else if constexpr (M == 8) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppRowRor8, 0xF, 0xF, true);
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+template <int M>
+__device__ __forceinline__ float xor_lane_f32(float v, int lane) {
+  return __uint_as_float(xor_lane_u32<M>(__float_as_uint(v), lane));
+}
+template <int M>
+__device__ __forceinline__ int xor_lane_i32(int v, int lane) {
+  return static_cast<int>(xor_lane_u32<M>(static_cast<uint32_t>(v), lane));
+}
+// f(x, x[lane ^ M]) for M = 1, 2, 4, .., 32 in that order.
+template <typename T, typename F>
+__device__ __forceinline__ T butterfly_all(T x, int lane, F f) {
+  if constexpr (std::is_same<T, float>::value) {
+    x = f(x, xor_lane_f32<1>(x, lane));
+    x = f(x, xor_lane_f32<2>(x, lane));
+    x = f(x, xor_lane_f32<4>(x, lane));
+    x = f(x, xor_lane_f32<8>(x, lane));
+    x = f(x, xor_lane_f32<16>(x, lane));
+    return f(x, xor_lane_f32<32>(x, lane));
+  } else {
+    x = f(x, xor_lane_i32<1>(x, lane));
+    x = f(x, xor_lane_i32<2>(x, lane));
+    x = f(x, xor_lane_i32<4>(x, lane));
+    x = f(x, xor_lane_i32<8>(x, lane));
+    x = f(x, xor_lane_i32<16>(x, lane));
+    return f(x, xor_lane_i32<32>(x, lane));
+  }
+}
+
 // Absmax int8 quantisation of the wave's 64 * EPL values (EPL per lane);
 // returns amax and writes the lane's EPL codes packed little-endian into
 // codes[EPL / 4].
@@ -47,11 +101,8 @@ __device__ __forceinline__ float absmax_quantize(const float* r, uint32_t* codes
     const float a = fabsf(r[e]);
     vmax = a > vmax ? a : vmax;
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float o = shfl_xor_f32(vmax, m);
-    vmax = o > vmax ? o : vmax;
-  }
+  const int lane = __lane_id();
+  vmax = butterfly_all(vmax, lane, [](float a, float o) { return o > a ? o : a; });
   float amax = vmax;
   if (amax < 1e-10f) amax = 1e-10f;
   const float inv = 127.0f / amax;
@@ -70,8 +121,7 @@ __device__ __forceinline__ float absmax_quantize(const float* r, uint32_t* codes
     }
     codes[w] = packed;
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) s += shfl_xor_i32(s, m);
+  s = butterfly_all(s, lane, [](int a, int o) { return a + o; });
   *qsum = s;
   return amax;
 }
@@ -92,15 +142,23 @@ __device__ __forceinline__ void fwht_wave(float* r, int lane) {
       r[e + st] = a - b;
     }
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {  // strides EPL .. 32 * EPL
+  // Strides EPL .. 32 * EPL: lane bit m; the lower lane of a pair takes
+  // a + b, the upper a - b (a the lower lane's value), on the VALU.
+  auto stage = [&](auto mc) {
+    constexpr int m = decltype(mc)::value;
     const bool upper = (lane & m) != 0;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      const float p = shfl_xor_f32(r[e], m);
+      const float p = xor_lane_f32<m>(r[e], lane);
       r[e] = upper ? (p - r[e]) : (r[e] + p);
     }
-  }
+  };
+  stage(std::integral_constant<int, 1>{});
+  stage(std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 8>{});
+  stage(std::integral_constant<int, 16>{});
+  stage(std::integral_constant<int, 32>{});
   const float sc = static_cast<float>(1.0 / static_cast<double>(sqrtf(64.0f * EPL)));
 #pragma unroll
   for (int e = 0; e < EPL; ++e) r[e] = r[e] * sc;
@@ -168,10 +226,10 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
           ssq = fmaf(x, x, ssq);
         }
       }
-      ssq = ssq + shfl_xor_f32(ssq, 8);
-      ssq = ssq + shfl_xor_f32(ssq, 4);
-      ssq = ssq + shfl_xor_f32(ssq, 2);
-      ssq = ssq + shfl_xor_f32(ssq, 1);
+      ssq = ssq + xor_lane_f32<8>(ssq, lane);
+      ssq = ssq + xor_lane_f32<4>(ssq, lane);
+      ssq = ssq + xor_lane_f32<2>(ssq, lane);
+      ssq = ssq + xor_lane_f32<1>(ssq, lane);
       const float total = readlane_f32(ssq, 0);
       const float inv_rms = sqrt_n / sqrtf(total + n_eps);
       const uint16_t* gamma = is_q ? q_norm : k_norm;
@@ -524,7 +582,7 @@ __global__ __launch_bounds__(256) void bq_block_quant_kernel(
   const uint16_t* s = src + base;
   float amax = 0.0f;
   for (int i = lane; i < block; i += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(s[i])));
-  for (int msk = 1; msk < 64; msk <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, msk));
+  amax = butterfly_all(amax, lane, [](float a, float o) { return fmaxf(a, o); });
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int8_t* d = x_i8 + base;
   for (int i = lane; i < block; i += 64) {

@@ -109,7 +109,7 @@ __device__ __forceinline__ int dpp_i32(int v) {
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8 lanes
-constexpr int kDppRowRor8 = 0x128;     // lane i <- (i+8)%16 within 16 lanes
+constexpr int kDppRowRor8 = 0x128;     // lane i <- (i-8)%16 = lane i ^ 8 within 16 lanes
 
 __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
   int lane = __lane_id();
@@ -132,7 +132,7 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
 // the pair.  A commutative op on them therefore gives, bit for bit, what
 // x op shfl_xor(x, 32 | 16) gives, as one VALU operation instead of an LDS
 // permute round trip.
-constexpr int kDppRowRor4 = 0x124;  // lane i <- (i+4)%16 within 16 lanes
+constexpr int kDppRowRor4 = 0x124;  // lane i <- (i-4)%16 within 16 lanes
 __device__ __forceinline__ float pair_sum32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
                                                   false, false);
