@@ -1,10 +1,12 @@
-"""Randomized GPU parity sweep over the bf16 attention routes: seeded cases
+"""Randomized GPU parity sweep over the attention routes: seeded cases
 drawing the layer shape (16q/8kv x 256 or 16q/2kv x 512), full attention or
 sliding windows (multiples of 16 and not, so both prefill kernels and the
 token route run), page sizes 8-1024, rings that wrap, batches of 1-12 runs,
 contexts including 0, 15/16/17 and page edges, decode steps or prefill
 chunks, and worker caps 1-512.  Every output element against the oracle,
-within 1e-2 (one bf16 spacing where |x| >= 2); each case prints its draw."""
+within 1e-2 (one bf16 spacing where |x| >= 2); each case prints its draw.
+The butterquant routes run on the same draws (at the bq layer shapes), bit-
+exact off the MFMA prefill."""
 import numpy as np
 import pytest
 
@@ -97,3 +99,53 @@ def test_random_plan(seed):
     print(f"  mode={plan.summary.mode} items={plan.summary.num_items} "
           f"qblocks={int(plan.info[14])}: {r}", flush=True)
     assert r["n_nan"] == 0 and r["n_fail"] == 0, (c, r)
+
+
+def _codes(n, rng):
+    return rng.integers(-127, 128, n).astype(np.int8)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_bq_plan(seed):
+    """The butterquant routes on the same draws (synthetic codes, scales with
+    O(1) outputs): bit-exact off the MFMA prefill, within the bar on it."""
+    c = _draw(100 + seed)
+    if c["kind"] == SLIDING and (c["nq"], c["d"]) == (16, 512):
+        c["kind"], c["window"] = FULL, 0  # bq sliding layers are 16q/8kv x 256
+    if c["kind"] == FULL and c["d"] == 256:
+        c["nq"], c["nkv"], c["d"] = 16, 2, 512  # bq full layers are 16q/2kv x 512
+    rng = np.random.default_rng(3000 + seed)
+    runs, rows, cache_rows, ring, n = _layout(c, rng)
+    nq, nkv, d, pl = c["nq"], c["nkv"], c["d"], c["page_len"]
+    kvs = nkv * d
+    cache_size = ring * pl if c["kind"] == SLIDING else pl
+    announce(f"random bq plan {seed}: {'sliding' if c['kind'] == SLIDING else 'full'} "
+             f"{nq}q/{nkv}kv x {d} page {pl} window {c['window']} "
+             f"{'decode' if c['decode'] else 'prefill'} B={len(c['prefix'])} cap={c['cap']} "
+             f"prefix={c['prefix']} new={c['new']}")
+    q = _codes(n * nq * d, rng)
+    qb = (128.0 * q.reshape(n * nq, d).astype(np.int64).sum(axis=1)).astype(np.float32)
+    fq = (rng.uniform(0.5, 1.5, n * nq) / np.sqrt(d / 256)).astype(np.float32)
+    k, v = _codes(cache_rows * kvs, rng), _codes(cache_rows * kvs, rng)
+    ks = rng.uniform(0.5, 1.5, cache_rows * nkv).astype(np.float32)
+    vs = rng.uniform(0.5, 2.0, cache_rows * nkv).astype(np.float32)
+    plan = AttentionPlan(_table(runs, rows), n, kind=c["kind"], window=c["window"],
+                         cache_size=cache_size, page_len=pl, cache_rows=cache_rows,
+                         cap=c["cap"], kv_row_bytes=kvs)
+    out = empty_dev(n * nq * d, np.uint16)
+    partials, ps = A.partials_buffer(plan, nq, d)
+    A.bq_attention(plan, to_dev(q), to_dev(qb), to_dev(fq), to_dev(k), to_dev(ks), to_dev(v),
+                   to_dev(vs), out, partials, ps, num_q=nq, num_kv=nkv, head_dim=d,
+                   kv_stride=kvs)
+    got = from_dev(out, np.uint16)
+    ref = oracle.bq_attention(c["kind"], runs, rows, q, qb, fq, k, ks, v, vs, num_q=nq,
+                              num_kv=nkv, head_dim=d, kv_stride=kvs, window=c["window"],
+                              cache_size=cache_size, page_len=pl, seq_len=n, cap=c["cap"],
+                              threads=16)
+    r = compare_bf16(got, ref)
+    mfma = int(plan.info[14]) > 0 and plan.summary.mode in (1, 2)
+    print(f"  mode={plan.summary.mode} items={plan.summary.num_items} mfma={mfma}: {r}",
+          flush=True)
+    assert r["n_nan"] == 0 and r["n_fail"] == 0, (c, r)
+    if not mfma:
+        assert np.array_equal(got, ref), (c, r)
