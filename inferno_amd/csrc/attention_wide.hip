@@ -103,8 +103,8 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   __shared__ __align__(16) uint8_t qs[kBq ? 16 : kWG * kWQPitch];
 
   const int lane = threadIdx.x;
-  const int g = blockIdx.y;
-  const int32_t* item = image + sload(image + kHdrOffItems) + blockIdx.x * kItemWords;
+  const int g = blockIdx.x;
+  const int32_t* item = image + sload(image + kHdrOffItems) + blockIdx.y * kItemWords;
   const int q_row = sload(item);
   const int run = sload(item + 1);
   const int start_pos = sload(item + 2);
@@ -316,7 +316,7 @@ hipError_t launch_wide(const int32_t* image, int num_items, const void* q,
                        int64_t kv_stride, PagedGeom geom, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   const int64_t row_bytes = kv_stride * (kBq ? 1 : 2);
-  dim3 grid(num_items, num_kv);
+  dim3 grid(num_kv, num_items);  // an item's kv heads side by side
   const auto* qp = static_cast<const uint8_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k);
   const auto* vp = static_cast<const uint8_t*>(v);

@@ -324,9 +324,9 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
   constexpr int D = kBqD;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
-  const int g = blockIdx.y * 4 + wave;
+  const int g = blockIdx.x * 4 + wave;
   if (g >= num_kv) return;
-  const int32_t* item = image + image[kHdrOffItems] + blockIdx.x * kItemWords;
+  const int32_t* item = image + image[kHdrOffItems] + blockIdx.y * kItemWords;
   const int q_row = item[0];
   const int run = item[1];
   const int start_pos = item[2];
@@ -547,7 +547,8 @@ hipError_t launch_bq_attention(const int32_t* image, int num_items, int num_unit
                                              num_kv, kv_stride, geom, stream);
     if (err != hipSuccess) return err;
   } else if (num_items > 0) {
-    dim3 grid(num_items, (num_kv + 3) / 4);
+    // kv-head groups of an item side by side, as in the bf16 decode.
+    dim3 grid((num_kv + 3) / 4, num_items);
     if (geom.row_mask + 1 >= kTile)
       hipLaunchKernelGGL((bq_partial_kernel<2, true>), grid, dim3(256), 0, stream, image,
                          static_cast<const int8_t*>(q_i8), qi_bias, f_q,
