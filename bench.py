@@ -145,6 +145,11 @@ class DecodeBf16:
 
     dtype = "bf16"
     phases = ("append", "partials", "merge")
+    # The timed step: the append, then the attention as the host calls it
+    # (ifr_attention_bf16: the partials and the merge in one call, as
+    # dispatch_full_attention / dispatch_sliding_attention).
+    timed_phases = ("append", "attention")
+    graph = True
     dominant = "flash_partial_bf16_kernel<256,2>"
 
     def __init__(self, config: int, seed: int):
@@ -297,6 +302,10 @@ class DecodeBf16:
                                         self.sin, num_q=self.nq, num_kv=self.nkv,
                                         half=self.half, pair_stride=self.pair,
                                         head_dim=self.hd)
+        elif phase == "attention":
+            A.attention_bf16(p, self.q, kc, vc, self.out, self.partials, self.ps,
+                             num_q=self.nq, num_kv=self.nkv, head_dim=self.hd,
+                             kv_stride=self.kvs)
         elif phase == "partials":
             A.flash_partials_bf16(p, self.q, kc, vc, self.partials, self.ps,
                                   num_q=self.nq, num_kv=self.nkv, head_dim=self.hd,
@@ -384,6 +393,7 @@ class DecodeBq:
 
     dtype = "int8 KV (f32 scales), f32 accumulate"
     phases = ("append", "attention")
+    graph = True
     dominant = "bq_partial_kernel<2> + merge_kernel<256>"
 
     def __init__(self, config: int, seed: int):
@@ -1399,13 +1409,20 @@ class GatherBench:
                 "sample": f"the first {n} rows, one thread, median of {len(times)}"}
 
 
-def measure(w, steps: int, warmup: int):
+def measure(w, steps: int, warmup: int, graph: bool):
+    """Returns the wall time of K eager steps, of K steps replayed from a HIP
+    graph (None unless graph), and per-phase HIP-event times."""
     import torch
 
     stream = w.stream
-    for _ in range(warmup):
-        for ph in w.phases:
+    timed = getattr(w, "timed_phases", w.phases)
+
+    def step():
+        for ph in timed:
             w.launch(ph)
+
+    for _ in range(warmup):
+        step()
     torch.cuda.synchronize()
     # Past the W warmup steps, keep stepping (untimed) until at least 0.2 s of
     # work has run, so that a step of a few microseconds (config 1) is timed
@@ -1413,17 +1430,34 @@ def measure(w, steps: int, warmup: int):
     t_warm = time.perf_counter()
     while time.perf_counter() - t_warm < 0.2:
         for _ in range(8):
-            for ph in w.phases:
-                w.launch(ph)
+            step()
         torch.cuda.synchronize()
-    # Timed region 1: wall clock over K steps, nothing but the step's launches.
+    # Timed region 1: wall clock over K steps, nothing but the step's launches
+    # (each a C-ABI call from Python).
     t0 = time.perf_counter()
     for _ in range(steps):
-        for ph in w.phases:
-            w.launch(ph)
+        step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # Timed region 2: the same K steps with HIP events between the kernels.
+    # Timed region 2: the same K steps captured once in a HIP graph (the same
+    # C-ABI calls, recorded on torch's capture stream) and replayed: the GPU
+    # time of the step without the host's per-launch cost, as a serving loop
+    # that captures a layer's decode runs it.
+    wall_graph = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(steps):
+                step()
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        wall_graph = time.perf_counter() - t0
+        del g
+    # Timed region 3: K steps phase by phase with HIP events between them.
     n = len(w.phases)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
     torch.cuda.synchronize()
@@ -1436,7 +1470,7 @@ def measure(w, steps: int, warmup: int):
     per = {ph: statistics.mean(e[j].elapsed_time(e[j + 1]) * 1e3 for e in evs)
            for j, ph in enumerate(w.phases)}
     per["step"] = statistics.mean(e[0].elapsed_time(e[n]) * 1e3 for e in evs)
-    return wall, per
+    return wall, wall_graph, per
 
 
 def copy_calibration(dev) -> None:
@@ -1474,6 +1508,10 @@ def main() -> None:
     ap.add_argument("--oquant", choices=("none", "separate", "fused"), default="none",
                     help="config 5: int8 block quant of the attention output for o_proj, "
                          "as its own pass or fused into the merge")
+    ap.add_argument("--launch", choices=("graph", "eager"), default="graph",
+                    help="decode configs: time the K steps replayed from a HIP graph "
+                         "(default; the eager per-call figure is reported beside it) or "
+                         "as eager C-ABI calls")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="one 1 GiB device-to-device copy (torch's copy kernel): the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -1508,7 +1546,9 @@ def main() -> None:
         w = DecodeBf16(a.config, a.seed)
     w.setup(dev, a)
     torch.cuda.synchronize()
-    wall, per = measure(w, a.steps, a.warmup)
+    use_graph = a.launch == "graph" and getattr(w, "graph", False)
+    wall_eager, wall_graph, per = measure(w, a.steps, a.warmup, use_graph)
+    wall = wall_graph if use_graph else wall_eager
     ms_per_step = wall / a.steps * 1e3
     value = w.step_bytes() / (wall / a.steps) / 1e9
     dom_us = per[getattr(w, "dominant_phase", "partials" if "partials" in per else "attention")]
@@ -1542,6 +1582,9 @@ def main() -> None:
         "config": w.config(),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "us_per_layer": round(ms_per_step * 1e3, 2),
+        "launch": ("hip graph: the K steps' C-ABI calls captured once and replayed"
+                   if use_graph else "eager C-ABI calls from Python"),
+        "eager_us_per_layer": round(wall_eager / a.steps * 1e6, 2),
         "us_breakdown_events": {k: round(v, 2) for k, v in per.items()},
         "step_bytes": w.step_bytes(),
         "roofline": roof,

@@ -16,8 +16,13 @@ from .kv import FULL, SLIDING, AttentionPlan, KVRunTable, flash_partial_stride
 
 
 def _stream() -> int:
+    """The current HIP stream of the current device (torch's capture stream
+    under graph capture), as the raw handle the C ABI takes."""
     import torch
 
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return int(raw(torch.cuda.current_device()))
     return int(torch.cuda.current_stream().cuda_stream)
 
 

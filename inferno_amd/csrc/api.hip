@@ -288,7 +288,9 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
     it[3] = static_cast<int32_t>(start);
     it[4] = static_cast<int32_t>(end);
     it[5] = static_cast<int32_t>(stripe);
-    it[6] = 0;
+    // The run's row table as a word offset into the image, so a kernel
+    // reaches its pages in two dependent loads (item, rows).
+    it[6] = hdr[kHdrOffRows] + runs[4 * run + 2];
     it[7] = 0;
     ++n_items;
   };

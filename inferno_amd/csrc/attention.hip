@@ -81,7 +81,7 @@ __device__ __forceinline__ uint2 load_kv(const uint2* p) {
   return make_uint2(v.x, v.y);
 }
 
-template <int D, int G, bool kTwoPages>
+template <int D, int G, bool kTwoPages, bool kShort>
 __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
     const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
@@ -99,13 +99,11 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
 
   const int32_t* item = image + image[kHdrOffItems] + blockIdx.y * kItemWords;
   const int q_row = item[0];
-  const int run = item[1];
   const int start_pos = item[2];
   const int start = item[3];
   const int end = item[4];
   const int stripe = item[5];
-  const int32_t* rows =
-      image + image[kHdrOffRows] + image[image[kHdrOffRuns] + run * 4 + 2];
+  const int32_t* rows = image + item[kItemRowsOff];
 
   const int tk = lane >> 3;
   const int c = lane & 7;
@@ -121,7 +119,9 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
   }
 
   const uint16_t* kh = kc + static_cast<int64_t>(g) * D + 8 * c;
-  const uint16_t* vh = vc + static_cast<int64_t>(g) * D + DPL * lane;
+  // V rows are wave-uniform (one position per load): a scalar row base plus
+  // the lane's byte offset, so the loads need no per-lane address registers.
+  const uint16_t* vg = vc + static_cast<int64_t>(g) * D;
 
   float m[G], l[G], acc[G][DPL];
 #pragma unroll
@@ -134,12 +134,10 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
 
   // Loads of one tile: K for the two passes of 8 positions (lane's position
   // tk and tk + 8) and V for all 16 positions (wave-uniform slots).
-  uint4 kbuf[2][NCH];
-  VT vbuf[kTile];
   // kTwoPages (pages of >= 16 positions): a tile spans at most two pages,
   // whose rows come from two scalar loads, so no K/V load waits behind a
   // page-table vector load (vmcnt counts in order).
-  auto load_tile = [&](int pos0) {
+  auto load_tile = [&](uint4 (&kbuf)[2][NCH], VT (&vbuf)[kTile], int pos0) {
     const int tile_len = min(kTile, end - pos0);
     const int p0 = start_pos + pos0;
     const int pg0 = p0 >> shift;
@@ -168,20 +166,36 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
       for (int i = 0; i < NCH; ++i)
         kbuf[b][i] = load_kv(reinterpret_cast<const uint4*>(kr + 64 * i));
     }
+    if constexpr (kTwoPages) {
+      // The rows of a page are consecutive: byte offsets of the tile's first
+      // row in page A and of page B's row 0 less the positions left in page
+      // A, each stepped by one row per position.  A position past the tile
+      // reads a row of the same two pages (within the first 16 rows of page
+      // B, or of page A when the tile ends in it); its value is skipped.
+      const int in_a = row_mask + 1 - (p0 & row_mask);
+      const int64_t row_bytes = kv_stride * 2;
+      int64_t oa = (ra + (p0 & row_mask)) * row_bytes;
+      int64_t ob = (rb - in_a) * row_bytes;
+      const char* vgb = reinterpret_cast<const char*>(vg);
 #pragma unroll
-    for (int t = 0; t < kTile; ++t) {
-      const int64_t slot = slot_of(p0 + (t < tile_len ? t : 0));
-      vbuf[t] = load_kv(reinterpret_cast<const VT*>(vh + slot * kv_stride));
+      for (int t = 0; t < kTile; ++t) {
+        vbuf[t] = load_kv(reinterpret_cast<const VT*>(vgb + (t < in_a ? oa : ob)) + lane);
+        oa += row_bytes;
+        ob += row_bytes;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kTile; ++t) {
+        const int64_t slot = slot_of(p0 + (t < tile_len ? t : 0));
+        vbuf[t] = load_kv(reinterpret_cast<const VT*>(vg + slot * kv_stride) + lane);
+      }
     }
     // Keep the V loads ahead of the score math: one memory round trip a tile.
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  for (int pos0 = start; pos0 < end; pos0 += kTile) {
+  auto process = [&](const uint4 (&kv4s)[2][NCH], const VT (&vv)[kTile], int pos0) {
     const int tile_len = min(kTile, end - pos0);
-    load_tile(pos0);
-    uint4 (&kv4s)[2][NCH] = kbuf;
-    VT (&vv)[kTile] = vbuf;
 
     // ---- scores for the tile's 16 positions (two passes of 8) ----
     float s[2][G];
@@ -242,6 +256,32 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
 #pragma unroll
           for (int r = 0; r < G; ++r) acc[r][e] = fmaf(vf[e], wr[r], acc[r][e]);
       }
+    }
+    };
+
+  uint4 kbuf[2][NCH];
+  VT vbuf[kTile];
+  const int n_tiles = (end - start + kTile - 1) / kTile;
+  if (kShort && n_tiles <= 3) {
+    // Items of at most three tiles (one sequence over many splits, about
+    // one wave per SIMD): straight-line code with the loads of the first two
+    // tiles issued together and the third's issued while the second is
+    // processed.  Every load is unconditional (a missing tile rereads the
+    // previous one, never used), so each wait covers only older loads.
+    uint4 kbuf2[2][NCH];
+    VT vbuf2[kTile];
+    const int p1 = n_tiles > 1 ? start + kTile : start;
+    const int p2 = n_tiles > 2 ? start + 2 * kTile : p1;
+    load_tile(kbuf, vbuf, start);
+    load_tile(kbuf2, vbuf2, p1);
+    process(kbuf, vbuf, start);
+    load_tile(kbuf, vbuf, p2);
+    if (n_tiles > 1) process(kbuf2, vbuf2, p1);
+    if (n_tiles > 2) process(kbuf, vbuf, p2);
+  } else {
+    for (int pos0 = start; pos0 < end; pos0 += kTile) {
+      load_tile(kbuf, vbuf, pos0);
+      process(kbuf, vbuf, pos0);
     }
   }
 
@@ -422,81 +462,23 @@ __global__ __launch_bounds__(256) void merge_kernel(
   }
 }
 
-// The sliced merge of one (head, dim) over n <= 64 * kChunks splits with
-// every load of the unit issued at once (m and l of the lane's splits, the
-// lane's dim of all n splits), then the operations of the chunked path in
-// merge_sliced_kernel in the same order: global max, per 64-split chunk the
-// corrections and the halving-tree sums of L in batches of 16, and the acc
-// chain over the splits in order.
-template <int kChunks>
-__device__ __forceinline__ void merge_sliced_direct(const float* base, int64_t partial_stride,
-                                                    int m_off, int l_off, int h, int D, int dim,
-                                                    int lane, int n, float& acc, float& inv_l,
-                                                    bool& live) {
-  float mv[kChunks], lv[kChunks];
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    mv[c] = kNegBig;
-    lv[c] = 0.0f;
-    if (64 * c + lane < n) {
-      const float* sp = base + static_cast<int64_t>(64 * c + lane) * partial_stride;
-      mv[c] = sp[m_off + h];
-      lv[c] = sp[l_off + h];
-    }
-  }
-  float src[64 * kChunks];
-  const float* col = base + static_cast<int64_t>(h) * D + dim;
-#pragma unroll
-  for (int u = 0; u < 64 * kChunks; ++u)
-    src[u] = col[static_cast<int64_t>(min(u, n - 1)) * partial_stride];
-  float gm = kNegBig;
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    const float sm = wave_max_ref(mv[c]);
-    gm = max_ref(gm, sm);
-  }
-  float gl = 0.0f;
-  bool first = true;
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    const float delta = 64 * c + lane < n ? mv[c] - gm : kNegBig;
-    float cv = fexp(max_ref(-87.0f, delta));
-    cv = lv[c] > 0.0f ? cv : 0.0f;
-    float prod = lv[c] * cv;
-    prod = tree16_sum(prod);
-    const int cnt = min(64, n - 64 * c);
-    for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
-#pragma unroll
-    for (int u = 0; u < 64; ++u) {
-      const float cu = u < cnt ? readlane_f32(cv, u) : 0.0f;  // cv is 0 past n
-      if (cu <= 0.0f) continue;
-      if (first) {
-        acc = src[64 * c + u] * cu;
-        first = false;
-      } else {
-        acc = fmaf(src[64 * c + u], cu, acc);
-      }
-    }
-  }
-  if (gl > 0.0f) {
-    live = true;
-    inv_l = 1.0f / gl;
-  }
-}
-
+// The merge for units with many splits (single-sequence decode): a block
+// owns one (unit, q head, 64-dim slice), a lane one dim.  The four waves
+// load 32 splits each of every 128-split group into LDS, so a wave has at
+// most 34 loads in flight and the group costs one memory round trip; wave 0
+// then runs the operations of merge_kernel in the same order: the global
+// max, per 64-split chunk the corrections and the halving-tree sums of L in
+// batches of 16, and the acc chain over the splits in order.
 template <int D>
-__global__ __launch_bounds__(256) void merge_sliced_kernel(
+__global__ __launch_bounds__(256) void merge_staged_kernel(
     const int32_t* __restrict__ image, const float* __restrict__ partials,
-    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int mode,
-    int direct_n) {
-  // The same merge with the head's dims spread over D/64 waves (blockIdx.z
-  // picks a 64-dim slice, a lane owns one dim): for units with many splits,
-  // whose acc chain is long, this puts D/64 times more waves on the loads.
-  constexpr int kAhead = 32;  // split loads in flight ahead of the fma chain
+    uint16_t* __restrict__ out, int64_t partial_stride, int num_q, int direct_n) {
+  constexpr int kGroup = 128;  // splits staged per round, 32 per wave
+  __shared__ float stage[kGroup][64];
+  __shared__ float coef[64];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * 4 + wave;
-  if (h >= num_q) return;
+  const int h = blockIdx.y;
   const int dim = 64 * blockIdx.z + lane;
   // direct_n > 0: one output row 0 over stripes [0, direct_n), no plan image.
   int out_row = 0, stripe_base = 0, n = direct_n;
@@ -509,85 +491,94 @@ __global__ __launch_bounds__(256) void merge_sliced_kernel(
   const float* base = partials + static_cast<int64_t>(stripe_base) * partial_stride;
   const int m_off = num_q * D;
   const int l_off = m_off + num_q;
-  float acc = 0.0f;
-  float inv_l = 0.0f;
-  bool live = false;
+  const float* col = base + static_cast<int64_t>(h) * D + dim;
 
-  if (mode == 1) {
-    const float lv = base[l_off + h];
-    if (lv > 0.0f) {
-      live = true;
-      inv_l = 1.0f / lv;
-      acc = base[static_cast<int64_t>(h) * D + dim];
-    }
-  } else if (n > 0 && n <= 64) {
-    merge_sliced_direct<1>(base, partial_stride, m_off, l_off, h, D, dim, lane, n, acc, inv_l,
-                           live);
-  } else if (n > 0 && n <= 128) {
-    merge_sliced_direct<2>(base, partial_stride, m_off, l_off, h, D, dim, lane, n, acc, inv_l,
-                           live);
-  } else {
-    // Lanes own splits.  Global max: wave max per 64-split chunk (exact in any
-    // order).  Corrections and L: the reference sums the splits in batches
-    // of 16, each batch by the halving tree (lane ^ 8, ^ 4, ^ 2, ^ 1 inside
-    // 16-lane groups), batches in order.  acc: the splits in order, loads
-    // issued kAhead at a time ahead of the fma chain.
-    float gm = kNegBig;
+  float gm = kNegBig;
+  if (wave == 0 && n > kGroup) {
     for (int s0 = 0; s0 < n; s0 += 64) {
       float sm = kNegBig;
       if (s0 + lane < n)
         sm = base[static_cast<int64_t>(s0 + lane) * partial_stride + m_off + h];
-      sm = wave_max_ref(sm);
-      gm = max_ref(gm, sm);
-    }
-    float gl = 0.0f;
-    bool first = true;
-    for (int s0 = 0; s0 < n; s0 += 64) {
-      float delta = kNegBig, ls = 0.0f;
-      if (s0 + lane < n) {
-        const float* sp = base + static_cast<int64_t>(s0 + lane) * partial_stride;
-        delta = sp[m_off + h] - gm;
-        ls = sp[l_off + h];
-      }
-      float cv = fexp(max_ref(-87.0f, delta));
-      cv = ls > 0.0f ? cv : 0.0f;
-      float prod = ls * cv;
-      prod = tree16_sum(prod);
-      const int cnt = min(64, n - s0);
-      for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
-      for (int j = 0; j < cnt; j += kAhead) {
-        float src[kAhead];
-        float cs[kAhead];
-#pragma unroll
-        for (int u = 0; u < kAhead; ++u) {
-          cs[u] = 0.0f;
-          src[u] = 0.0f;
-          if (j + u < cnt) {
-            cs[u] = readlane_f32(cv, j + u);
-            src[u] = base[static_cast<int64_t>(s0 + j + u) * partial_stride +
-                          static_cast<int64_t>(h) * D + dim];
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kAhead; ++u) {
-          if (cs[u] <= 0.0f) continue;
-          if (first) {
-            acc = src[u] * cs[u];
-            first = false;
-          } else {
-            acc = fmaf(src[u], cs[u], acc);
-          }
-        }
-      }
-    }
-    if (gl > 0.0f) {
-      live = true;
-      inv_l = 1.0f / gl;
+      gm = max_ref(gm, wave_max_ref(sm));
     }
   }
-
-  uint16_t* dst = out + (static_cast<int64_t>(out_row) * num_q + h) * D + dim;
-  *dst = static_cast<uint16_t>(live ? f32_to_bf16_bits(acc * inv_l) : 0u);
+  float acc = 0.0f, gl = 0.0f;
+  bool first = true;
+  for (int g0 = 0; g0 < n; g0 += kGroup) {
+    // All 32 loads issue before the first LDS write (a split past n rereads
+    // split n - 1; the chain never uses it).
+    float ld[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      ld[j] = col[static_cast<int64_t>(min(g0 + 32 * wave + j, n - 1)) * partial_stride];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) stage[32 * wave + j][lane] = ld[j];
+    float mv[2], lv[2];
+    if (wave == 0) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int sp = g0 + 64 * c + lane;
+        mv[c] = kNegBig;
+        lv[c] = 0.0f;
+        if (sp < n) {
+          const float* p = base + static_cast<int64_t>(sp) * partial_stride;
+          mv[c] = p[m_off + h];
+          lv[c] = p[l_off + h];
+        }
+      }
+      if (n <= kGroup) gm = max_ref(wave_max_ref(mv[0]), wave_max_ref(mv[1]));
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int c0 = g0 + 64 * c;
+        if (c0 >= n) break;
+        const float delta = c0 + lane < n ? mv[c] - gm : kNegBig;
+        float cv = fexp(max_ref(-87.0f, delta));
+        cv = lv[c] > 0.0f ? cv : 0.0f;
+        float prod = lv[c] * cv;
+        prod = tree16_sum(prod);
+        const int cnt = min(64, n - c0);
+        for (int b = 0; b * 16 < cnt; ++b) gl = gl + readlane_f32(prod, 16 * b);
+        float x[64];
+#pragma unroll
+        for (int u = 0; u < 64; ++u) x[u] = stage[64 * c + u][lane];
+        if (cnt == 64 && __builtin_amdgcn_ballot_w64(cv > 0.0f) == ~0ull) {
+          // Every split of the chunk live (the normal case): the same
+          // operations as below without a test per split, the corrections
+          // broadcast from LDS so that each step waits only on the last fma.
+          coef[lane] = cv;
+          float cb[64];
+#pragma unroll
+          for (int u = 0; u < 64; ++u) cb[u] = coef[u];
+          acc = first ? x[0] * cb[0] : fmaf(x[0], cb[0], acc);
+          first = false;
+#pragma unroll
+          for (int u = 1; u < 64; ++u) acc = fmaf(x[u], cb[u], acc);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 64; ++u) {
+            const float cu = u < cnt ? readlane_f32(cv, u) : 0.0f;  // cv is 0 past n
+            if (cu <= 0.0f) continue;
+            if (first) {
+              acc = x[u] * cu;
+              first = false;
+            } else {
+              acc = fmaf(x[u], cu, acc);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+    const bool live = gl > 0.0f;
+    const float inv_l = live ? 1.0f / gl : 0.0f;
+    uint16_t* dst = out + (static_cast<int64_t>(out_row) * num_q + h) * D + dim;
+    *dst = static_cast<uint16_t>(live ? f32_to_bf16_bits(acc * inv_l) : 0u);
+  }
 }
 
 template <int D, int G>
@@ -602,15 +593,19 @@ hipError_t launch_partials(const int32_t* image, int num_items, const void* q,
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint16_t*>(k);
   const auto* vp = static_cast<const uint16_t*>(v);
-  if (geom.row_mask + 1 >= kTile) {
-    hipLaunchKernelGGL((flash_partial_bf16_kernel<D, G, true>), grid,
-                       dim3(64 * kDecodeWaves), 0, stream, image, qp, kp, vp, partials, ps,
-                       num_q, num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
-  } else {
-    hipLaunchKernelGGL((flash_partial_bf16_kernel<D, G, false>), grid,
-                       dim3(64 * kDecodeWaves), 0, stream, image, qp, kp, vp, partials, ps,
-                       num_q, num_kv, kv_stride, geom.shift, geom.row_mask, geom.page_mask);
-  }
+  // Grids of at most one wave per SIMD (256 CUs x 4 SIMDs) take the
+  // straight-line path for short items; larger grids keep 4 waves per SIMD.
+  const bool small = static_cast<int64_t>(grid.x) * grid.y * kDecodeWaves <= 1024;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * kDecodeWaves), 0, stream, image, qp, kp, vp,
+                       partials, ps, num_q, num_kv, kv_stride, geom.shift, geom.row_mask,
+                       geom.page_mask);
+  };
+  const bool two_pages = geom.row_mask + 1 >= kTile;
+  if (two_pages && small) go(flash_partial_bf16_kernel<D, G, true, true>);
+  else if (two_pages) go(flash_partial_bf16_kernel<D, G, true, false>);
+  else if (small) go(flash_partial_bf16_kernel<D, G, false, true>);
+  else go(flash_partial_bf16_kernel<D, G, false, false>);
   return hipGetLastError();
 }
 
@@ -624,9 +619,9 @@ bool attention_shape_supported(int head_dim, int gqa) {
 hipError_t launch_merge_stripes(const float* partials, void* output, int64_t ps,
                                 int n_stripes, int num_q, hipStream_t stream) {
   if (n_stripes <= 0) return hipSuccess;
-  dim3 grid(1, (num_q + 3) / 4, 128 / 64);
-  hipLaunchKernelGGL(merge_sliced_kernel<128>, grid, dim3(256), 0, stream, nullptr, partials,
-                     static_cast<uint16_t*>(output), ps, num_q, 0, n_stripes);
+  dim3 grid(1, num_q, 128 / 64);
+  hipLaunchKernelGGL(merge_staged_kernel<128>, grid, dim3(256), 0, stream, nullptr, partials,
+                     static_cast<uint16_t*>(output), ps, num_q, n_stripes);
   return hipGetLastError();
 }
 
@@ -635,28 +630,29 @@ hipError_t launch_merge(const int32_t* image, int num_units, int num_stripes, in
                         int num_q, int head_dim, hipStream_t stream, int8_t* q_out,
                         float* q_scale) {
   if (num_units <= 0) return hipSuccess;
-  // Measured on MI355X: a unit with 64 splits merges in half the time with
-  // one dim per lane over D/64 waves; with 8-16 splits per unit (batched
-  // decode) the one-wave-per-head kernel is faster.  The fused int8 epilogue
-  // needs a whole head per wave.
-  const bool sliced = mode != 1 && num_stripes >= 32 * num_units && q_out == nullptr;
-  dim3 grid(num_units, (num_q + 3) / 4, sliced ? head_dim / 64 : 1);
+  // Measured on MI355X: units with many splits (single-sequence decode)
+  // merge fastest staged through LDS by one block per (unit, head, 64-dim
+  // slice); with 8-16 splits per unit (batched decode) the one-wave-per-head
+  // kernel is faster.  The fused int8 epilogue needs a whole head per wave.
+  const bool staged = mode != 1 && num_stripes >= 32 * num_units && q_out == nullptr;
   uint16_t* o = static_cast<uint16_t*>(output);
-  if (head_dim == 256) {
-    if (sliced)
-      hipLaunchKernelGGL(merge_sliced_kernel<256>, grid, dim3(256), 0, stream, image,
-                         partials, o, ps, num_q, mode, 0);
+  if (staged) {
+    dim3 grid(num_units, num_q, head_dim / 64);
+    if (head_dim == 256)
+      hipLaunchKernelGGL(merge_staged_kernel<256>, grid, dim3(256), 0, stream, image,
+                         partials, o, ps, num_q, 0);
     else
-      hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image, partials, o,
-                         ps, num_q, mode, q_out, q_scale);
-  } else {
-    if (sliced)
-      hipLaunchKernelGGL(merge_sliced_kernel<512>, grid, dim3(256), 0, stream, image,
-                         partials, o, ps, num_q, mode, 0);
-    else
-      hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image, partials, o,
-                         ps, num_q, mode, q_out, q_scale);
+      hipLaunchKernelGGL(merge_staged_kernel<512>, grid, dim3(256), 0, stream, image,
+                         partials, o, ps, num_q, 0);
+    return hipGetLastError();
   }
+  dim3 grid(num_units, (num_q + 3) / 4, 1);
+  if (head_dim == 256)
+    hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(256), 0, stream, image, partials, o, ps,
+                       num_q, mode, q_out, q_scale);
+  else
+    hipLaunchKernelGGL(merge_kernel<512>, grid, dim3(256), 0, stream, image, partials, o, ps,
+                       num_q, mode, q_out, q_scale);
   return hipGetLastError();
 }
 

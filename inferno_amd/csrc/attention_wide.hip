@@ -106,13 +106,11 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   const int g = blockIdx.x;
   const int32_t* item = image + sload(image + kHdrOffItems) + blockIdx.y * kItemWords;
   const int q_row = sload(item);
-  const int run = sload(item + 1);
   const int start_pos = sload(item + 2);
   const int start = sload(item + 3);
   const int end = sload(item + 4);
   const int stripe = sload(item + 5);
-  const int32_t* rows = image + sload(image + kHdrOffRows) +
-                        sload(image + sload(image + kHdrOffRuns) + run * 4 + 2);
+  const int32_t* rows = image + sload(item + kItemRowsOff);
 
   const int r16 = lane & 15;
   const int qd = lane >> 4;

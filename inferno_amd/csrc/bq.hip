@@ -328,13 +328,11 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
   if (g >= num_kv) return;
   const int32_t* item = image + image[kHdrOffItems] + blockIdx.y * kItemWords;
   const int q_row = item[0];
-  const int run = item[1];
   const int start_pos = item[2];
   const int start = item[3];
   const int end = item[4];
   const int stripe = item[5];
-  const int32_t* rows =
-      image + image[kHdrOffRows] + image[image[kHdrOffRuns] + run * 4 + 2];
+  const int32_t* rows = image + item[kItemRowsOff];
   const float inv127 = 1.0f / 127.0f;
   const float inv127sq = inv127 * inv127;
 

@@ -31,7 +31,9 @@ enum PlanHeader : int {
   kHdrWords = 16
 };
 // A work item: one contiguous position range of one run, for every kv head.
-// {q_row, run, start_pos, start, end, stripe, 0, 0}
+// {q_row, run, start_pos, start, end, stripe, rows_off, 0}; rows_off is the
+// image word offset of the run's row table.
+constexpr int kItemRowsOff = 6;
 constexpr int kItemWords = 8;
 // A merge unit: one output token row, for every q head.
 // {out_row, stripe_base, n_stripes, 0}

@@ -131,7 +131,7 @@ def _bf16_attention(case, seq_len, cap, seed):
 def test_full_layer_decode(cap):
     """Batched decode over ragged contexts: cap 1 gives one split per
     sequence seeded then capped, 16 a few splits per unit (merge_kernel), 256
-    and 1024 tens to a hundred (merge_sliced_kernel), 4096 a split per tile."""
+    and 1024 tens to a hundred (merge_staged_kernel), 4096 a split per tile."""
     announce(f"full layer decode cap={cap}")
     rng = np.random.default_rng(100 + cap)
     ctx = [int(x) for x in rng.integers(1, 3000, 6)] + [0, 15, 16, 17]

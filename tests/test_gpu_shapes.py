@@ -1,7 +1,8 @@
 """GPU parity of the bf16 decode and token-partitioned prefill routes for the
 other head shapes the kernels are built for: head_dim 256 and 512, GQA 1 and
-2, and head_dim 512 with GQA 8 (attention_shape_supported).  Both merge kernels are reached: a unit of 32
-or more splits takes merge_sliced_kernel, fewer take merge_kernel.  Outputs
+2, and head_dim 512 with GQA 8 (attention_shape_supported).  Both merge
+kernels are reached: a unit of 32 or more splits takes merge_staged_kernel
+(more than 128 splits: several staging rounds), fewer take merge_kernel.  Outputs
 are within 1e-2 max-abs of the oracle (one bf16 spacing where |x| >= 2)."""
 import numpy as np
 import pytest
@@ -54,8 +55,8 @@ def _check(kind, runs, rows, cache_rows, seq_len, shape, cap, seed, window=0,
 def test_batched_decode_shapes(shape, cap):
     """cap is the worker count of the split plan: 16 workers over 5
     sequences give 1-5 splits a unit (merge_kernel), 256 about 50 and 1024
-    about 115 (merge_sliced_kernel, all loads in one go), 4096 up to one
-    split per 16-position tile."""
+    about 115 (merge_staged_kernel, one staging round), 4096 up to one
+    split per 16-position tile (several rounds)."""
     announce(f"decode shape={shape} cap={cap}")
     rng = np.random.default_rng(sum(shape) + cap)
     ctx = [int(x) for x in rng.integers(700, 3000, 5)]
