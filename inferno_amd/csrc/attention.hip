@@ -119,9 +119,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
   }
 
   const uint16_t* kh = kc + static_cast<int64_t>(g) * D + 8 * c;
-  // V rows are wave-uniform (one position per load): a scalar row base plus
-  // the lane's byte offset, so the loads need no per-lane address registers.
-  const uint16_t* vg = vc + static_cast<int64_t>(g) * D;
+  const uint16_t* vg = vc + static_cast<int64_t>(g) * D;  // + lane's dims at load
 
   float m[G], l[G], acc[G][DPL];
 #pragma unroll
@@ -166,29 +164,10 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
       for (int i = 0; i < NCH; ++i)
         kbuf[b][i] = load_kv(reinterpret_cast<const uint4*>(kr + 64 * i));
     }
-    if constexpr (kTwoPages) {
-      // The rows of a page are consecutive: byte offsets of the tile's first
-      // row in page A and of page B's row 0 less the positions left in page
-      // A, each stepped by one row per position.  A position past the tile
-      // reads a row of the same two pages (within the first 16 rows of page
-      // B, or of page A when the tile ends in it); its value is skipped.
-      const int in_a = row_mask + 1 - (p0 & row_mask);
-      const int64_t row_bytes = kv_stride * 2;
-      int64_t oa = (ra + (p0 & row_mask)) * row_bytes;
-      int64_t ob = (rb - in_a) * row_bytes;
-      const char* vgb = reinterpret_cast<const char*>(vg);
 #pragma unroll
-      for (int t = 0; t < kTile; ++t) {
-        vbuf[t] = load_kv(reinterpret_cast<const VT*>(vgb + (t < in_a ? oa : ob)) + lane);
-        oa += row_bytes;
-        ob += row_bytes;
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < kTile; ++t) {
-        const int64_t slot = slot_of(p0 + (t < tile_len ? t : 0));
-        vbuf[t] = load_kv(reinterpret_cast<const VT*>(vg + slot * kv_stride) + lane);
-      }
+    for (int t = 0; t < kTile; ++t) {
+      const int64_t slot = slot_of(p0 + (t < tile_len ? t : 0));
+      vbuf[t] = load_kv(reinterpret_cast<const VT*>(vg + slot * kv_stride) + lane);
     }
     // Keep the V loads ahead of the score math: one memory round trip a tile.
     __builtin_amdgcn_sched_barrier(0);
