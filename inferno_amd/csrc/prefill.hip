@@ -43,8 +43,6 @@
 // staged in LDS first.
 // Blocks are numbered kv-head-fastest so every block of a kv head lands on
 // one XCD (block id mod 8) and shares that XCD's L2.
-#include <type_traits>
-
 #include "common.hpp"
 #include "launch.hpp"
 #include "prefill_common.hpp"
@@ -168,25 +166,31 @@ void prefill_full_mfma_kernel(
   };
   // The same for an iteration whose kStageRows rows per wave all lie below
   // count_max and inside one page (pages of >= 16 rows): one page lookup, a
-  // wave-uniform 64-bit base and 32-bit row offsets.
+  // wave-uniform row base and per-lane byte offsets fixed for the kernel.
+  // Row rr = 2i + half of the wave's rows sits rr * kv_stride * 2 bytes past
+  // the base, i.e. i * 4 * kv_stride (uniform) + hk (lane); its K chunk
+  // row ^ rr = (row ^ half) ^ 2i gives the byte offset x16 ^ 32i, its V
+  // chunk row ^ 2*(rr & 3) one of two lane constants (i even or odd).
+  const int hk = half * static_cast<int>(kv_stride) * 2;
+  const uint32_t x16 = 16u * static_cast<uint32_t>(row ^ half);
+  const uint32_t hv0 = static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(row ^ (2 * half));
+  const uint32_t hv1 =
+      static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(row ^ (4 + 2 * half));
   auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
     const int key0 = it * kKeys + wave * kStageRows;  // wave-uniform
     const int prow = __builtin_amdgcn_readfirstlane(page_rows[key0 >> shift]);
     const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
-    const uint16_t* kb = kbase + slot0 * kv_stride;
-    const uint16_t* vb = vbase + slot0 * kv_stride;
-    const int stride = static_cast<int>(kv_stride);
+    const char* kb = reinterpret_cast<const char*>(kbase + slot0 * kv_stride);
+    const char* vb = reinterpret_cast<const char*>(vbase + slot0 * kv_stride);
+    const int64_t step = 4 * kv_stride;  // bytes from row pair i to i + 1
 #pragma unroll
     for (int i = 0; i < kStageRows / 2; ++i) {
-      const int rr = 2 * i + half;  // row within the wave's rows (r & 15 == rr)
-      const int roff = rr * stride;
       const int lds_row = wave * kStageRows + 2 * i;  // wave-uniform
-      __builtin_amdgcn_global_load_lds(
-          kb + roff + 8 * (row ^ rr),
-          (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          vb + roff + 8 * (row ^ (2 * (rr & 3))),
-          (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+      const uint32_t ko = static_cast<uint32_t>(hk) + (x16 ^ (32u * i));
+      __builtin_amdgcn_global_load_lds(kb + i * step + ko,
+                                       (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb + i * step + ((i & 1) ? hv1 : hv0),
+                                       (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
     }
   };
   // V rows of keys >= count_max in this wave's staged rows become zeros
@@ -401,9 +405,9 @@ void prefill_full_mfma_kernel(
   // The next iteration's rows are staged unconditionally (past the last
   // iteration they are clamped, in-bounds rows of an unused buffer), so the
   // staging shares a block with the score MFMAs.
-  auto full_iteration = [&](auto page_stage, int it, const uint8_t* kl, const uint8_t* vl,
+  auto full_iteration = [&](bool page_stage, int it, const uint8_t* kl, const uint8_t* vl,
                             uint8_t* knext, uint8_t* vnext) {
-    if (decltype(page_stage)::value)
+    if (page_stage)  // block-uniform
       stage_page(it + 1, knext, vnext);
     else
       stage(it + 1, knext, vnext);
@@ -446,18 +450,12 @@ void prefill_full_mfma_kernel(
   const int block_min = ntok == kPTokens ? base_pos + (t0 - buf_start) + 1 : 0;
   const int it_full = min(n_iters, block_min / kKeys) & ~1;
   int it = 0;
-  // Iteration it + 1 < it_full has every row below count_max, so with pages
-  // of >= 16 rows the first of a pair stages through stage_page.
-  if (shift >= 4) {
-    for (; it < it_full; it += 2) {
-      full_iteration(std::true_type{}, it, kbuf0, vbuf0, kbuf1, vbuf1);
-      full_iteration(std::false_type{}, it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
-    }
-  } else {
-    for (; it < it_full; it += 2) {
-      full_iteration(std::false_type{}, it, kbuf0, vbuf0, kbuf1, vbuf1);
-      full_iteration(std::false_type{}, it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
-    }
+  // A staged iteration below it_full has every row below count_max, so with
+  // pages of >= 16 rows it stages through stage_page.
+  const bool pages16 = shift >= 4;
+  for (; it < it_full; it += 2) {
+    full_iteration(pages16, it, kbuf0, vbuf0, kbuf1, vbuf1);
+    full_iteration(pages16 && it + 2 < it_full, it + 1, kbuf1, vbuf1, kbuf0, vbuf0);
   }
   for (; it < n_iters; ++it) {
     if (it & 1)
