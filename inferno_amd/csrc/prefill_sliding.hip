@@ -213,6 +213,62 @@ void prefill_sliding_mfma_kernel(
       }
     }
   };
+  // The same for an iteration whose keys all lie in [k_lo, p_last] (pages
+  // of >= 16 rows): iterations start at multiples of 64 keys, so a wave's
+  // kStageRows rows sit in one page, reached by one lookup; the per-lane
+  // byte offsets are fixed for the kernel.  bf16: row rr = 2i + half at
+  // i * 4 * kv_stride + hk bytes, K chunk (row ^ half) ^ 2i, V chunk one of
+  // two lane constants.  bq: row rr = 4i + lr (lr = lane / 16) at
+  // i * 4 * kv_stride + lr * kv_stride bytes, K chunk (c ^ lr) ^ 4i.
+  const int lr = lane >> 4;
+  const int cq = lane & 15;
+  const uint32_t hk = kBq ? static_cast<uint32_t>(lr * static_cast<int>(kv_stride))
+                          : static_cast<uint32_t>(half * static_cast<int>(kv_stride) * 2);
+  const uint32_t kx = kBq ? 16u * static_cast<uint32_t>(cq ^ lr)
+                          : 16u * static_cast<uint32_t>(row ^ half);
+  const uint32_t hv0 = kBq ? hk + 16u * static_cast<uint32_t>(cq)
+                           : hk + 16u * static_cast<uint32_t>(row ^ (2 * half));
+  const uint32_t hv1 = hk + 16u * static_cast<uint32_t>(row ^ (4 + 2 * half));
+  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst, int buf) {
+    const int key0 = kb0 + it * kKeys + wave * kStageRows;  // wave-uniform
+    const int prow = __builtin_amdgcn_readfirstlane(page_rows[(key0 >> shift) & page_mask]);
+    const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+    if constexpr (kBq) {
+      const char* kb = reinterpret_cast<const char*>(kbase8 + slot0 * kv_stride);
+      const char* vb = reinterpret_cast<const char*>(vbase8 + slot0 * kv_stride);
+      const int64_t step = 4 * kv_stride;
+#pragma unroll
+      for (int i = 0; i < kStageRows / 4; ++i) {
+        __builtin_amdgcn_global_load_lds(
+            kb + i * step + (hk + (kx ^ (64u * i))),
+            (lds_void_t*)(kdst + (wave * kStageRows + 4 * i) * kBqRowBytes), 16, 0, 0);
+        vcodes[i] = *reinterpret_cast<const uint4*>(vb + i * step + hv0);
+      }
+      if (wave == 0) {
+        const int key = kb0 + it * kKeys + lane;
+        const int64_t si = slot_of(key) * num_kv + g;
+        __builtin_amdgcn_global_load_lds(k_scale + si, (lds_void_t*)(&kscl[buf][0]), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(v_scale + si, (lds_void_t*)(&vscl[buf][0]), 4, 0, 0);
+      }
+    } else {
+      const char* kb = reinterpret_cast<const char*>(kbase + slot0 * kv_stride);
+      const char* vb = reinterpret_cast<const char*>(vbase + slot0 * kv_stride);
+      const int64_t step = 4 * kv_stride;
+#pragma unroll
+      for (int i = 0; i < kStageRows / 2; ++i) {
+        const int lds_row = wave * kStageRows + 2 * i;  // wave-uniform
+        __builtin_amdgcn_global_load_lds(kb + i * step + (hk + (kx ^ (32u * i))),
+                                         (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb + i * step + ((i & 1) ? hv1 : hv0),
+                                         (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+      }
+    }
+  };
+  // Iteration it's keys all in [k_lo, p_last] with pages of >= 16 rows.
+  auto interior = [&](int it) {
+    const int first = kb0 + it * kKeys;
+    return shift >= 4 && first >= k_lo && first + kKeys <= p_last + 1;  // block-uniform
+  };
   // After the wave's loads have landed: bf16 keeps the staged V rows and
   // zeroes those outside [k_lo, p_last]; bq writes its V codes as bf16 (the
   // bf16 swizzle: 16-byte chunk c of row rr at c ^ 2*(rr & 3)), zeros for
@@ -477,7 +533,12 @@ void prefill_sliding_mfma_kernel(
     // tile); it is read before that buffer is restaged.
     step(tb, st, vn, 48, it > 0, nb);
     __syncthreads();
-    if (it + 1 < n_iters) stage(it + 1, kn, vn, nb);
+    if (it + 1 < n_iters) {
+      if (interior(it + 1))
+        stage_page(it + 1, kn, vn, nb);
+      else
+        stage(it + 1, kn, vn, nb);
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s0[8 + i];
     step(tb + 1, st, vl, 0, true, cb);
