@@ -527,9 +527,36 @@ void prefill_wide_mfma_kernel(
   // An iteration whose keys are valid for every row of the block.  The
   // next iteration's rows are staged unconditionally (past the last
   // iteration they are clamped, in-bounds rows of an unused buffer).
+  // bf16: the staging of an iteration whose keys all lie below count_max,
+  // with pages of >= 8 rows: a wave's kWStageRows rows (a multiple of 8 from
+  // the iteration's start) sit in one page, reached by one lookup.  (Int8
+  // keeps the per-row lookups: its forms of this spill or measured slower.)
+  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+    const int key0 = it * kWKeys + wave * kWStageRows;  // wave-uniform
+    const int prow = __builtin_amdgcn_readfirstlane(page_rows[key0 >> shift]);
+    const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+    const uint8_t* krow0 = reinterpret_cast<const uint8_t*>(kbase + slot0 * kv_stride);
+    const uint8_t* vrow0 = reinterpret_cast<const uint8_t*>(vbase + slot0 * kv_stride);
+    const int64_t row_bytes = 2 * kv_stride;
+#pragma unroll
+    for (int i = 0; i < kWStageRows; ++i) {
+      const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
+      const uint32_t lk =
+          static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
+      const uint32_t lv =
+          static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+      __builtin_amdgcn_global_load_lds(krow0 + i * row_bytes + lk,
+                                       (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vrow0 + i * row_bytes + lv,
+                                       (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
+    }
+  };
   auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                             uint8_t* vnext) {
-    stage(it + 1, knext, vnext, (it + 1) & 1);
+    if (!kBq && shift >= 3 && (it + 2) * kWKeys <= count_max)  // block-uniform
+      stage_page(it + 1, knext, vnext);
+    else
+      stage(it + 1, knext, vnext, (it + 1) & 1);
     float w[2][8], corr[2];
     bool big[2];
     const f32x16_t s = exchange(qk(kl), it & 1);
