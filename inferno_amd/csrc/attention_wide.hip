@@ -41,6 +41,7 @@ namespace {
 constexpr int kWD = 512;                // head_dim
 constexpr int kWG = 8;                  // q heads per kv head
 constexpr int kWQPitch = 2 * kWD + 16;  // bytes per staged bf16 q row in LDS
+constexpr int kWQPitchBq = kWD + 16;    // bytes per staged int8 q row in LDS
 
 typedef __bf16 wbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float wf32x4_t __attribute__((ext_vector_type(4)));
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   constexpr int kSteps = Tile::kSteps;
   constexpr int kVB = kRow / 64;  // value bytes per lane per position
   using VT = typename Tile::VT;
-  __shared__ __align__(16) uint8_t qs[kBq ? 16 : kWG * kWQPitch];
+  __shared__ __align__(16) uint8_t qs[kWG * (kBq ? kWQPitchBq : kWQPitch)];
 
   const int lane = threadIdx.x;
   const int g = blockIdx.x;
@@ -118,19 +119,29 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   const int64_t qh = static_cast<int64_t>(q_row) * num_q + g * kWG + hq;
 
   // ---- the B operand of the scores ----
-  uint4 qv[kBq ? kSteps : 1];
+  // Both kinds stage the group's 8 q rows in LDS (lane (head lane/8, chunks
+  // lane%8 + 8i) copies 16 bytes at a time), so the operands take no
+  // registers across the tile loop; each score MFMA reads its 16 bytes.
   int qsum128 = 0;
   float qbias = 0.0f, fq = 0.0f;
   if constexpr (kBq) {
-    const uint8_t* qp = q + qh * kWD + 16 * qd;
+    const uint8_t* qg = q + (static_cast<int64_t>(q_row) * num_q + g * kWG) * kWD;
+    const int sh = lane >> 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = (lane & 7) + 8 * i;
+      *reinterpret_cast<uint4*>(qs + sh * kWQPitchBq + 16 * c) =
+          *reinterpret_cast<const uint4*>(qg + sh * kWD + 16 * c);
+    }
+    __syncthreads();
     int qs4 = 0;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      qv[s] = *reinterpret_cast<const uint4*>(qp + 64 * s);
-      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].x), 0x01010101, qs4, false);
-      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].y), 0x01010101, qs4, false);
-      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].z), 0x01010101, qs4, false);
-      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qv[s].w), 0x01010101, qs4, false);
+      const uint4 qc = *reinterpret_cast<const uint4*>(qs + hq * kWQPitchBq + 64 * s + 16 * qd);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qc.x), 0x01010101, qs4, false);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qc.y), 0x01010101, qs4, false);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qc.z), 0x01010101, qs4, false);
+      qs4 = __builtin_amdgcn_sdot4(static_cast<int>(qc.w), 0x01010101, qs4, false);
     }
     // The four lane groups hold disjoint quarters of the head's codes.
     qs4 = qs4 + __shfl_xor(qs4, 16);
@@ -139,8 +150,6 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     qbias = qi_bias[qh];
     fq = f_q[qh];
   } else {
-    // Stage the group's 8 q rows in LDS; lane (head lane/8, chunks lane%8 +
-    // 8i) copies 16 bytes at a time.
     const uint8_t* qg = q + (static_cast<int64_t>(q_row) * num_q + g * kWG) * (2 * kWD);
     const int sh = lane >> 3;
 #pragma unroll
@@ -221,10 +230,13 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     if constexpr (kBq) {
       wi32x4_t si = {0, 0, 0, 0};
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s)
+      for (int s = 0; s < kSteps; ++s) {
+        const uint4 qf =
+            *reinterpret_cast<const uint4*>(qs + hq * kWQPitchBq + 64 * s + 16 * qd);
         si = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(wi32x4_t, d.k[s]),
-                                                    __builtin_bit_cast(wi32x4_t, qv[s]), si,
+                                                    __builtin_bit_cast(wi32x4_t, qf), si,
                                                     0, 0, 0);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float sc = static_cast<float>(si[j] + qsum128) - qbias;
