@@ -152,3 +152,134 @@ def test_graph_replays_bq_attention():
             assert np.array_equal(from_dev(out, np.uint16), want), f"replay {r} differs"
             print(f"  replay {r}: bit-exact", flush=True)
         del g
+
+
+@pytest.mark.parametrize("nq,nkv,d,half,pair", [(16, 8, 256, 128, 128), (16, 2, 512, 64, 256)])
+def test_graph_replays_bq_prep_and_attention(nq, nkv, d, half, pair):
+    """The butterquant decode step as bench.py captures it for its int8 decode
+    workloads (16q/8kv x 256 and 16q/2kv x 512): the quantising append (ifr_bq_attn_prep: RMS norm, RoPE, FWHT, int8 codes of
+    q, k, v) and the int8 attention, at both layer shapes.  Every replay's
+    outputs, query codes and cache codes/scales equal the eager step's."""
+    import torch
+
+    announce(f"graph bq prep + attention {nq}q/{nkv}kv x {d}")
+    ctx = [3000, 700, 12000, 64]
+    B = len(ctx)
+    case = make_decode_case(61 + d, ctx)
+    rows_n = case.pool_pages * 64
+    kvs = nkv * d
+    plan = AttentionPlan(_table(case.runs, case.base_rows), B, kind=FULL, window=0,
+                         cache_size=64, page_len=64, cache_rows=rows_n, cap=64,
+                         kv_row_bytes=kvs, device=torch.device("cuda"))
+    q_src = to_dev(seeded_bf16(B * nq * d, 11))
+    k_src = to_dev(seeded_bf16(B * kvs, 12))
+    v_src = to_dev(seeded_bf16(B * kvs, 13))
+    norm_q, norm_k = to_dev(seeded_bf16(d, 14)), to_dev(seeded_bf16(d, 15))
+    cos, sin = _rope(max(ctx) + 2, 16)
+    rng = np.random.default_rng(17)
+    kc0 = to_dev(rng.integers(-127, 128, rows_n * kvs).astype(np.int8))
+    vc0 = to_dev(rng.integers(-127, 128, rows_n * kvs).astype(np.int8))
+    ks0 = to_dev(rng.uniform(0.5, 1.5, rows_n * nkv).astype(np.float32))
+    vs0 = to_dev(rng.uniform(0.5, 2.0, rows_n * nkv).astype(np.float32))
+    kc, vc, ks, vs = kc0.clone(), vc0.clone(), ks0.clone(), vs0.clone()
+    q_i8 = empty_dev(B * nq * d, np.int8)
+    qb, fq = empty_dev(B * nq, np.float32), empty_dev(B * nq, np.float32)
+    out = empty_dev(B * nq * d, np.uint16)
+    partials, ps = A.partials_buffer(plan, nq, d)
+
+    def step():
+        A.dispatch_bq_attn_prep(plan, q_src, k_src, v_src, norm_q, norm_k, q_i8, qb, fq, kc, ks,
+                                vc, vs, cos, sin, num_q=nq, num_kv=nkv, head_dim=d,
+                                rope_half=half, pair_stride=pair,
+                                sqrt_n=float(np.sqrt(np.float32(d))),
+                                n_eps=float(np.float32(d) * np.float32(1e-6)))
+        A.bq_attention(plan, q_i8, qb, fq, kc, ks, vc, vs, out, partials, ps, num_q=nq,
+                       num_kv=nkv, head_dim=d, kv_stride=kvs)
+
+    def reset():
+        for t, t0 in ((kc, kc0), (vc, vc0), (ks, ks0), (vs, vs0)):
+            t.copy_(t0)
+        for t in (q_i8, qb, fq, out):
+            t.zero_()
+
+    def state():
+        return [from_dev(out, np.uint16), from_dev(q_i8, np.int8), from_dev(kc, np.int8),
+                from_dev(vc, np.int8), from_dev(ks, np.float32).view(np.uint32),
+                from_dev(vs, np.float32).view(np.uint32)]
+
+    step()
+    torch.cuda.synchronize()
+    want = state()
+    reset()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for r in range(REPLAYS):
+        reset()
+        A.bq_attention(plan, q_i8, qb, fq, kc0, ks0, vc0, vs0, empty_dev(B * nq * d, np.uint16),
+                       partials, ps, num_q=nq, num_kv=nkv, head_dim=d, kv_stride=kvs)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("output", "q codes", "k codes", "v codes", "k scales",
+                               "v scales"), state(), want):
+            assert np.array_equal(a, b), f"replay {r}: {name} differs from the eager step"
+        print(f"  replay {r}: bit-exact", flush=True)
+    del g
+
+
+def test_graph_replays_full_layer_decode_bf16():
+    """The bf16 decode step at Gemma-4's full-attention shape (16q/2kv x 512,
+    partial RoPE): the append and the wide-kernel attention, replayed."""
+    import torch
+
+    nq, nkv, d, half, pair = 16, 2, 512, 64, 256
+    kvs = nkv * d
+    announce("graph full-layer decode bf16")
+    ctx = [5000, 300, 16000, 2048, 77]
+    B = len(ctx)
+    case = make_decode_case(71, ctx)
+    rows_n = case.pool_pages * 64
+    plan = AttentionPlan(_table(case.runs, case.base_rows), B, kind=FULL, window=0,
+                         cache_size=64, page_len=64, cache_rows=rows_n, cap=128,
+                         kv_row_bytes=kvs * 2, device=torch.device("cuda"))
+    q0 = to_dev(seeded_bf16(B * nq * d, 21))
+    k0 = to_dev(seeded_bf16(rows_n * kvs, 22))
+    v0 = to_dev(seeded_bf16(rows_n * kvs, 23))
+    ks, vs = to_dev(seeded_bf16(B * kvs, 24)), to_dev(seeded_bf16(B * kvs, 25))
+    cos, sin = _rope(max(ctx) + 2, 26)
+    q, k, v = q0.clone(), k0.clone(), v0.clone()
+    out = empty_dev(B * nq * d, np.uint16)
+    partials, ps = A.partials_buffer(plan, nq, d)
+
+    def step():
+        A.dispatch_rope_cache_write(plan, q, ks, vs, k, v, cos, sin, num_q=nq, num_kv=nkv,
+                                    half=half, pair_stride=pair, head_dim=d)
+        A.attention_bf16(plan, q, k, v, out, partials, ps, num_q=nq, num_kv=nkv, head_dim=d,
+                         kv_stride=kvs)
+
+    def reset():
+        q.copy_(q0)
+        k.copy_(k0)
+        v.copy_(v0)
+        out.zero_()
+
+    step()
+    torch.cuda.synchronize()
+    want = [from_dev(t, np.uint16) for t in (out, q, k, v)]
+    reset()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for r in range(REPLAYS):
+        reset()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("output", "rotated q", "k cache", "v cache"),
+                              [from_dev(t, np.uint16) for t in (out, q, k, v)], want):
+            assert np.array_equal(a, b), f"replay {r}: {name} differs from the eager step"
+        print(f"  replay {r}: bit-exact", flush=True)
+    del g
