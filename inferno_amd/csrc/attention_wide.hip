@@ -30,6 +30,12 @@
 //           reference's per-element order; each weight reaches every lane with
 //           v_readlane.  The V row of a position (1 KiB bf16 or 512 B int8) is
 //           one load instruction.
+// Loads are software-pipelined in the tile's own registers (no second tile
+// buffer): the next tile's K loads are issued once the score MFMAs have read
+// K and run under the softmax and P.V; its V loads are issued after the P.V
+// and run under the next scores and softmax.  A wave thus always has about
+// one tile in flight (218-226 VGPRs for bf16, 181-189 for int8: two waves
+// per SIMD).
 #include <type_traits>
 
 #include "common.hpp"
@@ -174,34 +180,48 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
-  // One tile's loads, branch-free: a position past the tile reloads the
-  // tile's first row (its score is masked, its value skipped).  kTwoPages
-  // (pages of >= 16 positions): a tile spans at most two pages, whose rows
-  // come from two scalar loads.
-  auto load_tile = [&](int pos0, int tile_len) {
-    Tile d;
-    const int p0 = start_pos + pos0;
-    const int pg0 = p0 >> shift;
-    int64_t ra = 0, rb = 0;
+  // A tile's row lookups and loads, branch-free: a position past the tile
+  // reloads the tile's first row (its score is masked, its value skipped).
+  // kTwoPages (pages of >= 16 positions): a tile spans at most two pages,
+  // whose rows come from two scalar loads.
+  struct TileRows {
+    int p0, pg0, len;
+    int64_t ra, rb;
+  };
+  auto tile_rows = [&](int pos0) {
+    TileRows r;
+    r.p0 = start_pos + pos0;
+    r.pg0 = r.p0 >> shift;
+    r.len = min(kTile, end - pos0);
+    r.ra = r.rb = 0;
     if constexpr (kTwoPages) {
-      const int pg1 = (p0 + tile_len - 1) >> shift;
-      ra = sload(rows + (pg0 & page_mask));
-      rb = pg1 != pg0 ? sload(rows + (pg1 & page_mask)) : ra;
+      const int pg1 = (r.p0 + r.len - 1) >> shift;
+      r.ra = sload(rows + (r.pg0 & page_mask));
+      r.rb = pg1 != r.pg0 ? sload(rows + (pg1 & page_mask)) : r.ra;
     }
-    auto slot_of = [&](int t) -> int64_t {
-      const int p = p0 + (t < tile_len ? t : 0);
-      if constexpr (kTwoPages) {
-        return ((p >> shift) == pg0 ? ra : rb) + (p & row_mask);
-      } else {
-        return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
-      }
-    };
-    const uint8_t* kr = kh + slot_of(r16) * row_bytes;
+    return r;
+  };
+  auto slot_of = [&](const TileRows& r, int t) -> int64_t {
+    const int p = r.p0 + (t < r.len ? t : 0);
+    if constexpr (kTwoPages) {
+      return ((p >> shift) == r.pg0 ? r.ra : r.rb) + (p & row_mask);
+    } else {
+      return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+    }
+  };
+  auto load_k = [&](Tile& d, const TileRows& r) {
+    const uint8_t* kr = kh + slot_of(r, r16) * row_bytes;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) d.k[s] = wide_load16(kr + 64 * s);
+    if constexpr (kBq) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d.ks[j] = k_scale[slot_of(r, 4 * qd + j) * num_kv + g];
+    }
+  };
+  auto load_v = [&](Tile& d, const TileRows& r) {
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      const uint8_t* vr = vh + slot_of(t) * row_bytes;
+      const uint8_t* vr = vh + slot_of(r, t) * row_bytes;
       if constexpr (kBq) {
         d.v[t] = wide_load8(vr);
       } else {
@@ -210,20 +230,22 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     }
     if constexpr (kBq) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t sl = slot_of(4 * qd + j) * num_kv + g;
-        d.ks[j] = k_scale[sl];
-        d.vs[j] = v_scale[sl];
-      }
+      for (int j = 0; j < 4; ++j) d.vs[j] = v_scale[slot_of(r, 4 * qd + j) * num_kv + g];
     }
-    // Keep every load of the tile ahead of the math: one round trip a tile.
-    __builtin_amdgcn_sched_barrier(0);
-    return d;
   };
 
-  for (int pos0 = start; pos0 < end; pos0 += kTile) {
-    const int tile_len = min(kTile, end - pos0);
-    const Tile d = load_tile(pos0, tile_len);
+  Tile d;
+  // One tile: scores, online softmax, P.V.  kFlat: the P.V visits all
+  // kTile positions without branches, a position past the tile with weight
+  // 0 (its V row is the tile's first row, so fma(v, 0, acc) leaves acc as
+  // it is: the accumulators start at +0 and never become -0 by addition).
+  // Otherwise positions past the tile are skipped.  kNext: the loads of
+  // tile rn are issued into the tile's registers as soon as this tile is
+  // done with them (K after the score MFMAs, V after the P.V).
+  auto step = [&](auto flat_c, auto next_c, const TileRows& r, const TileRows& rn) {
+    constexpr bool kFlat = decltype(flat_c)::value;
+    constexpr bool kNext = decltype(next_c)::value;
+    const int tile_len = r.len;
 
     // ---- scores: lane holds positions 4*qd + j of head hq ----
     float sj[4];
@@ -257,6 +279,11 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) sj[j] = 4 * qd + j < tile_len ? sc[j] : kNegBig;
     }
+    if constexpr (kNext) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_k(d, rn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     // ---- online softmax of head hq (online_softmax_tile) ----
     float mx = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
@@ -282,6 +309,11 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
       }
     }
 
+    if constexpr (kFlat) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = 4 * qd + j < tile_len ? w[j] : 0.0f;
+    }
+
     // ---- scale_unrolled, then P.V in position order ----
 #pragma unroll
     for (int h = 0; h < kWG; ++h) {
@@ -291,7 +323,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     }
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      if (t < tile_len) {  // wave-uniform
+      if (kFlat || t < tile_len) {  // wave-uniform
         float vf[8];
         unpack8(d.v[t], vf);
 #pragma unroll
@@ -301,6 +333,40 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
           for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(vf[e], wt, acc[h][e]);
         }
       }
+      // One position at a time (unpacking every V row ahead of its FMAs
+      // would not fit the registers).
+      if constexpr (kFlat) __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (kNext) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_v(d, rn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const std::true_type yes{};
+  const std::false_type no{};
+
+  if (start < end) {
+    // Software-pipelined in the tile's own registers: the next tile's K
+    // loads run under this tile's softmax and P.V, its V loads under the
+    // next tile's scores and softmax.  The last tile loads itself again
+    // (in bounds, unused), so every iteration leaves the same loads in
+    // flight and the waits stay exact.
+    TileRows r = tile_rows(start);
+    load_k(d, r);
+    __builtin_amdgcn_sched_barrier(0);  // K before V, as in the loop
+    load_v(d, r);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int pos0 = start; pos0 < end; pos0 += kTile) {
+      const int nxt = pos0 + kTile;
+      const TileRows rn = nxt < end ? tile_rows(nxt) : r;
+      // bf16 with flat P.V; int8 skips positions past the tile (its
+      // outputs are compared bit for bit).
+      if constexpr (kBq)
+        step(no, yes, r, rn);
+      else
+        step(yes, yes, r, rn);
+      r = rn;
     }
   }
 

@@ -387,32 +387,42 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
     uint32_t v[kTile];
     float vs[kTile];
   };
-  auto load_tile = [&](int pos0) {
-    BqDecodeTile d;
-    const int tile_len = min(kTile, end - pos0);
-    const int p0 = start_pos + pos0;
-    const int pg0 = p0 >> shift;
-    int64_t ra = 0, rb = 0;
+  struct TileRows {
+    int p0, pg0, len;
+    int64_t ra, rb;
+  };
+  auto tile_rows = [&](int pos0) {
+    TileRows r;
+    r.p0 = start_pos + pos0;
+    r.pg0 = r.p0 >> shift;
+    r.len = min(kTile, end - pos0);
+    r.ra = r.rb = 0;
     if constexpr (kTwoPages) {
-      const int pg1 = (p0 + tile_len - 1) >> shift;
-      ra = sload(rows + (pg0 & page_mask));
-      rb = pg1 != pg0 ? sload(rows + (pg1 & page_mask)) : ra;
+      const int pg1 = (r.p0 + r.len - 1) >> shift;
+      r.ra = sload(rows + (r.pg0 & page_mask));
+      r.rb = pg1 != r.pg0 ? sload(rows + (pg1 & page_mask)) : r.ra;
     }
-    auto slot_of = [&](int p) -> int64_t {
-      if constexpr (kTwoPages) {
-        return ((p >> shift) == pg0 ? ra : rb) + (p & row_mask);
-      } else {
-        return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
-      }
-    };
-    const int64_t kslot = slot_of(p0 + min(tk, tile_len - 1));
+    return r;
+  };
+  auto slot_of = [&](const TileRows& r, int t) -> int64_t {
+    const int p = r.p0 + min(t, r.len - 1);
+    if constexpr (kTwoPages) {
+      return ((p >> shift) == r.pg0 ? r.ra : r.rb) + (p & row_mask);
+    } else {
+      return static_cast<int64_t>(rows[(p >> shift) & page_mask]) + (p & row_mask);
+    }
+  };
+  auto load_k = [&](BqDecodeTile& d, const TileRows& r) {
+    const int64_t kslot = slot_of(r, tk);
     const int8_t* kr = kh + kslot * kv_stride;
 #pragma unroll
     for (int i = 0; i < 4; ++i) d.k[i] = load_codes16(kr + 64 * i);
     d.ks = k_scale[kslot * num_kv + g];
+  };
+  auto load_v = [&](BqDecodeTile& d, const TileRows& r) {
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      const int64_t vslot = slot_of(p0 + min(t, tile_len - 1));
+      const int64_t vslot = slot_of(r, t);
       d.v[t] = load_codes4(vh + vslot * kv_stride);
       if constexpr (kTwoPages) {
         d.vs[t] = __int_as_float(sload(reinterpret_cast<const int32_t*>(v_scale) +
@@ -421,15 +431,27 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
         d.vs[t] = v_scale[vslot * num_kv + g];
       }
     }
-    return d;
   };
 
-  BqDecodeTile cur = load_tile(start);
+  // Software-pipelined in the tile's own registers: the next tile's key
+  // loads are issued once the scores have read this tile's keys and run
+  // under the softmax and P.V; its value loads are issued after the P.V and
+  // run under the next scores.  The loads are unconditional (past the
+  // item's last tile they reload that tile, in bounds and unused), so each
+  // wait covers only older loads.
+  BqDecodeTile cur;
+  TileRows rc = {0, 0, 0, 0, 0};
+  if (start < end) {
+    rc = tile_rows(start);
+    load_k(cur, rc);
+    __builtin_amdgcn_sched_barrier(0);  // keys before values, as in the loop
+    load_v(cur, rc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   for (int pos0 = start; pos0 < end; pos0 += kTile) {
-    const int tile_len = min(kTile, end - pos0);
+    const int tile_len = rc.len;
     const bool valid = tk < tile_len;
-    BqDecodeTile nxt;
-    if (pos0 + kTile < end) nxt = load_tile(pos0 + kTile);  // wave-uniform
+    const TileRows rn = pos0 + kTile < end ? tile_rows(pos0 + kTile) : rc;
     float s[G];
     {
       const float ks = cur.ks;
@@ -452,6 +474,9 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
         s[r] = valid ? sc : kNegBig;
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(cur, rn);
+    __builtin_amdgcn_sched_barrier(0);
 
     float w[G];
 #pragma unroll
@@ -490,7 +515,10 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
         }
       }
     }
-    cur = nxt;
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(cur, rn);
+    __builtin_amdgcn_sched_barrier(0);
+    rc = rn;
   }
 
   float* part = partials + static_cast<int64_t>(stripe) * partial_stride;
