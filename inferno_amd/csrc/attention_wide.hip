@@ -349,9 +349,10 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   if (start < end) {
     // Software-pipelined in the tile's own registers: the next tile's K
     // loads run under this tile's softmax and P.V, its V loads under the
-    // next tile's scores and softmax.  The last tile loads itself again
-    // (in bounds, unused), so every iteration leaves the same loads in
-    // flight and the waits stay exact.
+    // next tile's scores and softmax.  After the last tile the loads go on
+    // (in bounds, unused: all of them read the last tile's first row, which
+    // the caches hold), so every iteration leaves the same loads in flight
+    // and the waits stay exact.
     TileRows r = tile_rows(start);
     load_k(d, r);
     __builtin_amdgcn_sched_barrier(0);  // K before V, as in the loop
@@ -359,7 +360,11 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     __builtin_amdgcn_sched_barrier(0);
     for (int pos0 = start; pos0 < end; pos0 += kTile) {
       const int nxt = pos0 + kTile;
-      const TileRows rn = nxt < end ? tile_rows(nxt) : r;
+      TileRows rn = r;
+      if (nxt < end)
+        rn = tile_rows(nxt);
+      else
+        rn.len = 1;  // every load of the dummy tile reads the last tile's first row
       // bf16 with flat P.V; int8 skips positions past the tile (its
       // outputs are compared bit for bit).
       if constexpr (kBq)

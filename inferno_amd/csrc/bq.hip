@@ -436,9 +436,9 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
   // Software-pipelined in the tile's own registers: the next tile's key
   // loads are issued once the scores have read this tile's keys and run
   // under the softmax and P.V; its value loads are issued after the P.V and
-  // run under the next scores.  The loads are unconditional (past the
-  // item's last tile they reload that tile, in bounds and unused), so each
-  // wait covers only older loads.
+  // run under the next scores.  The loads are unconditional (after the
+  // item's last tile they all read that tile's first row, in bounds, cached
+  // and unused), so each wait covers only older loads.
   BqDecodeTile cur;
   TileRows rc = {0, 0, 0, 0, 0};
   if (start < end) {
@@ -451,7 +451,11 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
   for (int pos0 = start; pos0 < end; pos0 += kTile) {
     const int tile_len = rc.len;
     const bool valid = tk < tile_len;
-    const TileRows rn = pos0 + kTile < end ? tile_rows(pos0 + kTile) : rc;
+    TileRows rn = rc;
+    if (pos0 + kTile < end)
+      rn = tile_rows(pos0 + kTile);
+    else
+      rn.len = 1;  // every load of the dummy tile reads the last tile's first row
     float s[G];
     {
       const float ks = cur.ks;
