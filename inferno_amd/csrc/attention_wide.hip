@@ -326,12 +326,16 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
       if (kFlat || t < tile_len) {  // wave-uniform
         float vf[8];
         unpack8(d.v[t], vf);
+        // The position's 8 weights first, then its 64 FMAs: a v_readlane
+        // result read by the very next VALU instruction costs wait states.
+        float wt[kWG];
 #pragma unroll
-        for (int h = 0; h < kWG; ++h) {
-          const float wt = readlane_f32(w[t & 3], h + 16 * (t >> 2));
+        for (int h = 0; h < kWG; ++h) wt[h] = readlane_f32(w[t & 3], h + 16 * (t >> 2));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(vf[e], wt, acc[h][e]);
-        }
+        for (int h = 0; h < kWG; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(vf[e], wt[h], acc[h][e]);
       }
       // One position at a time (unpacking every V row ahead of its FMAs
       // would not fit the registers).

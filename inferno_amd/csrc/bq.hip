@@ -504,6 +504,14 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
       for (int e = 0; e < 4; ++e) acc[r][e] = acc[r][e] * corr;
     }
 
+    // Every position's weights first: a v_readlane result read by the very
+    // next VALU instruction costs wait states.
+    float wtl[kTile][G];
+#pragma unroll
+    for (int t = 0; t < kTile; ++t)
+#pragma unroll
+      for (int r = 0; r < G; ++r) wtl[t][r] = readlane_f32(w[r], 4 * t);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
       if (t < tile_len) {  // wave-uniform
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(256) void bq_partial_kernel(
         unpack_i8x4(cur.v[t], vf);
 #pragma unroll
         for (int r = 0; r < G; ++r) {
-          const float wt = readlane_f32(w[r], 4 * t);
+          const float wt = wtl[t][r];
           const float a = wt * cur.vs[t];
           const float wts = a * inv127;
 #pragma unroll
