@@ -3,8 +3,10 @@
 // attention (bq_process_kv_tile / BqFlashAttentionKernel, :27-167), whose
 // partials feed the shared log-sum-exp merge.
 //
-// Prep, one wave per head (D = 256 or 512, lane L owns elements EPL*L ..
-// EPL*L + EPL - 1, EPL = D/64):
+// Prep (bq_prep_rows_kernel: 16 lanes per head, four heads per wave, for the
+// Gemma-4 layer shapes; bq_prep_kernel below, one wave per head, for any
+// other RoPE split).  One wave per head (D = 256 or 512, lane L owns elements
+// EPL*L .. EPL*L + EPL - 1, EPL = D/64):
 //   RMS     the reference's lane-wise chain over 16 AVX-512 lanes
 //           (butterquant/head_prep.mojo:9-16) is replayed exactly: lane
 //           j < 16 runs ssq_j = x_j^2, then fma(x_{16ri+j}, x_{16ri+j}, ssq_j)
@@ -292,6 +294,198 @@ __global__ __launch_bounds__(256) void bq_prep_kernel(
   }
 }
 
+// The same prep with 16 lanes per head and four heads per wave: lane j of a
+// head's 16-lane row owns elements 16*i + j (i < E = D/16), so
+//   RMS     lane j's chain over elements 16*i + j is the reference's register
+//           chain of SIMD lane j, in the lane's own registers, and the 16
+//           partial sums take the xor 8, 4, 2, 1 tree of bq_prep_kernel;
+//   RoPE    the partner of element 16*i + j (pair_stride away, a multiple of
+//           16) is the lane's own element i + pair_stride/16;
+//   FWHT    strides 1 .. 8 are DPP lane exchanges inside the row and strides
+//           16 .. D/2 pairs of the lane's registers, in the reference's stage
+//           order with the same operand pairs;
+//   absmax  lane max, then the row's xor 1 .. 8 exchanges.
+// Every instruction serves four heads, about half the VALU work per head of
+// one wave per head.  The int8 codes go to LDS byte by byte and leave as
+// 16-byte rows.  Needs (num_q + 2 num_kv) % 4 == 0; a row's lanes share one
+// head, so the q/k-only steps branch per row.  RoPE's rope_half and
+// pair_stride are template constants (kRopeHalf, kPairStride: multiples of 16).
+template <int D, int kRopeHalf, int kPairStride>
+__global__ __launch_bounds__(512) void bq_prep_rows_kernel(
+    const int32_t* __restrict__ image, const uint16_t* __restrict__ q_src,
+    const uint16_t* __restrict__ k_src, const uint16_t* __restrict__ v_src,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
+    int8_t* __restrict__ q_i8, float* __restrict__ qi_bias,
+    float* __restrict__ f_q, int8_t* __restrict__ k_cache,
+    float* __restrict__ k_scale, int8_t* __restrict__ v_cache,
+    float* __restrict__ v_scale, const float* __restrict__ cos_table,
+    const float* __restrict__ sin_table, int num_q, int num_kv, int shift,
+    int row_mask, int page_mask, int rope_half, int pair_stride, float sqrt_n,
+    float n_eps) {
+  constexpr int E = D / 16;
+  constexpr int kMaxWaves = 512 / 64;
+  __shared__ __align__(16) uint8_t cbuf[kMaxWaves][4 * D];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15;
+  const int tok = blockIdx.x;
+  const int run = image[image[kHdrOffTokRun] + tok];
+  const int32_t* rp = image + image[kHdrOffRuns] + run * 4;
+  const int pos = rp[1] + (tok - rp[0]);
+  const int32_t* rows = image + image[kHdrOffRows] + rp[2];
+  const float* cos_row = cos_table + static_cast<int64_t>(pos) * rope_half;
+  const float* sin_row = sin_table + static_cast<int64_t>(pos) * rope_half;
+  const int64_t slot =
+      static_cast<int64_t>(rows[(pos >> shift) & page_mask]) + (pos & row_mask);
+  const int64_t kv_stride = static_cast<int64_t>(num_kv) * D;
+  const float inv_sqrt_n = 1.0f / sqrt_n;
+
+  // Head of a 16-lane row: q heads, then k heads, then v heads.
+  auto head_of = [&](int hh, bool& is_q, bool& is_k) {
+    is_q = hh < num_q;
+    is_k = !is_q && hh < num_q + num_kv;
+    return is_q ? hh : (is_k ? hh - num_q : hh - num_q - num_kv);
+  };
+  bool is_q, is_k;
+  const int hh = 4 * wave + (lane >> 4);
+  const int h = head_of(hh, is_q, is_k);
+  const uint16_t* src =
+      (is_q ? q_src + (static_cast<int64_t>(tok) * num_q + h) * D
+            : (is_k ? k_src : v_src) + (static_cast<int64_t>(tok) * num_kv + h) * D) + j;
+  float r[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) r[i] = bf16_to_f32(src[16 * i]);
+
+  if (is_q || is_k) {  // uniform over the row
+    // head_inv_rms: the chain of SIMD lane j, then the 16-lane tree.
+    float ssq = r[0] * r[0];
+#pragma unroll
+    for (int i = 1; i < E; ++i) ssq = fmaf(r[i], r[i], ssq);
+    ssq = ssq + xor_lane_f32<8>(ssq, lane);
+    ssq = ssq + xor_lane_f32<4>(ssq, lane);
+    ssq = ssq + xor_lane_f32<2>(ssq, lane);
+    ssq = ssq + xor_lane_f32<1>(ssq, lane);
+    const float inv_rms = sqrt_n / sqrtf(ssq + n_eps);
+    const uint16_t* gamma = (is_q ? q_norm : k_norm) + j;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const float g = bf16_to_f32(gamma[16 * i]);
+      const float t = r[i] * inv_rms;
+      r[i] = t * g;
+    }
+    // RoPE pairs (e, pair_stride + e), e < rope_half: element 16*i + j with
+    // i < rope_half/16 and its partner i + pair_stride/16, both this lane's.
+    constexpr int kNr = kRopeHalf / 16, kPs = kPairStride / 16;
+    static_assert(kRopeHalf % 16 == 0 && kPairStride % 16 == 0 && kNr <= kPs &&
+                      kPs + kNr <= E,
+                  "RoPE pairs inside the head");
+#pragma unroll
+    for (int i = 0; i < kNr; ++i) {
+      const float lo = r[i], hi = r[i + kPs];
+      const float cv = cos_row[16 * i + j], sv = sin_row[16 * i + j];
+      const float a = lo * cv, b = hi * sv;
+      const float c = hi * cv, d = lo * sv;
+      r[i] = a - b;
+      r[i + kPs] = c + d;
+    }
+  }
+
+  // fwht_apply: strides 1 .. 8 across the row's lanes (the lower lane of a
+  // pair takes a + b, the upper a - b, a the lower lane's value), strides
+  // 16 .. D/2 inside the lane.  fma(+-1, own, partner) is that sum or
+  // difference with its single rounding, one instruction for both halves.
+  // x[lane ^ 4] is taken as (x[lane ^ 7])[lane ^ 3]: two DPP moves.
+  auto stage = [&](auto mc) {
+    constexpr int m = decltype(mc)::value;
+    const float sg = (lane & m) != 0 ? -1.0f : 1.0f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      float p;
+      if constexpr (m == 4) {
+        p = dpp_f32<kDppQuadReverse>(dpp_f32<kDppHalfMirror>(r[i]));
+      } else {
+        p = xor_lane_f32<m>(r[i], lane);
+      }
+      r[i] = __builtin_fmaf(sg, r[i], p);
+    }
+  };
+  stage(std::integral_constant<int, 1>{});
+  stage(std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 8>{});
+#pragma unroll
+  for (int st = 1; st < E; st <<= 1) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if (i & st) continue;
+      const float a = r[i], b = r[i + st];
+      r[i] = a + b;
+      r[i + st] = a - b;
+    }
+  }
+  const float sc = static_cast<float>(1.0 / static_cast<double>(sqrtf(static_cast<float>(D))));
+#pragma unroll
+  for (int i = 0; i < E; ++i) r[i] = r[i] * sc;
+
+  // absmax_quantize over the row.
+  float vmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const float a = fabsf(r[i]);
+    vmax = a > vmax ? a : vmax;
+  }
+  {
+    float o = xor_lane_f32<1>(vmax, lane);
+    vmax = o > vmax ? o : vmax;
+    o = xor_lane_f32<2>(vmax, lane);
+    vmax = o > vmax ? o : vmax;
+    o = xor_lane_f32<4>(vmax, lane);
+    vmax = o > vmax ? o : vmax;
+    o = xor_lane_f32<8>(vmax, lane);
+    vmax = o > vmax ? o : vmax;
+  }
+  float amax = vmax;
+  if (amax < 1e-10f) amax = 1e-10f;
+  const float inv = 127.0f / amax;
+  uint8_t* crow = &cbuf[wave][(lane >> 4) * D + j];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    // clamp(roundeven(x * 127/amax), -128, 127) as one med3 (finite x).
+    const float v = __builtin_amdgcn_fmed3f(rintf(r[i] * inv), -128.0f, 127.0f);
+    const int qi = static_cast<int>(v);
+    s += qi;
+    crow[16 * i] = static_cast<uint8_t>(qi & 0xFF);
+  }
+  s = s + xor_lane_i32<1>(s, lane);
+  s = s + xor_lane_i32<2>(s, lane);
+  s = s + xor_lane_i32<4>(s, lane);
+  s = s + xor_lane_i32<8>(s, lane);
+  if (j == 0) {
+    if (is_q) {
+      qi_bias[static_cast<int64_t>(tok) * num_q + h] = static_cast<float>(s) * 128.0f;
+      f_q[static_cast<int64_t>(tok) * num_q + h] = amax * inv_sqrt_n;
+    } else if (is_k) {
+      k_scale[slot * num_kv + h] = amax;
+    } else {
+      v_scale[slot * num_kv + h] = amax;
+    }
+  }
+  // The wave's 4 rows of codes leave LDS 16 bytes per lane (the wave's own
+  // LDS bytes: its writes land before its reads).
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+#pragma unroll
+  for (int c = lane; c < 4 * D / 16; c += 64) {
+    bool cq, ck;
+    const int ch = head_of(4 * wave + c / (D / 16), cq, ck);
+    const int off = 16 * (c % (D / 16));
+    int8_t* dst = cq ? q_i8 + (static_cast<int64_t>(tok) * num_q + ch) * D
+                     : (ck ? k_cache : v_cache) + slot * kv_stride + ch * D;
+    *reinterpret_cast<uint4*>(dst + off) =
+        *reinterpret_cast<const uint4*>(&cbuf[wave][16 * c]);
+  }
+}
+
 typedef unsigned int bq_u32x4_t __attribute__((ext_vector_type(4)));
 
 // Codes are streamed once per step: non-temporal loads, as for the bf16
@@ -560,6 +754,25 @@ hipError_t launch_bq_attn_prep(const int32_t* image, int seq_len, const void* q_
                                int pair_stride, float sqrt_n, float n_eps,
                                hipStream_t stream) {
   if (seq_len <= 0) return hipSuccess;
+  const int n_heads = num_q + 2 * num_kv;
+  const bool rows_form = n_heads % 4 == 0 && n_heads / 4 <= 8 &&
+                         ((head_dim == 256 && rope_half == 128 && pair_stride == 128) ||
+                          (head_dim == 512 && rope_half == 64 && pair_stride == 256));
+  if (rows_form) {
+    auto kernel = head_dim == 512 ? bq_prep_rows_kernel<512, 64, 256>
+                                  : bq_prep_rows_kernel<256, 128, 128>;
+    hipLaunchKernelGGL(kernel, dim3(seq_len), dim3(16 * n_heads), 0, stream, image,
+                       static_cast<const uint16_t*>(q_src),
+                       static_cast<const uint16_t*>(k_src),
+                       static_cast<const uint16_t*>(v_src),
+                       static_cast<const uint16_t*>(q_norm),
+                       static_cast<const uint16_t*>(k_norm), static_cast<int8_t*>(q_i8),
+                       qi_bias, f_q, static_cast<int8_t*>(k_cache), k_scale,
+                       static_cast<int8_t*>(v_cache), v_scale, cos_table, sin_table, num_q,
+                       num_kv, geom.shift, geom.row_mask, geom.page_mask, rope_half,
+                       pair_stride, sqrt_n, n_eps);
+    return hipGetLastError();
+  }
   auto kernel = head_dim == 512 ? bq_prep_kernel<8> : bq_prep_kernel<4>;
   hipLaunchKernelGGL(kernel, dim3(seq_len), dim3(256), 0, stream, image,
                      static_cast<const uint16_t*>(q_src), static_cast<const uint16_t*>(k_src),

@@ -111,6 +111,7 @@ __device__ __forceinline__ int dpp_i32(int v) {
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8 lanes
+constexpr int kDppQuadReverse = 0x1B;  // quad_perm [3,2,1,0]: lane i <- i ^ 3
 constexpr int kDppRowRor8 = 0x128;     // lane i <- (i-8)%16 = lane i ^ 8 within 16 lanes
 
 __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {

@@ -132,10 +132,13 @@ def test_reference_parity_schedule():
     assert worst_ref <= bq.TOL
 
 
-def test_prep_codes_bit_exact_with_rope_and_gains():
+@pytest.mark.parametrize("rope_half,pair_stride", [(128, 128), (64, 128)])
+def test_prep_codes_bit_exact_with_rope_and_gains(rope_half, pair_stride):
     """Non-identity RoPE tables and non-unit norm gains: q/k/v codes, q bias,
-    f_q and scales bit-exact against the oracle."""
-    announce("bq prep rope+gain")
+    f_q and scales bit-exact against the oracle.  (128, 128) runs the
+    16-lanes-per-head prep (bq_prep_rows_kernel), (64, 128) -- partial RoPE,
+    no template instance -- the one-wave-per-head bq_prep_kernel."""
+    announce(f"bq prep rope+gain half={rope_half} pair={pair_stride}")
     rng = np.random.default_rng(5)
     case = make_decode_case(7, [300, 1000, 64, 5])
     n = 4
@@ -150,7 +153,8 @@ def test_prep_codes_bit_exact_with_rope_and_gains():
     state = BqState(case.cache_rows)
     got, ref, *_ = _prep_and_attend(state, runs, rows, q, k, v, gq, gk, cos, sin, kind=FULL,
                                     window=0, cache_size=64, cache_rows=case.cache_rows,
-                                    cap=64, seq_len=n, rope_half=128, pair_stride=128)
+                                    cap=64, seq_len=n, rope_half=rope_half,
+                                    pair_stride=pair_stride)
     r = compare_bf16(got, ref)
     assert r["n_fail"] == 0, r
 
