@@ -7,6 +7,19 @@
 namespace ifr {
 namespace {
 
+// Page copies stream through once: non-temporal loads and stores keep them
+// from displacing the caches' working set (config 9: 4.60 -> 4.70 TB/s; the
+// runtime's own 1 GiB device copy measures 5.0 TB/s).  The row gather keeps
+// ordinary loads and stores (non-temporal measured 8 % slower there).
+typedef unsigned int cu32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint4* p) {
+  const cu32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const cu32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_stream(uint4* p, uint4 v) {
+  __builtin_nontemporal_store(cu32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<cu32x4_t*>(p));
+}
+
 // PageCopyKernel (kernels/page_copy.mojo:25-60): the host splits every
 // CopyJob into chunks of at most kCopyChunk bytes; one workgroup copies one
 // chunk.  A chunk whose source and destination addresses agree modulo 16
@@ -35,11 +48,11 @@ __global__ __launch_bounds__(256) void copy_chunks_kernel(
   for (; i + (kIn - 1) * 256 < n16; i += kIn * 256) {
     uint4 v[kIn];
 #pragma unroll
-    for (int u = 0; u < kIn; ++u) v[u] = s[i + u * 256];
+    for (int u = 0; u < kIn; ++u) v[u] = load_stream(s + i + u * 256);
 #pragma unroll
-    for (int u = 0; u < kIn; ++u) d[i + u * 256] = v[u];
+    for (int u = 0; u < kIn; ++u) store_stream(d + i + u * 256, v[u]);
   }
-  for (; i < n16; i += 256) d[i] = s[i];
+  for (; i < n16; i += 256) store_stream(d + i, load_stream(s + i));
   const int64_t tail0 = head + (n16 << 4);
   if (tail0 + tid < bytes) arena[dst + tail0 + tid] = arena[src + tail0 + tid];
 }
