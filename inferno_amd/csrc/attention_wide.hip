@@ -27,14 +27,14 @@
 //           lane ^ 16, then (j, j+2), (j, j+1) in the lane.
 //   P.V     on VALU: lane L owns output dims 8L..8L+7 of all 8 heads (64
 //           accumulators) and adds fma(v, w, acc) in position order, the
-//           reference's per-element order; each weight reaches every lane with
-//           v_readlane.  The V row of a position (1 KiB bf16 or 512 B int8) is
-//           one load instruction.
+//           reference's per-element order; each position's weights reach
+//           every lane as two broadcast LDS reads.  The V row of a position
+//           (1 KiB bf16 or 512 B int8) is one load instruction.
 // Loads are software-pipelined in the tile's own registers (no second tile
 // buffer): the next tile's K loads are issued once the score MFMAs have read
 // K and run under the softmax and P.V; its V loads are issued after the P.V
 // and run under the next scores and softmax.  A wave thus always has about
-// one tile in flight (218-226 VGPRs for bf16, 181-189 for int8: two waves
+// one tile in flight (about 220 VGPRs for bf16, 185-190 for int8: two waves
 // per SIMD).
 #include <type_traits>
 
@@ -108,6 +108,10 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   constexpr int kVB = kRow / 64;  // value bytes per lane per position
   using VT = typename Tile::VT;
   __shared__ __align__(16) uint8_t qs[kWG * (kBq ? kWQPitchBq : kWQPitch)];
+  // The tile's weights, [position][q head]: each position's 8 weights reach
+  // every lane as two broadcast LDS reads (LDS instructions, where 8
+  // v_readlanes per position were VALU work in a VALU-bound loop).
+  __shared__ __align__(16) float wl[kTile * kWG];
 
   const int lane = threadIdx.x;
   const int g = blockIdx.x;
@@ -314,6 +318,13 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
       for (int j = 0; j < 4; ++j) w[j] = 4 * qd + j < tile_len ? w[j] : 0.0f;
     }
 
+    // Lanes of columns 0..7 publish their weights (the wave's own LDS: its
+    // writes land before its reads, and the previous tile's reads are done).
+    if ((lane & 15) < kWG) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wl[(4 * qd + j) * kWG + (lane & (kWG - 1))] = w[j];
+    }
+
     // ---- scale_unrolled, then P.V in position order ----
 #pragma unroll
     for (int h = 0; h < kWG; ++h) {
@@ -326,12 +337,9 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
       if (kFlat || t < tile_len) {  // wave-uniform
         float vf[8];
         unpack8(d.v[t], vf);
-        // The position's 8 weights first, then its 64 FMAs: a v_readlane
-        // result read by the very next VALU instruction costs wait states.
-        float wt[kWG];
-#pragma unroll
-        for (int h = 0; h < kWG; ++h) wt[h] = readlane_f32(w[t & 3], h + 16 * (t >> 2));
-        __builtin_amdgcn_sched_barrier(0);
+        const float4 wa = *reinterpret_cast<const float4*>(&wl[t * kWG]);
+        const float4 wb = *reinterpret_cast<const float4*>(&wl[t * kWG + 4]);
+        const float wt[kWG] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
         for (int h = 0; h < kWG; ++h)
 #pragma unroll
