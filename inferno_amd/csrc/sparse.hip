@@ -431,10 +431,12 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
   // A tile never straddles a page (page_len >= 16, tiles 16-aligned), so its
   // page row is one uniform (scalar) load, not a vector load the K/V loads
   // would have to wait behind.
-  auto load_tile = [&](const TileCursor& c) {
+  auto page_row = [&](const TileCursor& c) -> int64_t {
+    return sload(tp.rows + static_cast<int>(c.pos >> shift));
+  };
+  auto load_tile = [&](const TileCursor& c, int64_t prow) {
     TileRegs d;
     const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
-    const int64_t prow = sload(tp.rows + static_cast<int>(c.pos >> shift));
     const int off0 = static_cast<int>(c.pos) & row_mask;
     const int64_t kslot = prow + off0 + (r16 < tl ? r16 : 0);
     const uint16_t* kp = kh + kslot * kv_stride + 8 * g;
@@ -454,38 +456,28 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
 #pragma unroll
   for (int b = 0; b < kSDW / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Three tiles in flight: the current one (rg), and the next two (r1, then
-  // r2, issued during the current tile).
-  auto advance = [&](const TileCursor& c) {
-    return c.valid ? next_tile(c, brow, topk, block_size, cap) : c;
-  };
-  TileCursor cur = next_tile(TileCursor{-1, 0, 0, false}, brow, topk, block_size, cap);
-  TileCursor c1 = advance(cur);
-  TileRegs rg{}, r1{};
-  if (cur.valid) rg = load_tile(cur);
-  if (c1.valid) r1 = load_tile(c1);
-  int buf = 0;
-  while (cur.valid) {
-    const TileCursor c2 = advance(c1);
-    const int tl = static_cast<int>(min<int64_t>(kTile, cur.phi - cur.pos));
+  // A tile's scores and softmax, then P.V; between the two the caller
+  // reuses the tile's registers for the loads of a later tile.
+  auto scores = [&](const TileRegs& rg, const TileCursor& c, int buf) {
     uint8_t* vb = vlds[wave][buf];
     wave_sync();
     *reinterpret_cast<uint4*>(vb + vrow_l * kSVPitchW + vcol) = rg.v0;
-    TileRegs r2{};
-    if (c2.valid) r2 = load_tile(c2);
-
     f32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
     sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k0), qf[0], sc, 0, 0, 0);
     sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k1), qf[1], sc, 0, 0, 0);
     sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k2), qf[2], sc, 0, 0, 0);
     sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rg.k3), qf[3], sc, 0, 0, 0);
+    return sc;
+  };
+  auto softmax_pv = [&](const f32x4_t& sc, const TileCursor& c, int buf) {
+    const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
+    uint8_t* vb = vlds[wave][buf];
     // Scores of pad positions are -1e30 (their fexp(-87) enters l only).
     float sj[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) sj[j] = (4 * g + j < tl) ? sc[j] : kNegBig;
     float tmax = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
-    tmax = max_ref(tmax, shfl_xor_f32(tmax, 16));
-    tmax = max_ref(tmax, shfl_xor_f32(tmax, 32));
+    tmax = pair_max32(pair_max16(tmax));  // lane swaps, not LDS permutes
     const float m_new = tmax > m ? tmax : m;
     const float corr = fexp(max_ref(-87.0f, m - m_new));
     float w[4];
@@ -494,9 +486,7 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
     // 16-position halving tree: t with t+8 (xor 32), t+4 (xor 16), then j+2, j+1.
     float ws[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ws[j] = w[j] + shfl_xor_f32(w[j], 32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ws[j] = ws[j] + shfl_xor_f32(ws[j], 16);
+    for (int j = 0; j < 4; ++j) ws[j] = pair_sum16(pair_sum32(w[j]));
     const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
     lsum = lsum * corr + wsum;
     m = m_new;
@@ -526,12 +516,66 @@ __global__ __launch_bounds__(256) void sparse_attention_kernel(
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
     }
-    rg = r1;
-    r1 = r2;
-    cur = c1;
-    c1 = c2;
-    buf ^= 1;
+  };
+
+  // kAhead tiles in flight in rotating register sets (no copies between
+  // them): set s holds tile i + s; once tile i's scores have read its keys
+  // and its values are in LDS, the set takes the loads of tile i + kAhead.
+  // The loads are unconditional -- past the block list they all read the
+  // sequence's first row (in bounds, unused) -- so every step leaves the same
+  // loads in flight and each wait covers only older loads.  The next
+  // cursor's page row is read (scalar) one step before its loads use it.
+  // An even depth keeps each step's LDS buffer a compile-time choice
+  // (measured: depths 2 and 4 93 us, 3 and 5 100 us, 6 and 8 98.5 us).
+  constexpr int kAhead = 4;
+  auto advance = [&](const TileCursor& c) {
+    return c.valid ? next_tile(c, brow, topk, block_size, cap) : c;
+  };
+  auto dummy_or = [&](const TileCursor& c) {
+    TileCursor d = c;  // selects, not a branch: one code path for the loads
+    d.pos = c.valid ? c.pos : 0;
+    d.phi = c.valid ? c.phi : kTile;
+    return d;
+  };
+  TileCursor cs[kAhead];
+  TileRegs rs[kAhead];
+  cs[0] = next_tile(TileCursor{-1, 0, 0, false}, brow, topk, block_size, cap);
+#pragma unroll
+  for (int i = 1; i < kAhead; ++i) cs[i] = advance(cs[i - 1]);
+  // Issued in set order, as the loop issues them (the waits count on it).
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i) {
+    const TileCursor d = dummy_or(cs[i]);
+    rs[i] = load_tile(d, page_row(d));
+    __builtin_amdgcn_sched_barrier(0);
   }
+  TileCursor pend = dummy_or(advance(cs[kAhead - 1]));  // the next tile to issue
+  bool pend_valid = advance(cs[kAhead - 1]).valid;
+  TileCursor last = advance(cs[kAhead - 1]);
+  int64_t pend_row = page_row(pend);
+  int buf = 0;
+  for (;;) {
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s) {
+      // Leaving the loop is the only branch: every path that goes on has
+      // issued the same loads.
+      if (!cs[s].valid) goto tiles_done;  // uniform
+      const TileCursor c = cs[s];
+      const f32x4_t sc = scores(rs[s], c, buf);
+      __builtin_amdgcn_sched_barrier(0);
+      rs[s] = load_tile(pend, pend_row);
+      __builtin_amdgcn_sched_barrier(0);
+      cs[s] = pend;
+      cs[s].valid = pend_valid;
+      last = advance(last);
+      pend_valid = last.valid;
+      pend = dummy_or(last);
+      pend_row = page_row(pend);
+      softmax_pv(sc, c, buf);
+      buf ^= 1;
+    }
+  }
+tiles_done:
 
   // write_finalized_head over one stripe: cv = fexp(0) scales both acc and
   // l (l > 0), out = (acc * cv) * (1 / (0 + l * cv)).
@@ -743,8 +787,7 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
       sj[j] = (4 * g + j < tl) ? sc : kNegBig;
     }
     float tmax = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
-    tmax = max_ref(tmax, shfl_xor_f32(tmax, 16));
-    tmax = max_ref(tmax, shfl_xor_f32(tmax, 32));
+    tmax = pair_max32(pair_max16(tmax));  // lane swaps, not LDS permutes
     const float m_new = tmax > m ? tmax : m;
     const float corr = fexp(max_ref(-87.0f, m - m_new));
     float w[4];
@@ -752,9 +795,7 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
     for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sj[j] - m_new));
     float ws[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ws[j] = w[j] + shfl_xor_f32(w[j], 32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ws[j] = ws[j] + shfl_xor_f32(ws[j], 16);
+    for (int j = 0; j < 4; ++j) ws[j] = pair_sum16(pair_sum32(w[j]));
     const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
     lsum = lsum * corr + wsum;
     m = m_new;
@@ -816,6 +857,256 @@ __global__ __launch_bounds__(256) void bq_sparse_kernel(
     uint16_t* orow = out + qrow * kSD + 4 * g;
 #pragma unroll
     for (int b = 0; b < kSD / 16; ++b) {
+      uint32_t lo = 0, hi = 0;
+      if (gl > 0.0f) {
+        lo = f32_to_bf16_bits((acc[b][0] * cv) * inv) |
+             (f32_to_bf16_bits((acc[b][1] * cv) * inv) << 16);
+        hi = f32_to_bf16_bits((acc[b][2] * cv) * inv) |
+             (f32_to_bf16_bits((acc[b][3] * cv) * inv) << 16);
+      }
+      *reinterpret_cast<uint2*>(orow + 16 * b) = make_uint2(lo, hi);
+    }
+  }
+}
+
+// The batched route of bq_sparse_kernel (one sequential pass per (token, kv
+// head)) with the bf16 kernel's split: four waves per (token, kv head), each
+// forming the same int8 scores (exact integers, so identical) and owning 32
+// of the 128 output dims, with kSAhead tiles in flight in rotating register
+// sets.  One wave per (token, kv head) left three quarters of the SIMDs idle
+// at B = 64 with 4 kv heads.
+struct BqSplitRegs {
+  uint4 k0, k1;       // keys: row r16, bytes 16g and 64 + 16g
+  uint2 v;            // values: 8 bytes of the wave's 32 dims of row lane/4
+  float ks[4], vs[4];  // scales of positions 4g + j
+};
+constexpr int kSAhead = 4;
+
+__global__ __launch_bounds__(256) void bq_sparse_split_kernel(
+    const int32_t* __restrict__ image, const int8_t* __restrict__ q_i8,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const int8_t* __restrict__ k_base, const float* __restrict__ k_scale,
+    const int8_t* __restrict__ v_base, const float* __restrict__ v_scale,
+    const int32_t* __restrict__ block_idx, uint16_t* __restrict__ out, int64_t kv_stride,
+    int num_q, int num_kv, int block_size, int topk, int shift, int row_mask, int num_rows) {
+  __shared__ __align__(16) uint8_t vlds[4][2][kSVBytesW];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x;
+  if (row >= num_rows) return;
+  const int dq = wave;  // the wave's quarter of the output dims
+  const int t = row / num_kv;
+  const int h = row - t * num_kv;
+  const TokenPos tp = token_position(image, t);
+  const int64_t cap = static_cast<int64_t>(tp.abs_pos) + 1;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int gh = h * kSG + r16;  // q head of this lane's column
+  const int64_t qrow = static_cast<int64_t>(t) * num_q + gh;
+
+  // B operand of the scores: q codes of head r16, bytes 16g and 64 + 16g;
+  // qsum = sum of the head's 128 codes (exact).
+  const int8_t* qp = q_i8 + qrow * kSD + 16 * g;
+  const uint4 qa = *reinterpret_cast<const uint4*>(qp);
+  const uint4 qb4 = *reinterpret_cast<const uint4*>(qp + 64);
+  int qsum = 0;
+  {
+    const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb4.x, qb4.y, qb4.z, qb4.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      qsum += static_cast<int8_t>(w8[i]) + static_cast<int8_t>(w8[i] >> 8) +
+              static_cast<int8_t>(w8[i] >> 16) + static_cast<int8_t>(w8[i] >> 24);
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+  }
+  const float qbias = qi_bias[qrow];
+  const float fq = f_q[qrow];
+  const float inv127 = 1.0f / 127.0f;
+  const float inv127sq = inv127 * inv127;
+
+  const int8_t* kh = k_base + static_cast<int64_t>(h) * kSD;
+  const int8_t* vh = v_base + static_cast<int64_t>(h) * kSD + kSDW * dq;
+  const int32_t* brow = block_idx + static_cast<int64_t>(row) * topk;
+  // V staging: lane takes 8 bytes (dims 8*(l%4) ..) of the wave's 32 dims of
+  // row l/4 and writes them as 8 bf16 (exact); the transposing read as in
+  // sparse_attention_kernel.
+  const int vrow_l = lane >> 2;
+  const int vcol = 8 * (lane & 3);
+  const int tr_off = (4 * g + (r16 >> 2)) * kSVPitchW + 8 * (r16 & 3);
+
+  auto page_row = [&](const TileCursor& c) -> int64_t {
+    return sload(tp.rows + static_cast<int>(c.pos >> shift));
+  };
+  auto load_tile = [&](const TileCursor& c, int64_t prow) {
+    BqSplitRegs d;
+    const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
+    const int64_t base = prow + (static_cast<int>(c.pos) & row_mask);
+    const int8_t* kp = kh + (base + (r16 < tl ? r16 : 0)) * kv_stride + 16 * g;
+    d.k0 = *reinterpret_cast<const uint4*>(kp);
+    d.k1 = *reinterpret_cast<const uint4*>(kp + 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t sl = (base + (4 * g + j < tl ? 4 * g + j : 0)) * num_kv + h;
+      d.ks[j] = k_scale[sl];
+      d.vs[j] = v_scale[sl];
+    }
+    d.v = *reinterpret_cast<const uint2*>(vh + (base + (vrow_l < tl ? vrow_l : 0)) * kv_stride +
+                                          vcol);
+    return d;
+  };
+
+  float m = kNegBig;
+  float lsum = 0.0f;
+  f32x4_t acc[kSDW / 16];  // acc[b][j] = O[dim 32dq + 16b + 4g + j][head r16]
+#pragma unroll
+  for (int b = 0; b < kSDW / 16; ++b) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Values to LDS and the tile's scores; the caller then reuses the tile's
+  // registers for the loads of a later tile.
+  auto scores = [&](const BqSplitRegs& rg, const TileCursor& c, int buf, float (&sj)[4]) {
+    const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
+    uint8_t* vb = vlds[wave][buf];
+    wave_sync();
+    {
+      const uint32_t w8[2] = {rg.v.x, rg.v.y};
+      uint32_t o16[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int b = 0; b < 4; b += 2) {
+          const float f0 = static_cast<float>(static_cast<int8_t>(w8[i] >> (8 * b)));
+          const float f1 = static_cast<float>(static_cast<int8_t>(w8[i] >> (8 * b + 8)));
+          o16[2 * i + b / 2] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+        }
+      }
+      *reinterpret_cast<uint4*>(vb + vrow_l * kSVPitchW + 2 * vcol) =
+          make_uint4(o16[0], o16[1], o16[2], o16[3]);
+    }
+    i32x4_t si = {0, 0, 0, 0};
+    si = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+        __builtin_bit_cast(i32x4_t, rg.k0), __builtin_bit_cast(i32x4_t, qa), si, 0, 0, 0);
+    si = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+        __builtin_bit_cast(i32x4_t, rg.k1), __builtin_bit_cast(i32x4_t, qb4), si, 0, 0, 0);
+    // Lane holds positions 4g + j of head r16.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float raw = static_cast<float>(si[j] + 128 * qsum);
+      float sc = raw - qbias;
+      sc = sc * fq;
+      sc = sc * rg.ks[j];
+      sc = sc * inv127sq;
+      sj[j] = (4 * g + j < tl) ? sc : kNegBig;
+    }
+  };
+  auto softmax_pv = [&](const float (&sj)[4], const float (&vsj)[4], const TileCursor& c,
+                        int buf) {
+    const int tl = static_cast<int>(min<int64_t>(kTile, c.phi - c.pos));
+    uint8_t* vb = vlds[wave][buf];
+    float tmax = max_ref(max_ref(sj[0], sj[1]), max_ref(sj[2], sj[3]));
+    tmax = pair_max32(pair_max16(tmax));
+    const float m_new = tmax > m ? tmax : m;
+    const float corr = fexp(max_ref(-87.0f, m - m_new));
+    float w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = fexp(max_ref(-87.0f, sj[j] - m_new));
+    float ws[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ws[j] = pair_sum16(pair_sum32(w[j]));
+    const float wsum = (ws[0] + ws[2]) + (ws[1] + ws[3]);
+    lsum = lsum * corr + wsum;
+    m = m_new;
+    s16x4_t phi, plo;
+#pragma unroll
+    for (int j = 0; j < 4; j += 2) {
+      float p0 = w[j] * vsj[j];
+      p0 = p0 * inv127;
+      float p1 = w[j + 1] * vsj[j + 1];
+      p1 = p1 * inv127;
+      p0 = (4 * g + j < tl) ? p0 : 0.0f;
+      p1 = (4 * g + j + 1 < tl) ? p1 : 0.0f;
+      const bf16x2_t hb = __builtin_convertvector(f32x2_t{p0, p1}, bf16x2_t);
+      const float r0 = p0 - static_cast<float>(hb[0]);
+      const float r1 = p1 - static_cast<float>(hb[1]);
+      const bf16x2_t lb = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+      const s16x4_t hs = __builtin_bit_cast(s16x4_t, __builtin_shufflevector(hb, hb, 0, 1, 0, 1));
+      const s16x4_t ls = __builtin_bit_cast(s16x4_t, __builtin_shufflevector(lb, lb, 0, 1, 0, 1));
+      phi[j] = hs[0];
+      phi[j + 1] = hs[1];
+      plo[j] = ls[0];
+      plo[j + 1] = ls[1];
+    }
+    wave_sync();
+#pragma unroll
+    for (int b = 0; b < kSDW / 16; ++b) {
+      acc[b] = acc[b] * corr;
+      const s16x4_t va =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + tr_off + 32 * b));
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, phi, acc[b], 0, 0, 0);
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, plo, acc[b], 0, 0, 0);
+    }
+  };
+
+  // Rotating register sets as in sparse_attention_kernel: unconditional
+  // loads (past the block list they read the sequence's first row), leaving
+  // the loop the only branch, page rows read one step ahead.
+  auto advance = [&](const TileCursor& c) {
+    return c.valid ? next_tile(c, brow, topk, block_size, cap) : c;
+  };
+  auto dummy_or = [&](const TileCursor& c) {
+    TileCursor d = c;
+    d.pos = c.valid ? c.pos : 0;
+    d.phi = c.valid ? c.phi : kTile;
+    return d;
+  };
+  TileCursor cs[kSAhead];
+  BqSplitRegs rs[kSAhead];
+  cs[0] = next_tile(TileCursor{-1, 0, 0, false}, brow, topk, block_size, cap);
+#pragma unroll
+  for (int i = 1; i < kSAhead; ++i) cs[i] = advance(cs[i - 1]);
+#pragma unroll
+  for (int i = 0; i < kSAhead; ++i) {
+    const TileCursor d = dummy_or(cs[i]);
+    rs[i] = load_tile(d, page_row(d));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  TileCursor last = advance(cs[kSAhead - 1]);
+  TileCursor pend = dummy_or(last);
+  bool pend_valid = last.valid;
+  int64_t pend_row = page_row(pend);
+  int buf = 0;
+  for (;;) {
+#pragma unroll
+    for (int s = 0; s < kSAhead; ++s) {
+      if (!cs[s].valid) goto tiles_done;  // uniform
+      const TileCursor c = cs[s];
+      float sj[4], vsj[4];
+      scores(rs[s], c, buf, sj);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vsj[j] = rs[s].vs[j];
+      __builtin_amdgcn_sched_barrier(0);
+      rs[s] = load_tile(pend, pend_row);
+      __builtin_amdgcn_sched_barrier(0);
+      cs[s] = pend;
+      cs[s].valid = pend_valid;
+      last = advance(last);
+      pend_valid = last.valid;
+      pend = dummy_or(last);
+      pend_row = page_row(pend);
+      softmax_pv(sj, vsj, c, buf);
+      buf ^= 1;
+    }
+  }
+tiles_done:
+  {
+    // write_finalized_head over one stripe.
+    const float gm = m > kNegBig ? m : kNegBig;
+    float cv = fexp(max_ref(-87.0f, m - gm));
+    cv = lsum > 0.0f ? cv : 0.0f;
+    const float gl = 0.0f + lsum * cv;
+    const float inv = gl > 0.0f ? 1.0f / gl : 0.0f;
+    uint16_t* orow = out + qrow * kSD + kSDW * dq + 4 * g;
+#pragma unroll
+    for (int b = 0; b < kSDW / 16; ++b) {
       uint32_t lo = 0, hi = 0;
       if (gl > 0.0f) {
         lo = f32_to_bf16_bits((acc[b][0] * cv) * inv) |
@@ -906,10 +1197,9 @@ hipError_t launch_bq_block_sparse_attention(
                                 stream);
   }
   const int rows = seq_len * num_kv;
-  hipLaunchKernelGGL(bq_sparse_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, stream,
-                     image, q, qi_bias, f_q, k, k_scale, v, v_scale, block_idx, o, partials,
-                     partial_stride, kv_stride, num_q, num_kv, block_size, topk, 0, 1, shift,
-                     row_mask, rows);
+  hipLaunchKernelGGL(bq_sparse_split_kernel, dim3(rows), dim3(256), 0, stream, image, q,
+                     qi_bias, f_q, k, k_scale, v, v_scale, block_idx, o, kv_stride, num_q,
+                     num_kv, block_size, topk, shift, row_mask, rows);
   return hipGetLastError();
 }
 

@@ -280,3 +280,22 @@ def test_bq_sparse_prefill_chunk():
         bi[t, 2, :4] = [1, 2, -1, 5]
         bi[t, 3, :3] = [9, 6, 7]
     _check_bq_sparse(plan, runs, rows, _bq_inputs(rng, n_tok, cache_rows), bi, page_len, cap=8)
+
+
+@pytest.mark.parametrize("page_len", [64, 128])
+def test_bq_sparse_batched_decode_on_indexer_selection(page_len):
+    """seq_len > 1 with one token per sequence (config 6's batched decode):
+    the four-waves-per-(token, kv head) int8 kernel with its rotating tile
+    registers, over the GPU indexer's selections, including a sequence of
+    position 0 and a long one that fills all 16 slots."""
+    announce(f"bq sparse batched decode page_len={page_len}")
+    rng = np.random.default_rng(500 + page_len)
+    ctx = [0, 77, 300, 2048, 4100, 7000, 20000]
+    case = make_decode_case(29, ctx, page_len=page_len)
+    index_q = _bf(rng.standard_normal(len(ctx) * IH * HD))
+    index_k = _bf(rng.standard_normal(case.cache_rows * HD))
+    plan = _plan(case.runs, case.base_rows, len(ctx), case.cache_rows, page_len)
+    bi, _ = _run_indexer(plan, index_q, index_k)
+    inputs = _bq_inputs(rng, len(ctx), case.cache_rows)
+    r = _check_bq_sparse(plan, case.runs, case.base_rows, inputs, bi, page_len, cap=8)
+    print(f"  bq sparse batched decode vs oracle: {r}", flush=True)
