@@ -131,7 +131,7 @@ def test_fullsize_config2_headline():
 
 
 def test_fullsize_config3_sliding_rings():
-    """B=64 sliding window 1024 over 32-page rings, cap 384."""
+    """B=64 sliding window 1024 over 32-page rings, cap 256."""
     _run_bf16(3, bench.DEFAULT_CAP[3])
 
 
