@@ -6,8 +6,9 @@
 // full-attention plan image (ifr_plan_attention).
 //
 // index_scores_kernel   one wave per (token, block): each lane takes whole
-//                       positions and all index heads, and forms the dots in
-//                       the reference's VDPBF16PS order, so block scores, and
+//                       positions and all index heads (queries from SGPRs),
+//                       and forms the dots in the reference's VDPBF16PS order,
+//                       so block scores, and
 //                       with them the selected blocks, are bit-identical.
 // select_blocks_kernel  one wave per (token, index head): the reference's
 //                       32-slot streaming bank, each reduction done as a rank
@@ -58,7 +59,6 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
     int block_size, float scale, int shift, int row_mask) {
   constexpr int kP = D / 32;  // port-unroll accumulators, one strip
   static_assert(H * D == 64 * 8, "one 16-byte query load per lane");
-  __shared__ __align__(16) float qs[4][H * D];  // the token's queries, unpacked
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.y;
@@ -90,14 +90,11 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
     for (int c = 0; c < D / 8; ++c) kv[c] = kr[c];
   };
   uint4 kv[D / 8];
-  load_round(lo, kv);  // in flight while the queries are staged
-  {
-    const uint4 q8 = reinterpret_cast<const uint4*>(index_q + static_cast<int64_t>(t) * H * D)[lane];
-    float4* qd = reinterpret_cast<float4*>(&qs[wave][8 * lane]);
-    qd[0] = make_float4(bf16_lo(q8.x), bf16_hi(q8.x), bf16_lo(q8.y), bf16_hi(q8.y));
-    qd[1] = make_float4(bf16_lo(q8.z), bf16_hi(q8.z), bf16_lo(q8.w), bf16_hi(q8.w));
-  }
-  wave_sync();
+  load_round(lo, kv);
+  // The token's queries are wave-uniform: bf16 pairs read as scalar dwords
+  // and unpacked on the SALU, so each FMA takes its query value from an
+  // SGPR (no LDS staging or reads).
+  const int32_t* qg = reinterpret_cast<const int32_t*>(index_q + static_cast<int64_t>(t) * H * D);
   float best[H];
 #pragma unroll
   for (int h = 0; h < H; ++h) best[h] = kNegBig;
@@ -105,10 +102,10 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
   // once, the queries are read from LDS (every lane the same address).
   for (int p0 = lo; p0 < hi; p0 += 64) {
     const bool valid = p0 + lane < hi;
-    // The query reads stay inside the loop (hoisted, 512 floats would not
-    // fit in registers).
-    int qoff = wave * H * D;
-    asm volatile("" : "+v"(qoff));
+    // The query reads stay inside the loop (hoisted, 256 dwords would not
+    // fit in SGPRs).
+    int qoff = 0;
+    asm volatile("" : "+s"(qoff));
     float s[H][16];
 #pragma unroll
     for (int p = 0; p < kP; ++p) {
@@ -125,15 +122,14 @@ __global__ __launch_bounds__(256) void index_scores_kernel(
       }
 #pragma unroll
       for (int h = 0; h < H; ++h) {
-        const float4* qh = reinterpret_cast<const float4*>(&qs[0][qoff + h * D + 32 * p]);
+        const int32_t* qh = qg + qoff + (h * D + 32 * p) / 2;  // 16 dwords: pairs j = 0..15
 #pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          const float4 q4 = qh[j / 2];  // even, odd of pair j, then of pair j+1
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t qw = static_cast<uint32_t>(sload(qh + j));
+          const float qe = __uint_as_float(qw << 16), qo = __uint_as_float(qw & 0xFFFF0000u);
           // bf16 products are exact in f32, so the fma rounds (odd + even) once.
-          const float a0 = fmaf(klo[j], q4.x, khi[j] * q4.y);
-          const float a1 = fmaf(klo[j + 1], q4.z, khi[j + 1] * q4.w);
-          s[h][j] = p == 0 ? a0 : s[h][j] + a0;
-          s[h][j + 1] = p == 0 ? a1 : s[h][j + 1] + a1;
+          const float a = fmaf(klo[j], qe, khi[j] * qo);
+          s[h][j] = p == 0 ? a : s[h][j] + a;
         }
       }
     }
