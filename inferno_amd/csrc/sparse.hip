@@ -8,8 +8,8 @@
 // index_scores_kernel   one wave per (token, block): each lane takes whole
 //                       positions and all index heads (queries from SGPRs),
 //                       and forms the dots in the reference's VDPBF16PS order,
-//                       so block scores, and
-//                       with them the selected blocks, are bit-identical.
+//                       so block scores, and with them the selected blocks,
+//                       are bit-identical.
 // select_blocks_kernel  one wave per (token, index head): the reference's
 //                       32-slot streaming bank, each reduction done as a rank
 //                       count under reduce_argmax's order (value, then slot
