@@ -237,11 +237,15 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
     for (int i = 0; i < kFastChunks; ++i) {
       const int blk = 64 * i + lane;
       float x = -INFINITY;
-      if (i < n_chunks && blk < nb)
-        x = (blk >= local_start || blk < init_blocks) ? 1.0e30f : sr[blk] + 0.0f;  // -0 -> +0
+      const bool in = i < n_chunks && blk < nb;
+      if (in) x = (blk >= local_start || blk < init_blocks) ? 1.0e30f : sr[blk] + 0.0f;  // -0 -> +0
       vals[i] = x;
       const uint32_t u = __float_as_uint(x);
-      keys[i] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // order-preserving
+      // Order-preserving key; 0 for slots past the row, which no candidate
+      // (at least one bit set) counts, so the counting loop needs no
+      // per-chunk branch.
+      keys[i] = in ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+      asm volatile("" : "+v"(keys[i]));  // a plain register: one compare per chunk below
     }
     uint32_t prefix = 0;
     for (int bit = 31; bit >= 0; --bit) {
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
       int cnt = 0;
 #pragma unroll
       for (int i = 0; i < kFastChunks; ++i)
-        if (i < n_chunks) cnt += __popcll(__ballot(keys[i] >= cand));
+        cnt += __popcll(__builtin_amdgcn_ballot_w64(keys[i] >= cand));
       if (cnt >= topk) prefix = cand;
     }
     const uint32_t tu = (prefix & 0x80000000u) ? (prefix & 0x7FFFFFFFu) : ~prefix;
