@@ -258,16 +258,16 @@ __global__ __launch_bounds__(256) void select_blocks_kernel(
     }
     const uint32_t tu = (prefix & 0x80000000u) ? (prefix & 0x7FFFFFFFu) : ~prefix;
     const float thr = __uint_as_float(tu);
+    // Slots past the row hold -inf, below any threshold of finite scores.
     int cnt_ge = 0;
 #pragma unroll
     for (int i = 0; i < kFastChunks; ++i)
-      if (i < n_chunks) cnt_ge += __popcll(__ballot(vals[i] >= thr));
+      cnt_ge += __popcll(__builtin_amdgcn_ballot_w64(vals[i] >= thr));
     if (cnt_ge == topk) {
       const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
       int written = 0;
 #pragma unroll
       for (int i = 0; i < kFastChunks; ++i) {
-        if (i >= n_chunks) break;
         const bool sel = vals[i] >= thr;
         const uint64_t mask = __ballot(sel);
         if (sel) out[written + __popcll(mask & below)] = 64 * i + lane;
