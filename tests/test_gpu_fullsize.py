@@ -12,6 +12,10 @@ compared with the oracle run on host copies of the same caches.
   across a bf16 rounding boundary: every output within one bf16 spacing where
   |x| >= 2 and 1e-2 elsewhere, and at most 1e-5 of the outputs beyond 1e-2;
 - configs 5 and 8 (bq): outputs bit-exact;
+- config 6 (MiniMax-M3 sparse decode, bf16 and int8 KV): the indexer's
+  selected blocks bit-exact over every cached position of the 64 sequences,
+  the sparse attention on them within 1e-2 (one bf16 spacing where |x| >=
+  2);
 - the append of every config: the appended K/V rows and the rotated q
   bit-exact against the oracle's rope_cache_write / bq prep, computed on a
   compact copy of the appended pages.
@@ -216,3 +220,62 @@ def test_fullsize_config5_bq():
 def test_fullsize_config8_bq_full_layer():
     """The bq full-attention layer (16q/2kv hd512), B=128, cap 2048."""
     _run_bq(8, bench.DEFAULT_CAP[8])
+
+
+def _run_sparse(kv):
+    import torch
+
+    announce(f"fullsize config 6 kv {kv}: setup")
+    t0 = time.time()
+    w = bench.SparseM3(SEED)
+    dev = torch.device("cuda:0")
+    w.setup(dev, _args(0) if kv == "bf16" else argparse.Namespace(cap=0, kv=kv))
+    for ph in w.phases:
+        w.launch(ph)
+    ik, kc, vc, ks, vs = w.kl[w.layer]
+    B, IH, TOPK = len(w.pos), w.IH, w.TOPK
+    got_bi = _host(w.block_idx, np.int32).reshape(B, IH, TOPK)
+    got = _host(w.out, np.uint16)
+    iq, ikh = _host(w.index_q, np.uint16), _host(ik, np.uint16)
+    announce(f"  step done, index keys on host ({ikh.nbytes / 1e9:.1f} GB, "
+             f"{time.time() - t0:.1f} s)")
+
+    t1 = time.time()
+    runs, rows = w.table.arrays()
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(w.HD)))
+    want_bi, _ = oracle.lightning_indexer(runs, rows, iq, ikh, num_heads=IH, head_dim=w.HD,
+                                          block_size=w.BLOCK, topk=TOPK, local_blocks=1,
+                                          init_blocks=0, scale=scale, page_len=w.PLEN,
+                                          seq_len=B)
+    assert np.array_equal(got_bi, want_bi), np.argwhere(got_bi != want_bi)[:5]
+    announce(f"  indexer oracle {time.time() - t1:.1f} s: block ids bit-exact")
+    del ikh
+
+    t2 = time.time()
+    common = dict(num_q=w.NQ, num_kv=w.NKV, head_dim=w.HD, kv_stride=w.NKV * w.HD,
+                  block_size=w.BLOCK, topk=TOPK, page_len=w.PLEN, seq_len=B)
+    if kv == "bf16":
+        q, kh, vh = _host(w.q, np.uint16), _host(kc, np.uint16), _host(vc, np.uint16)
+        ref = oracle.block_sparse_attention(runs, rows, q, kh, vh, want_bi, **common)
+    else:
+        q, kh, vh = _host(w.q, np.int8), _host(kc, np.int8), _host(vc, np.int8)
+        qb, fq = _host(w.qb, np.float32), _host(w.fq, np.float32)
+        ksh, vsh = _host(ks, np.float32), _host(vs, np.float32)
+        ref = oracle.bq_block_sparse_attention(runs, rows, q, qb, fq, kh, ksh, vh, vsh,
+                                               want_bi, cap=128, **common)
+    r = compare_bf16(got, ref)
+    announce(f"  attention oracle {time.time() - t2:.1f} s, "
+             f"bit-exact {bool(np.array_equal(got, ref))}: {r}")
+    assert r["n_nan"] == 0 and r["n_fail"] == 0, r
+
+
+def test_fullsize_config6_sparse():
+    """MiniMax-M3 sparse decode, B=64, ctx ~ U[1024, 131072]: the indexer's
+    block ids bit-exact over every cached position, the sparse attention
+    within the bar on them."""
+    _run_sparse("bf16")
+
+
+def test_fullsize_config6_bq_sparse():
+    """The same over int8 KV (bench.py's random codes and scales, cap 128)."""
+    _run_sparse("bq")
