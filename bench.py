@@ -38,7 +38,7 @@ NUM_Q, NUM_KV, HEAD_DIM, PAGE_LEN = 16, 8, 256, 64
 HIDDEN = 2816  # Gemma 4 26B-A4B hidden size: o_proj maps 16 x 256 -> 2816
 KV_STRIDE = NUM_KV * HEAD_DIM
 MASK64 = (1 << 64) - 1
-DEFAULT_CAP = {1: 128, 2: 512, 3: 256, 4: 16, 5: 2048, 6: 0, 7: 1024, 8: 2048, 9: 0, 10: 0,
+DEFAULT_CAP = {1: 128, 2: 512, 3: 256, 4: 16, 5: 2048, 6: 0, 7: 512, 8: 2048, 9: 0, 10: 0,
                11: 16, 12: 16}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Gemma-4's two attention layer shapes (modeling/gemma4_common.mojo:10-20):
