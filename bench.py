@@ -1061,6 +1061,8 @@ class PrefillSliding:
 
     def __init__(self, seed: int, window: int, kv: str = "bf16"):
         self.seed, self.window, self.bq = seed, window, kv == "bq"
+        self.nq, self.nkv, self.hd, self.half, self.pair = NUM_Q, NUM_KV, HEAD_DIM, 128, 128
+        self.kvs = KV_STRIDE
         self.prefix = uniform_ints(seed, 8, 0, 16384)
         self.new = 2048
         if self.bq:

@@ -306,17 +306,25 @@ static int64_t reuse_panel_pu(int64_t head_dim, int64_t gqa) {
 
 static float bf16_dot_vdpbf16(const uint16_t* k_row, const uint16_t* x_row,
                               int64_t cols, int64_t pu) {
+    /* One 32-bit load holds a (even, odd) bf16 pair, as a VDPBF16PS lane
+     * reads it: the odd element is the high half (bits & 0xFFFF0000 as f32),
+     * the even one the low half (bits << 16).  The lanes are independent,
+     * so the j loops vectorise without changing any lane's order. */
     float acc[8][W];
-    memset(acc, 0, sizeof(acc));
+    for (int64_t p = 0; p < pu; p++)
+        for (int j = 0; j < W; j++) acc[p][j] = 0.0f;
     int64_t stride = pu * 2 * W;
+    const uint32_t* k32 = (const uint32_t*)k_row;
+    const uint32_t* x32 = (const uint32_t*)x_row;
     for (int64_t i = 0; i < cols / stride; i++) {
         for (int64_t p = 0; p < pu; p++) {
-            int64_t off = i * stride + p * 2 * W;
+            int64_t off = (i * stride + p * 2 * W) / 2;
             for (int j = 0; j < W; j++) {
-                float xo = ifo_bf16_to_f32(x_row[off + 2 * j + 1]);
-                float ko = ifo_bf16_to_f32(k_row[off + 2 * j + 1]);
-                float xe = ifo_bf16_to_f32(x_row[off + 2 * j]);
-                float ke = ifo_bf16_to_f32(k_row[off + 2 * j]);
+                uint32_t xp = x32[off + j], kp = k32[off + j];
+                float xo = bits_to_f32(xp & 0xFFFF0000u);
+                float ko = bits_to_f32(kp & 0xFFFF0000u);
+                float xe = bits_to_f32(xp << 16);
+                float ke = bits_to_f32(kp << 16);
                 float a = acc[p][j];
                 a = a + xo * ko;
                 a = a + xe * ke;
@@ -434,13 +442,14 @@ static void process_tile(const attn_ctx* c, const attn_item* it,
         }
         for (int64_t t = 0; t < tile_len; t++) {
             if (!c->is_bq) {
+                /* Each accumulator element takes one fma per key; the
+                 * (r, j) loop order does not change any element's chain. */
                 const uint16_t* v_head = c->v + slots[t] * c->kv_stride + head_off;
-                for (int64_t j = 0; j < D; j++) {
-                    float vv = ifo_bf16_to_f32(v_head[j]);
-                    for (int64_t r = 0; r < c->gqa; r++) {
-                        float* a = acc + (base_q + r) * D + j;
-                        *a = fmaf(vv, weights[t * c->gqa + r], *a);
-                    }
+                for (int64_t r = 0; r < c->gqa; r++) {
+                    float wr = weights[t * c->gqa + r];
+                    float* a = acc + (base_q + r) * D;
+                    for (int64_t j = 0; j < D; j++)
+                        a[j] = fmaf(bits_to_f32((uint32_t)v_head[j] << 16), wr, a[j]);
                 }
             } else {
                 const int8_t* v_head = c->vi + slots[t] * c->kv_stride + head_off;
@@ -450,12 +459,10 @@ static void process_tile(const attn_ctx* c, const attn_item* it,
                     float w = weights[t * c->gqa + r] * vs;
                     wts[r] = w * inv127;
                 }
-                for (int64_t j = 0; j < D; j++) {
-                    float vv = (float)v_head[j];
-                    for (int64_t r = 0; r < c->gqa; r++) {
-                        float* a = acc + (base_q + r) * D + j;
-                        *a = fmaf(vv, wts[r], *a);
-                    }
+                for (int64_t r = 0; r < c->gqa; r++) {
+                    float* a = acc + (base_q + r) * D;
+                    for (int64_t j = 0; j < D; j++)
+                        a[j] = fmaf((float)v_head[j], wts[r], a[j]);
                 }
             }
         }

@@ -34,7 +34,35 @@ def compare_bf16(got_bits, ref_bits, tol: float = 1e-2) -> dict:
         "n_over_tol": int((d > tol).sum()),
         "n_fail": int((d > allowed).sum()),
         "n_nan": int(np.isnan(a).sum()),
+        "n": int(d.size),
     }
+
+
+# How many outputs may sit beyond 1e-2 (each within one bf16 spacing, so only
+# where |x| >= 2).  A kernel whose f32 result is not the reference's bit for
+# bit (MFMA sums in the matrix core's order, P in bf16 parts, the fused-FMA
+# exp) lands on the neighbouring bf16 value when the two f32 results straddle
+# a rounding boundary; the MFMA prefill tests measured up to about 1e-5 of
+# their outputs doing so.  The cap is twice that plus a fixed margin of 8 for
+# the small cases, so a change that moves many outputs by one spacing fails.
+OVER_TOL_FIXED = 8
+OVER_TOL_FRAC = 2e-5
+
+
+def over_tol_cap(n: int) -> int:
+    return OVER_TOL_FIXED + int(OVER_TOL_FRAC * n)
+
+
+def assert_bar(r: dict, label: str = "", strict: bool = False) -> dict:
+    """Print the comparison and hold it to the bar: no NaN, every output within
+    1e-2 or one bf16 spacing, and at most over_tol_cap(n) outputs beyond 1e-2
+    (none when strict)."""
+    cap = 0 if strict else over_tol_cap(r["n"])
+    print(f"  {label}: n_over_tol={r['n_over_tol']} (cap {cap}) of {r['n']}, "
+          f"max_abs={r['max_abs']:.6g}, n_fail={r['n_fail']}", flush=True)
+    assert r["n_nan"] == 0 and r["n_fail"] == 0, (label, r)
+    assert r["n_over_tol"] <= cap, (label, r, cap)
+    return r
 
 
 @dataclass

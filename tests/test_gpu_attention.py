@@ -10,7 +10,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, compare_bf16,
+from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, assert_bar, compare_bf16,
                            make_decode_case, make_prefill_case, seeded_bf16)
 
 pytestmark = pytest.mark.gpu
@@ -45,10 +45,7 @@ def _run_attention(kind, runs, rows, q, k, v, *, seq_len, cap, window=0, cache_s
 
 
 def _assert_close(got, ref, what):
-    r = compare_bf16(got, ref)
-    print(f"  {what}: max_abs={r['max_abs']:.3g} over_1e-2={r['n_over_tol']} fail={r['n_fail']}",
-          flush=True)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, (what, r)
+    assert_bar(compare_bf16(got, ref), what)
 
 
 @pytest.mark.parametrize("cap", [1, 3, 64, 96, 128, 512])

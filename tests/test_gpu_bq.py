@@ -10,7 +10,7 @@ from inferno_amd import attention as A
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests import bq_schedule as bq
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, make_decode_case, seeded_bf16
+from tests.helpers import assert_bar, compare_bf16, make_decode_case, seeded_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -121,8 +121,7 @@ def test_reference_parity_schedule():
             window=bq.WINDOW, cache_size=bq.CACHE_SIZE, cache_rows=bq.CACHE_ROWS,
             cap=bq.POOL_WORKERS, seq_len=n, rope_half=bq.ROPE_HALF,
             pair_stride=bq.PAIR_STRIDE)
-        r = compare_bf16(got, ref)
-        assert r["n_fail"] == 0 and r["n_nan"] == 0, (step, r)
+        r = assert_bar(compare_bf16(got, ref), f"bq schedule step {step}")
         if not (plan.summary.mode == 1 and int(plan.info[14]) > 0):
             assert np.array_equal(got, ref), (step, r)  # bit-exact off the MFMA route
         worst_or = max(worst_or, r["max_abs"])
@@ -155,8 +154,7 @@ def test_prep_codes_bit_exact_with_rope_and_gains(rope_half, pair_stride):
                                     window=0, cache_size=64, cache_rows=case.cache_rows,
                                     cap=64, seq_len=n, rope_half=rope_half,
                                     pair_stride=pair_stride)
-    r = compare_bf16(got, ref)
-    assert r["n_fail"] == 0, r
+    assert_bar(compare_bf16(got, ref), "bq full layer prep + attention")
 
 
 @pytest.mark.parametrize("cap", [16, 512])
@@ -206,8 +204,7 @@ def test_bq_batched_decode_with_outliers(cap):
                                     cache_rows=case.cache_rows, cap=cap, seq_len=B,
                                     rope_half=128, pair_stride=128)
     r = compare_bf16(got, ref)
-    print(f"  bq decode cap={cap}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"bq decode cap={cap}")
     # Integer scores, the reference's softmax steps and summation orders, and
     # the merge's batch-of-16 halving tree: the outputs are the oracle's bits.
     assert np.array_equal(got, ref), r

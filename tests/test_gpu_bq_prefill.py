@@ -16,7 +16,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, make_prefill_case
+from tests.helpers import assert_bar, compare_bf16, make_prefill_case
 
 pytestmark = pytest.mark.gpu
 
@@ -104,16 +104,14 @@ def test_bq_sliding_prefill_windows(window):
     prefix, new = [0, 5, max(0, window - 3), 700, 3000], [100, 64, 129, 77, 200]
     ring = 1 << int(np.ceil(np.log2((window + max(new) + 128) / 64)))
     r = _run(window, prefix, new, ring, 64, window, quant=window == 1024)
-    print(f"  window {window}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"window {window}")
 
 
 def test_bq_sliding_prefill_diffuse():
     """f_q scaled by 1/16: attention spreads over the window."""
     announce("bq mfma sliding prefill diffuse")
     r = _run(1024, [0, 1500, 4000], [130, 64, 190], 32, 64, 7, q_scale=1.0 / 16)
-    print(f"  diffuse: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "diffuse")
 
 
 @pytest.mark.parametrize("page_len,ring", [(8, 512), (1024, 2)])
@@ -121,8 +119,7 @@ def test_bq_sliding_prefill_page_sizes(page_len, ring):
     """8-row pages and Gemma-4's 1024-token pages on 2-page rings."""
     announce(f"bq mfma sliding prefill page_len={page_len}")
     r = _run(1024, [0, 900, 2500], [96, 129, 64], ring, page_len, 11)
-    print(f"  page_len {page_len}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"page_len {page_len}")
 
 
 def _run_full(prefix, new, page_len, seed, quant=False):
@@ -173,13 +170,11 @@ def test_bq_full_layer_prefill():
     quant on top."""
     announce("bq mfma full-layer prefill")
     r = _run_full([0, 100, 1000, 3000, 63, 5], [40, 33, 100, 64, 1, 7], 64, 21, quant=True)
-    print(f"  full layer: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "full layer")
 
 
 @pytest.mark.parametrize("page_len", [8, 1024])
 def test_bq_full_layer_prefill_page_sizes(page_len):
     announce(f"bq mfma full-layer prefill page_len={page_len}")
     r = _run_full([0, 900, 2500], [96, 129, 64], page_len, 23)
-    print(f"  full layer page_len {page_len}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"full layer page_len {page_len}")

@@ -21,7 +21,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, make_decode_case, make_prefill_case, seeded_bf16
+from tests.helpers import assert_bar, compare_bf16, make_decode_case, make_prefill_case, seeded_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -121,10 +121,8 @@ def _bf16_attention(case, seq_len, cap, seed):
     ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=NQ, num_kv=NKV,
                            head_dim=D, kv_stride=KVS, window=0, cache_size=PAGE,
                            page_len=PAGE, seq_len=seq_len, cap=cap, threads=8)
-    r = compare_bf16(got, ref)
-    print(f"  mode={plan.summary.mode} items={plan.summary.num_items} "
-          f"stripes={plan.summary.num_stripes}: {r}", flush=True)
-    return r
+    return assert_bar(compare_bf16(got, ref), f"mode={plan.summary.mode} "
+                      f"items={plan.summary.num_items} stripes={plan.summary.num_stripes}")
 
 
 @pytest.mark.parametrize("cap", [1, 16, 256, 1024, 4096])
@@ -136,16 +134,14 @@ def test_full_layer_decode(cap):
     rng = np.random.default_rng(100 + cap)
     ctx = [int(x) for x in rng.integers(1, 3000, 6)] + [0, 15, 16, 17]
     case = make_decode_case(200 + cap, ctx)
-    r = _bf16_attention(case, len(ctx), cap, 300 + cap)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, r
+    _bf16_attention(case, len(ctx), cap, 300 + cap)
 
 
 def test_full_layer_single_sequence():
     """seq_len 1 routes through recommended_workers (config-1-like)."""
     announce("full layer single sequence")
     case = make_decode_case(41, [4095])
-    r = _bf16_attention(case, 1, 128, 42)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, r
+    _bf16_attention(case, 1, 128, 42)
 
 
 def test_full_layer_token_prefill():
@@ -153,8 +149,7 @@ def test_full_layer_token_prefill():
     test_gpu_prefill_wide.py covers it in depth)."""
     announce("full layer token prefill")
     case = make_prefill_case(9, [0, 300, 77], [20, 45, 33])
-    r = _bf16_attention(case, 98, 16, 80)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, r
+    _bf16_attention(case, 98, 16, 80)
 
 
 class _BqCache:
@@ -231,11 +226,11 @@ def _bq_step(cache, runs, rows, cache_rows, seq_len, cap, q, kraw, gq, gk, cos, 
                               cap=cap, threads=8)
     r = compare_bf16(got, ref)
     mfma = plan.summary.mode == 2 and int(plan.info[14]) > 0
-    print(f"  bq mode={plan.summary.mode} stripes={plan.summary.num_stripes} mfma={mfma}: {r}",
-          flush=True)
+    label = f"bq mode={plan.summary.mode} stripes={plan.summary.num_stripes} mfma={mfma}"
     if mfma:  # the MFMA prefill: the bf16 prefill's bar
-        assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+        assert_bar(r, label)
     else:
+        print(f"  {label}: {r}", flush=True)
         assert np.array_equal(got, ref), r
     assert np.array_equal(from_dev(out2, np.uint16), got), "fused quant changed the output"
     want_i8, want_sa = oracle.bq_block_quant(got, cols=NQ * D, block=D)

@@ -14,7 +14,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, make_decode_case, make_prefill_case, seeded_bf16
+from tests.helpers import assert_bar, compare_bf16, make_decode_case, make_prefill_case, seeded_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -64,10 +64,8 @@ def _attend(kind, runs, rows, cache_rows, seq_len, shape, cap, seed):
     ref = oracle.attention(kind, runs, rows, q, k, v, num_q=nq, num_kv=nkv, head_dim=d,
                            kv_stride=kvs, window=WINDOW, cache_size=cache_size, page_len=PAGE,
                            seq_len=seq_len, cap=cap, threads=16)
-    r = compare_bf16(got, ref)
-    print(f"  mode={plan.summary.mode} items={plan.summary.num_items} "
-          f"qblocks={int(plan.info[14])}: {r}", flush=True)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, r
+    assert_bar(compare_bf16(got, ref), f"mode={plan.summary.mode} "
+               f"items={plan.summary.num_items} qblocks={int(plan.info[14])}")
 
 
 @pytest.mark.parametrize("layer", ["sliding", "full"])

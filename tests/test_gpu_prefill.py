@@ -9,8 +9,8 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, compare_bf16,
-                           make_prefill_case, seeded_bf16)
+from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, assert_bar,
+                           compare_bf16, make_prefill_case, seeded_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -50,8 +50,7 @@ def test_prefill_small_all_tokens():
                            cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n, cap=16,
                            threads=8)
     r = compare_bf16(got, ref)
-    print(f"  prefill small: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "prefill small")
 
 
 def test_prefill_diffuse_scores():
@@ -74,8 +73,7 @@ def test_prefill_diffuse_scores():
                            cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n, cap=16,
                            threads=8)
     r = compare_bf16(got, ref)
-    print(f"  prefill diffuse: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "prefill diffuse")
 
 
 @pytest.mark.parametrize("page_len", [8, 128])
@@ -96,8 +94,7 @@ def test_prefill_page_sizes(page_len):
                            cache_size=page_len, page_len=page_len, seq_len=n, cap=16,
                            threads=8)
     r = compare_bf16(got, ref)
-    print(f"  prefill page_len={page_len}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"prefill page_len={page_len}")
 
 
 def test_prefill_config4_shape_append_then_attend():
@@ -156,5 +153,4 @@ def test_prefill_config4_shape_append_then_attend():
                            seq_len=len(picks), cap=2, threads=16)
     sel = np.concatenate([got[r * 2048 + t] for r, t in picks])
     res = compare_bf16(sel, ref)
-    print(f"  config4 sampled tokens: {res}", flush=True)
-    assert res["n_fail"] == 0 and res["n_nan"] == 0, res
+    assert_bar(res, "config4 sampled tokens")

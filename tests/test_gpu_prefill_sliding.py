@@ -11,8 +11,8 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, compare_bf16,
-                           seeded_bf16)
+from tests.helpers import (HEAD_DIM, KV_STRIDE, NUM_KV, NUM_Q, PAGE_LEN, assert_bar,
+                           compare_bf16, seeded_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -75,8 +75,7 @@ def test_sliding_prefill_windows(window):
     v = seeded_bf16(cache_rows * KV_STRIDE, 3)
     got = _run(runs, rows, cache_rows, n, window, ring, q, k, v)
     r = compare_bf16(got, _ref(runs, rows, n, window, ring, q, k, v))
-    print(f"  window {window} ring {ring}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"window {window} ring {ring}")
 
 
 def test_sliding_prefill_diffuse_scores():
@@ -93,8 +92,7 @@ def test_sliding_prefill_diffuse_scores():
     v = seeded_bf16(cache_rows * KV_STRIDE, 10)
     got = _run(runs, rows, cache_rows, n, 1024, 32, q, k, v)
     r = compare_bf16(got, _ref(runs, rows, n, 1024, 32, q, k, v))
-    print(f"  diffuse: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "diffuse")
 
 
 @pytest.mark.parametrize("page_len,ring_pages", [(8, 512), (1024, 4)])
@@ -110,8 +108,7 @@ def test_sliding_prefill_page_sizes(page_len, ring_pages):
     v = seeded_bf16(cache_rows * KV_STRIDE, 14)
     got = _run(runs, rows, cache_rows, n, 1024, ring_pages, q, k, v, page_len)
     r = compare_bf16(got, _ref(runs, rows, n, 1024, ring_pages, q, k, v, page_len))
-    print(f"  page_len {page_len}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"page_len {page_len}")
 
 
 def test_sliding_prefill_chunk_8x2048_append_then_attend():
@@ -167,5 +164,4 @@ def test_sliding_prefill_chunk_8x2048_append_then_attend():
                            seq_len=len(picks), cap=2, threads=16)
     sel = np.concatenate([got[r * 2048 + t] for r, t in picks])
     res = compare_bf16(sel, ref)
-    print(f"  8 x 2048 sampled tokens: {res}", flush=True)
-    assert res["n_fail"] == 0 and res["n_nan"] == 0, res
+    assert_bar(res, "8 x 2048 sampled tokens")

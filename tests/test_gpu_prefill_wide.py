@@ -13,7 +13,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, make_prefill_case, seeded_bf16
+from tests.helpers import assert_bar, compare_bf16, make_prefill_case, seeded_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -60,8 +60,7 @@ def test_wide_prefill_small_all_tokens():
     n = sum(new)
     r = _prefill(case, n, seeded_bf16(n * NQ * D, 1), seeded_bf16(case.cache_rows * KVS, 2),
                  seeded_bf16(case.cache_rows * KVS, 3))
-    print(f"  wide prefill small: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "wide prefill small")
 
 
 def test_wide_prefill_diffuse_scores():
@@ -77,8 +76,7 @@ def test_wide_prefill_diffuse_scores():
     q = ((u + ((u >> 16) & 1) + 0x7FFF) >> 16).astype(np.uint16)
     r = _prefill(case, n, q, seeded_bf16(case.cache_rows * KVS, 9),
                  seeded_bf16(case.cache_rows * KVS, 10))
-    print(f"  wide prefill diffuse: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "wide prefill diffuse")
 
 
 @pytest.mark.parametrize("page_len", [8, 1024])
@@ -91,8 +89,7 @@ def test_wide_prefill_page_sizes(page_len):
     n = sum(new)
     r = _prefill(case, n, seeded_bf16(n * NQ * D, 12), seeded_bf16(case.cache_rows * KVS, 13),
                  seeded_bf16(case.cache_rows * KVS, 14), page_len=page_len)
-    print(f"  wide prefill page_len {page_len}: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, f"wide prefill page_len {page_len}")
 
 
 def test_wide_prefill_long_run_takes_token_route():
@@ -104,8 +101,7 @@ def test_wide_prefill_long_run_takes_token_route():
     n = sum(new)
     r = _prefill(case, n, seeded_bf16(n * NQ * D, 16), seeded_bf16(case.cache_rows * KVS, 17),
                  seeded_bf16(case.cache_rows * KVS, 18), page_len=8)
-    print(f"  wide prefill long run: {r}", flush=True)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
+    assert_bar(r, "wide prefill long run")
 
 
 def test_wide_prefill_8x2048_append_then_attend():
@@ -157,5 +153,4 @@ def test_wide_prefill_8x2048_append_then_attend():
                            cache_size=64, page_len=64, seq_len=len(picks), cap=1, threads=16)
     sel = np.concatenate([got[r * 2048 + t] for r, t in picks])
     res = compare_bf16(sel, ref)
-    print(f"  wide prefill 8 x 2048 sampled tokens: {res}", flush=True)
-    assert res["n_fail"] == 0 and res["n_nan"] == 0, res
+    assert_bar(res, "wide prefill 8 x 2048 sampled tokens")

@@ -14,7 +14,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, seeded_bf16
+from tests.helpers import assert_bar, compare_bf16, seeded_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -95,10 +95,8 @@ def test_random_plan(seed):
     ref = oracle.attention(c["kind"], runs, rows, q, k, v, num_q=nq, num_kv=nkv, head_dim=d,
                            kv_stride=kvs, window=c["window"], cache_size=cache_size,
                            page_len=pl, seq_len=n, cap=c["cap"], threads=16)
-    r = compare_bf16(got, ref)
-    print(f"  mode={plan.summary.mode} items={plan.summary.num_items} "
-          f"qblocks={int(plan.info[14])}: {r}", flush=True)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, (c, r)
+    assert_bar(compare_bf16(got, ref), f"{c} mode={plan.summary.mode} "
+               f"items={plan.summary.num_items} qblocks={int(plan.info[14])}")
 
 
 def _codes(n, rng):
@@ -144,8 +142,6 @@ def test_random_bq_plan(seed):
                               threads=16)
     r = compare_bf16(got, ref)
     mfma = int(plan.info[14]) > 0 and plan.summary.mode in (1, 2)
-    print(f"  mode={plan.summary.mode} items={plan.summary.num_items} mfma={mfma}: {r}",
-          flush=True)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, (c, r)
+    assert_bar(r, f"{c} mode={plan.summary.mode} items={plan.summary.num_items} mfma={mfma}")
     if not mfma:
         assert np.array_equal(got, ref), (c, r)

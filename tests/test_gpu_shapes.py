@@ -11,7 +11,8 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, SLIDING, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import PAGE_LEN, compare_bf16, make_decode_case, make_prefill_case, seeded_bf16
+from tests.helpers import (PAGE_LEN, assert_bar, compare_bf16, make_decode_case,
+                           make_prefill_case, seeded_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -45,9 +46,8 @@ def _check(kind, runs, rows, cache_rows, seq_len, shape, cap, seed, window=0,
     ref = oracle.attention(kind, runs, rows, q, k, v, num_q=nq, num_kv=nkv, head_dim=d,
                            kv_stride=kvs, window=window, cache_size=cache_size,
                            page_len=PAGE_LEN, seq_len=seq_len, cap=cap, threads=8)
-    r = compare_bf16(got, ref)
-    print(f"  mode={plan.summary.mode} stripes={plan.summary.num_stripes}: {r}", flush=True)
-    assert r["n_nan"] == 0 and r["n_fail"] == 0, r
+    assert_bar(compare_bf16(got, ref),
+               f"mode={plan.summary.mode} stripes={plan.summary.num_stripes}")
 
 
 @pytest.mark.parametrize("shape", SHAPES)

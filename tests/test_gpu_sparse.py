@@ -14,7 +14,7 @@ import oracle
 from inferno_amd import attention as A
 from inferno_amd.kv import FULL, AttentionPlan, KVRunTable
 from tests.gpu_util import announce, empty_dev, from_dev, to_dev
-from tests.helpers import compare_bf16, make_decode_case
+from tests.helpers import assert_bar, compare_bf16, make_decode_case
 
 pytestmark = pytest.mark.gpu
 
@@ -153,9 +153,7 @@ def _check_sparse(plan, runs, rows, q, k, v, bi, page_len):
     want = oracle.block_sparse_attention(runs, rows, q, k, v, bi, num_q=NUM_Q, num_kv=NUM_KV,
                                          head_dim=HD, kv_stride=KV_STRIDE, block_size=BLOCK,
                                          topk=TOPK, page_len=page_len, seq_len=seq)
-    r = compare_bf16(got, want)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
-    return r
+    return assert_bar(compare_bf16(got, want), f"sparse seq={seq} page_len={page_len}")
 
 
 @pytest.mark.parametrize("page_len", [64, 128])
@@ -237,9 +235,7 @@ def _check_bq_sparse(plan, runs, rows, inputs, bi, page_len, cap):
                                             num_q=NUM_Q, num_kv=NUM_KV, head_dim=HD,
                                             kv_stride=KV_STRIDE, block_size=BLOCK, topk=TOPK,
                                             page_len=page_len, seq_len=seq, cap=cap)
-    r = compare_bf16(got, want)
-    assert r["n_fail"] == 0 and r["n_nan"] == 0, r
-    return r
+    return assert_bar(compare_bf16(got, want), f"sparse seq={seq} page_len={page_len}")
 
 
 @pytest.mark.parametrize("cap", [1, 7, 64])
