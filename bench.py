@@ -71,6 +71,84 @@ def host_cpu() -> dict:
             "threads": max(1, min(CPU_SHARE, avail))}
 
 
+# The CPU baseline's method: CPU_WARMUP untimed calls,
+# then CPU_ITERS timed calls of the same sample; the median is reported.
+CPU_WARMUP, CPU_ITERS = 5, 30
+
+
+def cpu_oracle():
+    """The oracle build the CPU baseline times: the -march=native build (AVX-512,
+    with VDPBF16PS and VPDPBUSD dots where the host has AVX-512 BF16 / VNNI, as
+    the reference's own kernels use them), built on this host; the portable
+    x86-64-v3 build if that fails.  Returns (handle, label)."""
+    import oracle
+
+    try:
+        return oracle.native_lib(), "native (-march=native)"
+    except Exception as e:  # no compiler, or a host gcc cannot target
+        return oracle.lib(), f"portable x86-64-v3 (native build failed: {e})"
+
+
+def _same(a, b) -> bool:
+    if isinstance(a, tuple):
+        return all(_same(x, y) for x, y in zip(a, b))
+    return a is None or np.array_equal(a, b)
+
+
+def cpu_sample(make, n_max: int, cost, budget_s: float, n0: int) -> dict:
+    """Size, check and time the CPU baseline's sample.
+
+    make(n) returns a call over the first n units of the workload (sequences,
+    query tokens, jobs or rows) that returns its output; cost(n) is their
+    algorithmic work.  One calibration call on n0 units runs through the
+    portable build and through the timed build, whose outputs must agree bit
+    for bit (else the portable build is timed); the sample is then the largest
+    n <= n_max whose CPU_WARMUP + CPU_ITERS calls fit budget_s at the
+    calibrated rate, and its median call time is returned."""
+    import oracle
+
+    handle, label = cpu_oracle()
+    fn0 = make(n0)
+    ref = fn0()
+    with oracle.using(handle):
+        t0 = time.perf_counter()
+        out = fn0()
+        dt = max(time.perf_counter() - t0, 1e-6)
+    identical = _same(ref, out)
+    if not identical:
+        handle, label = oracle.lib(), "portable x86-64-v3 (the native build's output differed)"
+    rate = cost(n0) / dt
+    per_call = budget_s / (CPU_WARMUP + CPU_ITERS)
+    lo, hi = n0, n_max
+    while lo < hi:  # the largest n whose estimated call fits per_call
+        mid = (lo + hi + 1) // 2
+        if cost(mid) / rate <= per_call:
+            lo = mid
+        else:
+            hi = mid - 1
+    n = lo
+    fn = fn0 if n == n0 else make(n)
+    del fn0
+    with oracle.using(handle):
+        for _ in range(CPU_WARMUP):
+            fn()
+        times = []
+        for _ in range(CPU_ITERS):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+    return {"n": n, "median": statistics.median(times), "build": label,
+            "native_bit_identical": identical, "calls": f"median of {CPU_ITERS} timed calls "
+            f"after {CPU_WARMUP} warm-up calls"}
+
+
+def cpu_result(hc, value, unit, cores, t, sample, **extra) -> dict:
+    return {"value": value, "unit": unit, "cores": cores, "kind": "port",
+            **{k: hc[k] for k in ("cpu_model", "logical_cpus", "affinity_cpus")},
+            "build": t["build"], "native_bit_identical": t["native_bit_identical"],
+            "sample": f"{sample}, {t['calls']}", **extra}
+
+
 def splitmix64(x: int) -> int:
     z = (x + 0x9E3779B97F4A7C15) & MASK64
     z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & MASK64
@@ -100,6 +178,65 @@ def _fill(t, seed, sid, outlier_every=0, scale=1.0):
 
     check(lib().ifr_fill_normal_bf16(t.data_ptr(), t.numel() * t.element_size() // 2, seed,
                                      outlier_every, scale, sid))
+
+
+def bq_quantize_cache(w, dev, spans, *, kind: int, cache_size: int, cache_rows: int,
+                      v_is_k: bool, seed: int, chunk_tokens: int = 1 << 18) -> None:
+    """Fill a butterquant cache the way the configuration produces it: every
+    cached position's K and V rows, drawn N(0,1) with every 100th element x20
+    (1 % outliers), go through the quantizing append (ifr_bq_attn_prep: RMS
+    norm and RoPE of K, FWHT, absmax int8 codes and f32 scales;
+    butterquant_kernels/attention.mojo:494-632) at their own positions.
+
+    spans: (first position, count, page list) per sequence; the positions land
+    where the page list (a ring when kind is sliding) puts them.  v_is_k: the
+    full-attention layer's V is its raw K projection
+    (modeling/gemma_4_moe_bq.mojo:566-573).  Untimed set-up work."""
+    import torch
+
+    from inferno_amd.kv import AttentionPlan, KVRunTable
+
+    sid = int(torch.cuda.current_stream().cuda_stream)
+    todo = [(p0, n, pages) for p0, n, pages in spans if n > 0]
+    while todo:
+        batch, tok = [], 0
+        while todo and (not batch or tok + todo[0][1] <= chunk_tokens):
+            p0, n, pages = todo.pop(0)
+            if n > chunk_tokens:  # split a long span
+                todo.insert(0, (p0 + chunk_tokens, n - chunk_tokens, pages))
+                n = chunk_tokens
+            batch.append((p0, n, pages))
+            tok += n
+        table = KVRunTable()
+        buf = 0
+        for p0, n, pages in batch:
+            table.begin_run(buf, p0)
+            for pg in pages:
+                table.add_base_row(int(pg) * PAGE_LEN)
+            buf += n
+        plan = AttentionPlan(table, tok, kind=kind, window=cache_size if kind == 0 else 0,
+                             cache_size=cache_size, page_len=PAGE_LEN, cache_rows=cache_rows,
+                             cap=16, kv_row_bytes=w.kvs, device=dev)
+        ksrc = torch.empty(tok * w.kvs, dtype=torch.int16, device=dev)
+        _fill(ksrc, seed, sid, outlier_every=100, scale=20.0)
+        if v_is_k:
+            vsrc = ksrc
+        else:
+            vsrc = torch.empty_like(ksrc)
+            _fill(vsrc, seed + 1, sid, outlier_every=100, scale=20.0)
+        seed += 2
+        qsrc = torch.zeros(tok * w.nq * w.hd, dtype=torch.int16, device=dev)
+        qi = torch.empty(tok * w.nq * w.hd, dtype=torch.int8, device=dev)
+        qb = torch.empty(tok * w.nq, dtype=torch.float32, device=dev)
+        gain = torch.full((w.hd,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
+        w.A.dispatch_bq_attn_prep(plan, qsrc, ksrc, vsrc, gain, gain, qi, qb, torch.empty_like(qb),
+                                  w.bq_k, w.bq_ks, w.bq_v, w.bq_vs, w.cos, w.sin, num_q=w.nq,
+                                  num_kv=w.nkv, head_dim=w.hd, rope_half=w.half,
+                                  pair_stride=w.pair,
+                                  sqrt_n=float(np.sqrt(np.float32(w.hd))),
+                                  n_eps=float(np.float32(w.hd) * np.float32(1e-6)))
+        torch.cuda.synchronize()
+        del ksrc, vsrc, qsrc, qi, qb, plan
 
 
 class CopyStager:
@@ -344,54 +481,61 @@ class DecodeBf16:
                 "plan_items": self.plan.summary.num_items, "layer_caches": self.layers}
 
     def cpu_baseline(self, budget_s):
+        """The oracle (FlashAttentionKernel + merge_segments under the
+        reference's routing, cap = worker threads) on the first n sequences of
+        the batch, their pages copied into a compact host cache; n is the whole
+        batch when its timed calls fit the budget."""
         import torch
 
         import oracle
 
         hc = host_cpu()
         threads = hc["threads"]
-        n_seq = min(len(self.pos), max(threads, 8))
         kc, vc = self.kl[self.layer]
-        pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
-        idx = torch.from_numpy(pages.astype(np.int64)).to(kc.device)
-        kp = kc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
-        vp = vc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
-        kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
-        vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
-        runs, rows, off = [], [], 0
-        for i in range(n_seq):
-            n = len(self.pages[i])
-            runs.append([i, self.pos[i], off, n])
-            rows.extend((off + j) * PAGE_LEN for j in range(n))
-            off += n
-        runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
-        q = np.ascontiguousarray(self.q_host[:n_seq * self.nq * self.hd])
-        sample_pos = self.kv_positions(self.pos[:n_seq])
-        nbytes = sample_pos * self.kvs * 4
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.attention(self.kind, runs, rows, q, kp, vp, num_q=self.nq, num_kv=self.nkv,
-                             head_dim=self.hd, kv_stride=self.kvs, window=self.window,
-                             cache_size=self.cache_size, page_len=PAGE_LEN, seq_len=n_seq,
-                             cap=threads, threads=threads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
-                           f"({nbytes / 1e9:.3f} GB of K+V), the reference's routing at "
-                           f"cap={threads} workers, median of {len(times)}"),
-                "us_per_layer_equiv": round(med * 1e6 * self.kv_positions() / sample_pos, 1)}
+        B = len(self.pos)
 
+        def make(n):
+            pages = np.concatenate([np.asarray(p) for p in self.pages[:n]])
+            idx = torch.from_numpy(pages.astype(np.int64)).to(kc.device)
+            kp = kc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
+            vp = vc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
+            kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
+            vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
+            runs, rows, off = [], [], 0
+            for i in range(n):
+                m = len(self.pages[i])
+                runs.append([i, self.pos[i], off, m])
+                rows.extend((off + j) * PAGE_LEN for j in range(m))
+                off += m
+            runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
+            q = np.ascontiguousarray(self.q_host[:n * self.nq * self.hd])
+            return lambda: oracle.attention(
+                self.kind, runs, rows, q, kp, vp, num_q=self.nq, num_kv=self.nkv,
+                head_dim=self.hd, kv_stride=self.kvs, window=self.window,
+                cache_size=self.cache_size, page_len=PAGE_LEN, seq_len=n, cap=threads,
+                threads=threads)
+
+        def cost(n):
+            return self.kv_positions(self.pos[:n]) * self.kvs * 4
+
+        t = cpu_sample(make, B, cost, budget_s, min(B, threads))
+        n, med = t["n"], t["median"]
+        nbytes = cost(n)
+        scope = ("the whole batch" if n == B else
+                 f"the first {n} of the {B} sequences, extrapolated to the batch by K/V bytes")
+        return cpu_result(hc, round(nbytes / med / 1e9, 3), "GB/s", threads, t,
+                          f"{scope} ({nbytes / 1e9:.3f} GB of K+V), the reference's routing "
+                          f"at cap={threads} workers",
+                          us_per_layer_equiv=round(med * 1e6 * cost(B) / nbytes, 1))
 
 class DecodeBq:
     """Configs 5 and 8: butterquant int8 KV -- quantizing append + int8 decode +
     merge."""
 
     dtype = "int8 KV (f32 scales), f32 accumulate"
+    data = ("synthetic: seeded SplitMix64/Box-Muller N(0,1) K/V with every 100th element x20 "
+            "(1 % outliers), the cached positions quantized through the bq append (RMS norm, "
+            "RoPE, FWHT, absmax int8 codes + f32 scales) at set-up, on device")
     phases = ("append", "attention")
     graph = True
     dominant = "bq_partial_kernel<2> + merge_kernel<256>"
@@ -441,14 +585,18 @@ class DecodeBq:
             off += n
         self.stream = torch.cuda.current_stream()
         sid = int(self.stream.cuda_stream)
-        self.kc = torch.empty(rows * self.kvs, dtype=torch.int8, device=dev)
-        self.vc = torch.empty_like(self.kc)
-        _fill(self.kc, self.seed * 16 + 1, sid)
-        _fill(self.vc, self.seed * 16 + 2, sid)
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(self.seed)
-        self.ksc = torch.rand(rows * self.nkv, device=dev, generator=gen) * 4 + 0.5
-        self.vsc = torch.rand(rows * self.nkv, device=dev, generator=gen) * 4 + 0.5
+        self.kc = torch.zeros(rows * self.kvs, dtype=torch.int8, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        self.ksc = torch.zeros(rows * self.nkv, dtype=torch.float32, device=dev)
+        self.vsc = torch.zeros_like(self.ksc)
+        cos, sin = rope_tables(max(self.pos) + 2, half=self.half)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        # The cached positions 0 .. pos-1 of every sequence, quantized through
+        # the append path from N(0,1) K/V with 1 % outliers x20.
+        self.bq_k, self.bq_ks, self.bq_v, self.bq_vs = self.kc, self.ksc, self.vc, self.vsc
+        bq_quantize_cache(self, dev, [(0, p, pg) for p, pg in zip(self.pos, self.pages)],
+                          kind=1, cache_size=PAGE_LEN, cache_rows=rows, v_is_k=self.cfg == 8,
+                          seed=self.seed * 16 + 1)
         self.qs = torch.empty(B * self.nq * self.hd, dtype=torch.int16, device=dev)
         self.kss = torch.empty(B * self.kvs, dtype=torch.int16, device=dev)
         self.vss = torch.empty_like(self.kss)
@@ -456,8 +604,6 @@ class DecodeBq:
             _fill(t, self.seed * 16 + 3 + i, sid, outlier_every=100, scale=20.0)
         self.qn = torch.full((self.hd,), 0x3F80, dtype=torch.int16, device=dev)  # bf16 1.0
         self.kn = self.qn
-        cos, sin = rope_tables(max(self.pos) + 2, half=self.half)
-        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.q_i8 = torch.empty(B * self.nq * self.hd, dtype=torch.int8, device=dev)
         self.qb = torch.empty(B * self.nq, dtype=torch.float32, device=dev)
         self.fq = torch.empty_like(self.qb)
@@ -525,54 +671,56 @@ class DecodeBq:
 
     def cpu_baseline(self, budget_s):
         """The oracle's bq attention (bq_process_kv_tile and the merge, the
-        reference's routing) on the first sequences of the batch."""
+        reference's routing) on the first n sequences of the batch, n the whole
+        batch when its timed calls fit the budget."""
         import torch
 
         import oracle
 
         hc = host_cpu()
         threads = hc["threads"]
-        n_seq = min(len(self.pos), max(threads, 8))
-        pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
-        idx = torch.from_numpy(pages.astype(np.int64)).to(self.kc.device)
-        kp = self.kc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
-        vp = self.vc.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
-        ksp = self.ksc.view(-1, PAGE_LEN * self.nkv).index_select(0, idx).cpu().numpy()
-        vsp = self.vsc.view(-1, PAGE_LEN * self.nkv).index_select(0, idx).cpu().numpy()
-        kp, vp = (np.ascontiguousarray(x.reshape(-1)) for x in (kp, vp))
-        ksp, vsp = (np.ascontiguousarray(x.reshape(-1)) for x in (ksp, vsp))
-        runs, rows, off = [], [], 0
-        for i in range(n_seq):
-            n = len(self.pages[i])
-            runs.append([i, self.pos[i], off, n])
-            rows.extend((off + j) * PAGE_LEN for j in range(n))
-            off += n
-        runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
-        nq = n_seq * self.nq
-        q_i8 = np.ascontiguousarray(self.q_i8.cpu().numpy()[:nq * self.hd])
-        qb = np.ascontiguousarray(self.qb.cpu().numpy()[:nq])
-        fq = np.ascontiguousarray(self.fq.cpu().numpy()[:nq])
-        sample_pos = sum(p + 1 for p in self.pos[:n_seq])
-        nbytes = sample_pos * (self.kvs * 2 + self.nkv * 8)
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.bq_attention(1, runs, rows, q_i8, qb, fq, kp, ksp, vp, vsp, num_q=self.nq,
-                                num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs,
-                                window=0, cache_size=PAGE_LEN, page_len=PAGE_LEN,
-                                seq_len=n_seq, cap=threads, threads=threads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        total_pos = sum(p + 1 for p in self.pos)
-        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
-                           f"({nbytes / 1e9:.3f} GB of int8 K+V and scales), the reference's "
-                           f"bq routing at cap={threads} workers, median of {len(times)}"),
-                "us_per_layer_equiv": round(med * 1e6 * total_pos / sample_pos, 1)}
+        B = len(self.pos)
 
+        def make(n):
+            pages = np.concatenate([np.asarray(p) for p in self.pages[:n]])
+            idx = torch.from_numpy(pages.astype(np.int64)).to(self.kc.device)
+
+            def sel(t, per_row):
+                return np.ascontiguousarray(
+                    t.view(-1, PAGE_LEN * per_row).index_select(0, idx).cpu().numpy()
+                ).reshape(-1)
+
+            kp, vp = sel(self.kc, self.kvs), sel(self.vc, self.kvs)
+            ksp, vsp = sel(self.ksc, self.nkv), sel(self.vsc, self.nkv)
+            runs, rows, off = [], [], 0
+            for i in range(n):
+                m = len(self.pages[i])
+                runs.append([i, self.pos[i], off, m])
+                rows.extend((off + j) * PAGE_LEN for j in range(m))
+                off += m
+            runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
+            nq = n * self.nq
+            q_i8 = np.ascontiguousarray(self.q_i8.cpu().numpy()[:nq * self.hd])
+            qb = np.ascontiguousarray(self.qb.cpu().numpy()[:nq])
+            fq = np.ascontiguousarray(self.fq.cpu().numpy()[:nq])
+            return lambda: oracle.bq_attention(
+                1, runs, rows, q_i8, qb, fq, kp, ksp, vp, vsp, num_q=self.nq,
+                num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs, window=0,
+                cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n, cap=threads,
+                threads=threads)
+
+        def cost(n):
+            return sum(p + 1 for p in self.pos[:n]) * (self.kvs * 2 + self.nkv * 8)
+
+        t = cpu_sample(make, B, cost, budget_s, min(B, threads))
+        n, med = t["n"], t["median"]
+        nbytes = cost(n)
+        scope = ("the whole batch" if n == B else
+                 f"the first {n} of the {B} sequences, extrapolated to the batch by bytes")
+        return cpu_result(hc, round(nbytes / med / 1e9, 3), "GB/s", threads, t,
+                          f"{scope} ({nbytes / 1e9:.3f} GB of int8 K+V and scales), the "
+                          f"reference's bq routing at cap={threads} workers",
+                          us_per_layer_equiv=round(med * 1e6 * cost(B) / nbytes, 1))
 
 class SparseM3:
     """Config 6 (widening row, no BASELINE counterpart): MiniMax-M3 block-sparse
@@ -713,8 +861,9 @@ class SparseM3:
                 "layer_caches": self.layers}
 
     def cpu_baseline(self, budget_s):
-        """The oracle's indexer + sparse attention on the first sequences of the
-        batch, one thread (bf16 KV)."""
+        """The oracle's indexer + block-sparse attention (one thread: the
+        prototypes run them as single kernels) on the first n sequences of the
+        batch (bf16 KV), n sized to the budget."""
         import torch
 
         if self.kv == "bq":
@@ -722,45 +871,53 @@ class SparseM3:
 
         import oracle
 
-        n_seq = 4
-        pages = np.concatenate([np.asarray(p) for p in self.pages[:n_seq]])
-        idx = torch.from_numpy(pages.astype(np.int64)).to(self.k.device)
+        hc = host_cpu()
         P, kvs = self.PLEN, self.NKV * self.HD
-        ik = self.index_k.view(-1, P * self.HD).index_select(0, idx).cpu().numpy()
-        kp = self.k.view(-1, P * kvs).index_select(0, idx).cpu().numpy()
-        vp = self.v.view(-1, P * kvs).index_select(0, idx).cpu().numpy()
-        ik, kp, vp = (np.ascontiguousarray(x.view(np.uint16).reshape(-1)) for x in (ik, kp, vp))
-        runs, rows, off = [], [], 0
-        for i in range(n_seq):
-            n = len(self.pages[i])
-            runs.append([i, self.pos[i], off, n])
-            rows.extend((off + j) * P for j in range(n))
-            off += n
-        runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
-        iq = self.index_q.cpu().numpy().view(np.uint16)[:n_seq * self.IH * self.HD].copy()
-        q = self.q.cpu().numpy().view(np.uint16)[:n_seq * self.NQ * self.HD].copy()
         scale = float(np.float32(1.0) / np.sqrt(np.float32(self.HD)))
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 3 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            bi, _ = oracle.lightning_indexer(runs, rows, iq, ik, num_heads=self.IH,
-                                             head_dim=self.HD, block_size=self.BLOCK,
-                                             topk=self.TOPK, local_blocks=1, init_blocks=0,
-                                             scale=scale, page_len=P, seq_len=n_seq)
-            oracle.block_sparse_attention(runs, rows, q, kp, vp, bi, num_q=self.NQ,
-                                          num_kv=self.NKV, head_dim=self.HD, kv_stride=kvs,
-                                          block_size=self.BLOCK, topk=self.TOPK, page_len=P,
-                                          seq_len=n_seq)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        frac = n_seq / len(self.pos)
-        sample_bytes = self.step_bytes() * sum(self.pos[:n_seq]) / sum(self.pos)
-        return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
-                "kind": "port",
-                "sample": (f"first {n_seq} of the {len(self.pos)} sequences "
-                           f"({frac:.3f} of the batch by count), indexer + sparse attention, "
-                           f"one thread, median of {len(times)}")}
+        B = len(self.pos)
+
+        def make(n):
+            pages = np.concatenate([np.asarray(p) for p in self.pages[:n]])
+            idx = torch.from_numpy(pages.astype(np.int64)).to(self.k.device)
+            ik = self.index_k.view(-1, P * self.HD).index_select(0, idx).cpu().numpy()
+            kp = self.k.view(-1, P * kvs).index_select(0, idx).cpu().numpy()
+            vp = self.v.view(-1, P * kvs).index_select(0, idx).cpu().numpy()
+            ik, kp, vp = (np.ascontiguousarray(x.view(np.uint16).reshape(-1))
+                          for x in (ik, kp, vp))
+            runs, rows, off = [], [], 0
+            for i in range(n):
+                m = len(self.pages[i])
+                runs.append([i, self.pos[i], off, m])
+                rows.extend((off + j) * P for j in range(m))
+                off += m
+            runs, rows = np.asarray(runs, dtype=np.int32), np.asarray(rows, dtype=np.int32)
+            iq = self.index_q.cpu().numpy().view(np.uint16)[:n * self.IH * self.HD].copy()
+            q = self.q.cpu().numpy().view(np.uint16)[:n * self.NQ * self.HD].copy()
+
+            def call():
+                bi, _ = oracle.lightning_indexer(runs, rows, iq, ik, num_heads=self.IH,
+                                                 head_dim=self.HD, block_size=self.BLOCK,
+                                                 topk=self.TOPK, local_blocks=1,
+                                                 init_blocks=0, scale=scale, page_len=P,
+                                                 seq_len=n)
+                return bi, oracle.block_sparse_attention(
+                    runs, rows, q, kp, vp, bi, num_q=self.NQ, num_kv=self.NKV,
+                    head_dim=self.HD, kv_stride=kvs, block_size=self.BLOCK, topk=self.TOPK,
+                    page_len=P, seq_len=n)
+            return call
+
+        def cost(n):
+            return self.step_bytes() * sum(self.pos[:n]) / sum(self.pos)
+
+        t = cpu_sample(make, B, cost, budget_s, 1)
+        n, med = t["n"], t["median"]
+        nbytes = cost(n)
+        return cpu_result(hc, round(nbytes / med / 1e9, 3), "GB/s", 1, t,
+                          f"first {n} of the {B} sequences ({n / B:.3f} of the batch by "
+                          f"count, extrapolated by cached positions), indexer + sparse "
+                          f"attention, one thread",
+                          us_per_layer_equiv=round(med * 1e6 * sum(self.pos) /
+                                                   sum(self.pos[:n]), 1))
 
 
 class PrefillBf16:
@@ -895,6 +1052,17 @@ class PrefillBf16:
             if len(sjobs) else None
         cos, sin = rope_tables(max(self.prefix) + self.new + 1, self.half)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        if self.bq:
+            # The cached prefixes as the configuration produces them: N(0,1) K/V
+            # with 1 % outliers x20 through the quantizing append.  A pair's
+            # second sequence reads the first's sealed pages and the copy of its
+            # partial page, so the first sequence of each pair is filled.
+            self.data = DecodeBq.data
+            self.bq_k, self.bq_ks, self.bq_v, self.bq_vs = self.k, self.ksc, self.v, self.vsc
+            bq_quantize_cache(self, dev, [(0, self.prefix[i], tables[i])
+                                          for i in range(0, n_seq, 2)],
+                              kind=1, cache_size=PAGE_LEN, cache_rows=rows,
+                              v_is_k=self.cfg == 12, seed=self.seed * 16 + 8)
         self.plan = AttentionPlan(table, n, kind=1, window=0, cache_size=PAGE_LEN,
                                   page_len=PAGE_LEN, cache_rows=rows, cap=a.cap,
                                   kv_row_bytes=self.kvs * (1 if self.bq else 2), device=dev)
@@ -958,8 +1126,9 @@ class PrefillBf16:
                 "algorithmic_tflop": round(self.flops() / 1e12, 3)}
 
     def cpu_baseline(self, budget_s):
-        """The oracle's token route (FlashPrefillFullKernel) on a bounded sample:
-        the last 16 query tokens of the longest sequence."""
+        """The oracle's token route (FlashPrefillFullKernel + PrefillMergeKernel,
+        or BqFlashPrefillFullKernel) over the last n query tokens of the longest
+        sequence (the most keys per token), n sized to the budget."""
         import torch
 
         import oracle
@@ -971,77 +1140,52 @@ class PrefillBf16:
         pages = np.asarray(self.tables[i], dtype=np.int64)
         npage = pages.size
         idx = torch.from_numpy(pages).to(self.k.device)
-        if self.bq:
-            return self._cpu_baseline_bq(budget_s, hc, i, p0, idx, npage)
-        kp = self.k.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
-        vp = self.v.view(-1, PAGE_LEN * self.kvs).index_select(0, idx).cpu().numpy()
-        kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
-        vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
-        n_s = 16
-        first = self.new - n_s
-        runs = np.asarray([[0, p0 + first, 0, npage]], dtype=np.int32)
-        base = np.arange(npage, dtype=np.int32) * PAGE_LEN
-        qh = self.q.view(-1, self.nq * self.hd)[i * self.new + first:(i + 1) * self.new]
-        qh = np.ascontiguousarray(qh.cpu().numpy().view(np.uint16).reshape(-1))
-        keys = sum(p0 + first + t + 1 for t in range(n_s))
-        fl = 4 * self.hd * self.nq * keys
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.attention(1, runs, base, qh, kp, vp, num_q=self.nq, num_kv=self.nkv,
-                             head_dim=self.hd, kv_stride=self.kvs, window=0,
-                             cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
-                             cap=threads, threads=threads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"last {n_s} query tokens of the longest sequence "
-                           f"({keys} query-key pairs), the reference's token route at "
-                           f"cap={threads} workers, median of {len(times)}")}
 
-    def _cpu_baseline_bq(self, budget_s, hc, i, p0, idx, npage):
-        """The oracle's bq token route (BqFlashPrefillFullKernel) on the last
-        16 query tokens of the longest sequence."""
-        import oracle
-
-        threads = hc["threads"]
-
-        def pages_of(t, per_row):
+        def sel(t, per_row):
             return np.ascontiguousarray(
                 t.view(-1, PAGE_LEN * per_row).index_select(0, idx).cpu().numpy()).reshape(-1)
 
-        kp, vp = pages_of(self.k, self.kvs), pages_of(self.v, self.kvs)
-        ksp, vsp = pages_of(self.ksc, self.nkv), pages_of(self.vsc, self.nkv)
-        n_s = 16
-        first = self.new - n_s
-        runs = np.asarray([[0, p0 + first, 0, npage]], dtype=np.int32)
+        kp, vp = sel(self.k, self.kvs), sel(self.v, self.kvs)
+        if self.bq:
+            ksp, vsp = sel(self.ksc, self.nkv), sel(self.vsc, self.nkv)
+        else:
+            kp, vp = kp.view(np.uint16), vp.view(np.uint16)
         base = np.arange(npage, dtype=np.int32) * PAGE_LEN
-        t0_, t1_ = i * self.new + first, (i + 1) * self.new
-        qh = np.ascontiguousarray(
-            self.q_i8.view(-1, self.nq * self.hd)[t0_:t1_].cpu().numpy()).reshape(-1)
-        qb = np.ascontiguousarray(self.qb.view(-1, self.nq)[t0_:t1_].cpu().numpy()).reshape(-1)
-        fq = np.ascontiguousarray(self.fq.view(-1, self.nq)[t0_:t1_].cpu().numpy()).reshape(-1)
-        keys = sum(p0 + first + t + 1 for t in range(n_s))
-        fl = 4 * self.hd * self.nq * keys
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.bq_attention(1, runs, base, qh, qb, fq, kp, ksp, vp, vsp, num_q=self.nq,
-                                num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs,
-                                window=0, cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
-                                cap=threads, threads=threads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"last {n_s} query tokens of the longest sequence ({keys} query-key "
-                           f"pairs), the reference's bq token route at cap={threads} workers, "
-                           f"median of {len(times)}")}
+
+        def make(n):
+            first = self.new - n
+            runs = np.asarray([[0, p0 + first, 0, npage]], dtype=np.int32)
+            t0_, t1_ = i * self.new + first, (i + 1) * self.new
+            if not self.bq:
+                qh = np.ascontiguousarray(self.q.view(-1, self.nq * self.hd)[t0_:t1_].cpu()
+                                          .numpy().view(np.uint16).reshape(-1))
+                return lambda: oracle.attention(
+                    1, runs, base, qh, kp, vp, num_q=self.nq, num_kv=self.nkv,
+                    head_dim=self.hd, kv_stride=self.kvs, window=0, cache_size=PAGE_LEN,
+                    page_len=PAGE_LEN, seq_len=n, cap=threads, threads=threads)
+            qh = np.ascontiguousarray(
+                self.q_i8.view(-1, self.nq * self.hd)[t0_:t1_].cpu().numpy()).reshape(-1)
+            qb = np.ascontiguousarray(self.qb.view(-1, self.nq)[t0_:t1_].cpu().numpy())
+            fq = np.ascontiguousarray(self.fq.view(-1, self.nq)[t0_:t1_].cpu().numpy())
+            return lambda: oracle.bq_attention(
+                1, runs, base, qh, qb.reshape(-1), fq.reshape(-1), kp, ksp, vp, vsp,
+                num_q=self.nq, num_kv=self.nkv, head_dim=self.hd, kv_stride=self.kvs,
+                window=0, cache_size=PAGE_LEN, page_len=PAGE_LEN, seq_len=n, cap=threads,
+                threads=threads)
+
+        def cost(n):
+            first = self.new - n
+            return 4 * self.hd * self.nq * sum(p0 + first + t + 1 for t in range(n))
+
+        t = cpu_sample(make, self.new, cost, budget_s, 16)
+        n, med = t["n"], t["median"]
+        fl = cost(n)
+        route = "bq token route" if self.bq else "token route"
+        return cpu_result(hc, round(fl / med / 1e12, 5), "TFLOP/s", threads, t,
+                          f"last {n} query tokens of the longest sequence "
+                          f"({fl // (4 * self.hd * self.nq)} query-key pairs), the reference's "
+                          f"{route} at cap={threads} workers",
+                          us_per_layer_equiv=round(med * 1e6 * self.flops() / fl, 1))
 
 class PrefillSliding:
     """Config 11 (widening): chunked prefill of a sliding-window layer --
@@ -1116,6 +1260,16 @@ class PrefillSliding:
             self.fq = torch.empty_like(self.qb)
         cos, sin = rope_tables(max(self.prefix) + self.new + 1)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        if self.bq:
+            # The ring positions the chunk's windows reach back to, quantized
+            # from N(0,1) K/V with 1 % outliers x20 through the append path.
+            self.data = DecodeBq.data
+            self.bq_k, self.bq_ks, self.bq_v, self.bq_vs = self.k, self.ksc, self.v, self.vsc
+            rings = [perm[i * self.RING:(i + 1) * self.RING] for i in range(n_seq)]
+            bq_quantize_cache(self, dev, [(max(0, p - self.new), p - max(0, p - self.new), rg)
+                                          for p, rg in zip(self.prefix, rings)],
+                              kind=0, cache_size=self.RING * PAGE_LEN, cache_rows=rows,
+                              v_is_k=False, seed=self.seed * 16 + 8)
         self.plan = AttentionPlan(table, n, kind=0, window=self.window,
                                   cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN,
                                   cache_rows=rows, cap=a.cap,
@@ -1171,8 +1325,9 @@ class PrefillSliding:
                 "algorithmic_tflop": round(self.flops() / 1e12, 3)}
 
     def cpu_baseline(self, budget_s):
-        """The oracle's sliding token route (FlashPrefillSlidingKernel) on the
-        last 16 query tokens of the first sequence."""
+        """The oracle's sliding token route (FlashPrefillSlidingKernel, or
+        BqFlashPrefillSlidingKernel) over the last n query tokens of the first
+        sequence, n sized to the budget."""
         import torch
 
         import oracle
@@ -1182,78 +1337,50 @@ class PrefillSliding:
         p0 = self.prefix[0]
         pages = np.asarray(self.table.base_rows[:self.RING], dtype=np.int64) // PAGE_LEN
         idx = torch.from_numpy(pages).to(self.k.device)
-        if self.bq:
-            return self._cpu_baseline_bq(budget_s, hc, p0, idx)
-        kp = self.k.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
-        vp = self.v.view(-1, PAGE_LEN * KV_STRIDE).index_select(0, idx).cpu().numpy()
-        kp = np.ascontiguousarray(kp.view(np.uint16).reshape(-1))
-        vp = np.ascontiguousarray(vp.view(np.uint16).reshape(-1))
-        n_s = 16
-        first = self.new - n_s
-        runs = np.asarray([[0, p0 + first, 0, self.RING]], dtype=np.int32)
-        base = np.arange(self.RING, dtype=np.int32) * PAGE_LEN
-        qh = self.q.view(-1, NUM_Q * HEAD_DIM)[first:self.new]
-        qh = np.ascontiguousarray(qh.cpu().numpy().view(np.uint16).reshape(-1))
-        keys = sum(min(p0 + first + t + 1, self.window) for t in range(n_s))
-        fl = 4 * HEAD_DIM * NUM_Q * keys
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.attention(0, runs, base, qh, kp, vp, num_q=NUM_Q, num_kv=NUM_KV,
-                             head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=self.window,
-                             cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN, seq_len=n_s,
-                             cap=threads, threads=threads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"last {n_s} query tokens of the first sequence ({keys} query-key "
-                           f"pairs), the reference's sliding token route at cap={threads} "
-                           f"workers, median of {len(times)}")}
 
-    def _cpu_baseline_bq(self, budget_s, hc, p0, idx):
-        """The oracle's bq sliding token route (BqFlashPrefillSlidingKernel) on
-        the last 16 query tokens of the first sequence."""
-        import oracle
-
-        threads = hc["threads"]
-
-        def pages_of(t, per_row):
+        def sel(t, per_row):
             return np.ascontiguousarray(
                 t.view(-1, PAGE_LEN * per_row).index_select(0, idx).cpu().numpy()).reshape(-1)
 
-        kp, vp = pages_of(self.k, KV_STRIDE), pages_of(self.v, KV_STRIDE)
-        ksp, vsp = pages_of(self.ksc, NUM_KV), pages_of(self.vsc, NUM_KV)
-        n_s = 16
-        first = self.new - n_s
-        runs = np.asarray([[0, p0 + first, 0, self.RING]], dtype=np.int32)
+        kp, vp = sel(self.k, KV_STRIDE), sel(self.v, KV_STRIDE)
+        if self.bq:
+            ksp, vsp = sel(self.ksc, NUM_KV), sel(self.vsc, NUM_KV)
+        else:
+            kp, vp = kp.view(np.uint16), vp.view(np.uint16)
         base = np.arange(self.RING, dtype=np.int32) * PAGE_LEN
-        qh = np.ascontiguousarray(
-            self.q_i8.view(-1, NUM_Q * HEAD_DIM)[first:self.new].cpu().numpy()).reshape(-1)
-        qb = np.ascontiguousarray(self.qb.view(-1, NUM_Q)[first:self.new].cpu().numpy())
-        fq = np.ascontiguousarray(self.fq.view(-1, NUM_Q)[first:self.new].cpu().numpy())
-        keys = sum(min(p0 + first + t + 1, self.window) for t in range(n_s))
-        fl = 4 * HEAD_DIM * NUM_Q * keys
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.bq_attention(0, runs, base, qh, qb.reshape(-1), fq.reshape(-1), kp, ksp, vp,
-                                vsp, num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM,
-                                kv_stride=KV_STRIDE, window=self.window,
-                                cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN,
-                                seq_len=n_s, cap=threads, threads=threads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"last {n_s} query tokens of the first sequence ({keys} query-key "
-                           f"pairs), the reference's bq sliding token route at cap={threads} "
-                           f"workers, median of {len(times)}")}
+        geo = dict(num_q=NUM_Q, num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE,
+                   window=self.window, cache_size=self.RING * PAGE_LEN, page_len=PAGE_LEN,
+                   cap=threads, threads=threads)
 
+        def make(n):
+            first = self.new - n
+            runs = np.asarray([[0, p0 + first, 0, self.RING]], dtype=np.int32)
+            if not self.bq:
+                qh = np.ascontiguousarray(self.q.view(-1, NUM_Q * HEAD_DIM)[first:self.new]
+                                          .cpu().numpy().view(np.uint16).reshape(-1))
+                return lambda: oracle.attention(0, runs, base, qh, kp, vp, seq_len=n, **geo)
+            qh = np.ascontiguousarray(
+                self.q_i8.view(-1, NUM_Q * HEAD_DIM)[first:self.new].cpu().numpy()).reshape(-1)
+            qb = np.ascontiguousarray(self.qb.view(-1, NUM_Q)[first:self.new].cpu().numpy())
+            fq = np.ascontiguousarray(self.fq.view(-1, NUM_Q)[first:self.new].cpu().numpy())
+            return lambda: oracle.bq_attention(0, runs, base, qh, qb.reshape(-1),
+                                               fq.reshape(-1), kp, ksp, vp, vsp, seq_len=n,
+                                               **geo)
+
+        def cost(n):
+            first = self.new - n
+            return 4 * HEAD_DIM * NUM_Q * sum(min(p0 + first + t + 1, self.window)
+                                              for t in range(n))
+
+        t = cpu_sample(make, self.new, cost, budget_s, 16)
+        n, med = t["n"], t["median"]
+        fl = cost(n)
+        route = "bq sliding token route" if self.bq else "sliding token route"
+        return cpu_result(hc, round(fl / med / 1e12, 5), "TFLOP/s", threads, t,
+                          f"last {n} query tokens of the first sequence "
+                          f"({fl // (4 * HEAD_DIM * NUM_Q)} query-key pairs), the reference's "
+                          f"{route} at cap={threads} workers",
+                          us_per_layer_equiv=round(med * 1e6 * self.flops() / fl, 1))
 
 class PageCopyBench:
     """Config 9 (widening): dispatch_copy_jobs (kernels/page_copy.mojo:63-94) as
@@ -1314,34 +1441,40 @@ class PageCopyBench:
                 "row_bytes": KV_STRIDE * 2, "seed": self.seed}
 
     def cpu_baseline(self, budget_s):
-        """The oracle's copy (one memcpy per job, as a PageCopyKernel worker
-        does for its byte range) over the first 512 jobs, remapped into a
-        compact host arena, one thread."""
+        """The oracle's fanned-out copy (dispatch_copy_jobs: 64-byte aligned
+        worker shares of the concatenated jobs, one PageCopyKernel per worker)
+        over the first n jobs remapped into a compact host arena, on the worker
+        threads; n is every job when the timed calls fit the budget."""
         import oracle
 
-        n = 512
-        page_bytes = PAGE_LEN * KV_STRIDE * 2
-        jobs = np.empty((n, 3), dtype=np.int64)
-        jobs[:, 0] = np.arange(n) * page_bytes
-        jobs[:, 1] = (n + np.arange(n)) * page_bytes
-        jobs[:, 2] = self.jobs[:n, 2]
-        arena = np.ones(2 * n * page_bytes, dtype=np.uint8)
-        oracle.copy_jobs(arena, jobs)  # first touch of every page
-        nbytes = 2 * int(jobs[:, 2].sum())
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.copy_jobs(arena, jobs)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
         hc = host_cpu()
-        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": (f"the first {n} jobs ({nbytes / 2e6:.1f} MB copied) in a "
-                           f"compact host arena, one thread, median of {len(times)}")}
+        threads = hc["threads"]
+        total = self.jobs.shape[0]
+        page_bytes = PAGE_LEN * KV_STRIDE * 2
 
+        def make(n):
+            jobs = np.empty((n, 3), dtype=np.int64)
+            jobs[:, 0] = np.arange(n) * page_bytes
+            jobs[:, 1] = (n + np.arange(n)) * page_bytes
+            jobs[:, 2] = self.jobs[:n, 2]
+            arena = np.ones(2 * n * page_bytes, dtype=np.uint8)
+
+            def call():
+                oracle.copy_jobs_workers(arena, jobs, threads, threads)
+                return None
+            call()  # first touch of every page
+            return call
+
+        def cost(n):
+            return 2 * int(self.jobs[:n, 2].sum())
+
+        t = cpu_sample(make, total, cost, budget_s, min(total, 64))
+        n, med = t["n"], t["median"]
+        nbytes = cost(n)
+        return cpu_result(hc, round(nbytes / med / 1e9, 3), "GB/s", threads, t,
+                          f"{'all' if n == total else 'the first'} {n} of the {total} jobs "
+                          f"({nbytes / 2e6:.1f} MB copied) in a compact host arena, "
+                          f"{threads} worker shares on {threads} threads")
 
 class GatherBench:
     """Config 10 (widening): dispatch_gather_rows (kernels/gather.mojo:30-55)
@@ -1389,27 +1522,30 @@ class GatherBench:
                 "cols": self.COLS, "seed": self.seed}
 
     def cpu_baseline(self, budget_s):
-        """The oracle's gather over the first 4096 rows, one thread."""
+        """The oracle's fanned-out gather (dispatch_gather_rows: worker_range
+        shares of the rows) of the first n rows on the worker threads, n every
+        row when the timed calls fit the budget."""
         import oracle
 
-        n = 4096
-        src = self.src.cpu().numpy().view(np.uint16)
-        rows = self.rows_host[:n]
-        nbytes = 2 * n * self.COLS * 2
-        oracle.gather_rows(src, rows, self.COLS)
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 5 and (not times or time.perf_counter() < t_end):
-            t0 = time.perf_counter()
-            oracle.gather_rows(src, rows, self.COLS)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
         hc = host_cpu()
-        return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
-                "kind": "port", **{k: hc[k] for k in ("cpu_model", "logical_cpus",
-                                                      "affinity_cpus")},
-                "sample": f"the first {n} rows, one thread, median of {len(times)}"}
+        threads = hc["threads"]
+        src = self.src.cpu().numpy().view(np.uint16)
 
+        def make(n):
+            rows = np.ascontiguousarray(self.rows_host[:n])
+            dst = np.zeros(n * self.COLS, dtype=np.uint16)
+            return lambda: oracle.gather_rows_workers(src, rows, self.COLS, threads, threads,
+                                                      dst=dst)
+
+        def cost(n):
+            return 2 * n * self.COLS * 2
+
+        t = cpu_sample(make, self.ROWS, cost, budget_s, min(self.ROWS, 1024))
+        n, med = t["n"], t["median"]
+        nbytes = cost(n)
+        return cpu_result(hc, round(nbytes / med / 1e9, 3), "GB/s", threads, t,
+                          f"{'all' if n == self.ROWS else 'the first'} {n} of the {self.ROWS} "
+                          f"rows, {threads} worker shares on {threads} threads")
 
 def measure(w, steps: int, warmup: int, graph: bool):
     """Returns the wall time of K eager steps, of K steps replayed from a HIP
@@ -1498,7 +1634,7 @@ def main() -> None:
                     help="config 11: sliding window (a multiple of 16 takes the MFMA kernel)")
     ap.add_argument("--cap", type=int, default=0, help="worker capacity (0: per-config default)")
     ap.add_argument("--seed", type=int, default=20241)
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--norm", choices=("none", "separate", "fused"), default="none",
                     help="configs 1-3: head RMS norm of q/k/v ahead of the append, as its "
@@ -1580,7 +1716,7 @@ def main() -> None:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": w.dtype,
-        "data": "synthetic (seeded SplitMix64/Box-Muller N(0,1) on device)",
+        "data": getattr(w, "data", "synthetic (seeded SplitMix64/Box-Muller N(0,1) on device)"),
         "config": w.config(),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "us_per_layer": round(ms_per_step * 1e3, 2),

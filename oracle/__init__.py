@@ -44,6 +44,8 @@ _SIG = {
     "ifo_rms_norm_qkv_heads": (None, [VP, VP, VP, VP, VP, I64, I64, I64, I64, F32, F32]),
     "ifo_copy_jobs": (None, [VP, VP, I64]),
     "ifo_gather_rows": (None, [VP, VP, VP, I64, I64]),
+    "ifo_copy_jobs_workers": (None, [VP, VP, I64, I64, I64]),
+    "ifo_gather_rows_workers": (None, [VP, VP, VP, I64, I64, I64, I64]),
     "ifo_fwht": (None, [VP, I64]),
     "ifo_head_inv_rms": (F32, [VP, I64, F32, F32]),
     "ifo_absmax_quantize": (F32, [VP, I64, VP, VP]),
@@ -67,6 +69,8 @@ _SIG = {
 }
 
 _LIB = None
+_ACTIVE = None
+NATIVE_PATH = HERE / "_native" / "liboracle.so"
 
 
 def build() -> Path:
@@ -74,17 +78,55 @@ def build() -> Path:
     return LIB_PATH
 
 
+def build_native() -> Path:
+    """The same source built with -march=native for this host (AVX-512, and the
+    VDPBF16PS / VPDPBUSD dots where the host has them): the timed CPU baseline."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "native"], check=True)
+    return NATIVE_PATH
+
+
+def _load(path: Path):
+    h = C.CDLL(str(path))
+    for name, (res, args) in _SIG.items():
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    return h
+
+
+def native_lib():
+    """Handle of the -march=native build (built on first use)."""
+    if not NATIVE_PATH.exists():
+        build_native()
+    return _load(NATIVE_PATH)
+
+
+class using:
+    """Route this module's calls through another build of the oracle inside
+    a with-block: `with oracle.using(oracle.native_lib()): ...`."""
+
+    def __init__(self, handle):
+        self.handle, self.prev = handle, None
+
+    def __enter__(self):
+        global _ACTIVE
+        self.prev, _ACTIVE = _ACTIVE, self.handle
+        return self.handle
+
+    def __exit__(self, *exc):
+        global _ACTIVE
+        _ACTIVE = self.prev
+        return False
+
+
 def lib():
     global _LIB
+    if _ACTIVE is not None:
+        return _ACTIVE
     if _LIB is None:
         if not LIB_PATH.exists():
             build()
-        h = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in _SIG.items():
-            fn = getattr(h, name)
-            fn.restype = res
-            fn.argtypes = args
-        _LIB = h
+        _LIB = _load(LIB_PATH)
     return _LIB
 
 
@@ -195,6 +237,24 @@ def gather_rows(src, rows, cols) -> np.ndarray:
     rows = np.ascontiguousarray(rows, dtype=np.int32)
     dst = np.zeros(rows.size * cols, dtype=np.uint16)
     lib().ifo_gather_rows(_p(src), _p(dst), _p(rows), rows.size, cols)
+    return dst
+
+
+def copy_jobs_workers(arena: np.ndarray, jobs, workers: int, threads: int) -> None:
+    """dispatch_copy_jobs' fan-out: 64-byte aligned worker shares of the
+    concatenated jobs, run on `threads` threads."""
+    j = np.ascontiguousarray(jobs, dtype=np.int64)
+    lib().ifo_copy_jobs_workers(_p(arena), _p(j), j.shape[0], workers, threads)
+
+
+def gather_rows_workers(src, rows, cols, workers: int, threads: int,
+                        dst: np.ndarray | None = None) -> np.ndarray:
+    """dispatch_gather_rows' fan-out: worker_range shares of the rows."""
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    if dst is None:
+        dst = np.zeros(rows.size * cols, dtype=np.uint16)
+    lib().ifo_gather_rows_workers(_p(src), _p(dst), _p(rows), rows.size, cols, workers,
+                                  threads)
     return dst
 
 

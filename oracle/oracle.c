@@ -70,6 +70,9 @@
  */
 #include "oracle.h"
 
+#if defined(__AVX512F__)
+#include <immintrin.h>
+#endif
 #include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
@@ -304,6 +307,38 @@ static int64_t reuse_panel_pu(int64_t head_dim, int64_t gqa) {
     return pu;
 }
 
+#if defined(__AVX512BF16__) && defined(__AVX512F__)
+/* The same lanes through the instruction itself, for a -march=native build on
+ * a host with AVX-512 BF16 (the reference's own path on such hosts):
+ * VDPBF16PS lane j adds x[2j+1]*k[2j+1] and then x[2j]*k[2j] to its f32
+ * accumulator, each step rounded to nearest even; bf16 products are exact in
+ * f32, so this equals the portable form below for all normal inputs (the
+ * instruction treats denormal inputs and results as zero). */
+static float bf16_dot_vdpbf16(const uint16_t* k_row, const uint16_t* x_row,
+                              int64_t cols, int64_t pu) {
+    __m512 acc[8];
+    for (int64_t p = 0; p < pu; p++) acc[p] = _mm512_setzero_ps();
+    int64_t stride = pu * 2 * W;
+    for (int64_t i = 0; i < cols / stride; i++) {
+        for (int64_t p = 0; p < pu; p++) {
+            int64_t off = i * stride + p * 2 * W;
+            __m512i xv = _mm512_loadu_si512((const void*)(x_row + off));
+            __m512i kv = _mm512_loadu_si512((const void*)(k_row + off));
+            acc[p] = _mm512_dpbf16_ps(acc[p], (__m512bh)xv, (__m512bh)kv);
+        }
+    }
+    /* Port accumulators summed in order, then the halving tree of
+     * SIMD.reduce_add (lanes j and j + w for w = 8, 4, 2, 1), lane for lane
+     * as ifo_tree_sum16 adds them. */
+    __m512 v = _mm512_setzero_ps();
+    for (int64_t p = 0; p < pu; p++) v = _mm512_add_ps(v, acc[p]);
+    __m256 h8 = _mm256_add_ps(_mm512_castps512_ps256(v), _mm512_extractf32x8_ps(v, 1));
+    __m128 h4 = _mm_add_ps(_mm256_castps256_ps128(h8), _mm256_extractf128_ps(h8, 1));
+    __m128 h2 = _mm_add_ps(h4, _mm_movehl_ps(h4, h4));
+    __m128 h1 = _mm_add_ss(h2, _mm_shuffle_ps(h2, h2, 1));
+    return _mm_cvtss_f32(h1);
+}
+#else
 static float bf16_dot_vdpbf16(const uint16_t* k_row, const uint16_t* x_row,
                               int64_t cols, int64_t pu) {
     /* One 32-bit load holds a (even, odd) bf16 pair, as a VDPBF16PS lane
@@ -339,6 +374,29 @@ static float bf16_dot_vdpbf16(const uint16_t* k_row, const uint16_t* x_row,
         s[j] = v;
     }
     return ifo_tree_sum16(s);
+}
+#endif
+
+/* Raw int8 score dot of bq_process_kv_tile: VPDPBUSD over (k ^ 0x80) read as
+ * unsigned bytes times the signed q codes.  The sum is exact in int32, so any
+ * order gives the same value. */
+static int32_t i8_dot_vpdpbusd(const int8_t* k_row, const int8_t* q_row, int64_t D) {
+#if defined(__AVX512VNNI__) && defined(__AVX512F__)
+    if (D % 64 == 0) {
+        __m512i acc = _mm512_setzero_si512();
+        const __m512i flip = _mm512_set1_epi8((char)0x80);
+        for (int64_t e = 0; e < D; e += 64) {
+            __m512i kv = _mm512_xor_si512(_mm512_loadu_si512((const void*)(k_row + e)), flip);
+            __m512i qv = _mm512_loadu_si512((const void*)(q_row + e));
+            acc = _mm512_dpbusd_epi32(acc, kv, qv);
+        }
+        return _mm512_reduce_add_epi32(acc);
+    }
+#endif
+    int32_t raw = 0;
+    for (int64_t e = 0; e < D; e++)
+        raw += (int32_t)((uint8_t)((uint8_t)k_row[e] ^ 0x80u)) * (int32_t)q_row[e];
+    return raw;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -419,9 +477,7 @@ static void process_tile(const attn_ctx* c, const attn_item* it,
                 for (int64_t r = 0; r < c->gqa; r++) {
                     int64_t qi = base_q + r;
                     const int8_t* qrow = c->qi + q_heads_off[qi];
-                    int32_t raw = 0;   /* vpdpbusd over (k ^ 0x80) as u8 */
-                    for (int64_t e = 0; e < D; e++)
-                        raw += (int32_t)((uint8_t)((uint8_t)k_head[e] ^ 0x80u)) * (int32_t)qrow[e];
+                    int32_t raw = i8_dot_vpdpbusd(k_head, qrow, D);
                     float qb = c->qi_bias[it->q_row * c->num_q + qi];
                     float fq = c->f_q[it->q_row * c->num_q + qi];
                     float s = (float)raw - qb;
@@ -1320,6 +1376,115 @@ void ifo_gather_rows(const uint16_t* src, uint16_t* dst, const int32_t* rows,
                      int64_t num_rows, int64_t cols) {
     for (int64_t j = 0; j < num_rows; j++)
         memcpy(dst + j * cols, src + (int64_t)rows[j] * cols, sizeof(uint16_t) * (size_t)cols);
+}
+
+/* The reference's fanned-out forms: dispatch_copy_jobs
+ * (kernels/page_copy.mojo:63-94) cuts the concatenated jobs' byte range
+ * [0, total) into `workers` worker_range shares whose ends are rounded up to
+ * 64 bytes (align_split, :18-22), and each PageCopyKernel (:25-60) copies its
+ * share job segment by job segment; dispatch_gather_rows (gather.mojo:30-55)
+ * gives each worker a worker_range share of the rows.  The shares run on
+ * `threads` threads; the bytes written are those of the one-thread forms. */
+typedef struct {
+    uint8_t* arena;
+    const int64_t* jobs;
+    const int64_t* bounds;
+    int64_t num_jobs, workers;
+    const uint16_t* src;
+    uint16_t* dst;
+    const int32_t* rows;
+    int64_t num_rows, cols;
+    atomic_llong next;
+} share_pool;
+
+static int64_t align_split64(int64_t offset, int64_t total) {
+    int64_t a = (offset + 63) / 64 * 64;
+    return a < total ? a : total;
+}
+
+static void copy_share(share_pool* p, int64_t w) {
+    int64_t total = p->bounds[p->num_jobs];
+    int64_t wr[2];
+    ifo_worker_range(total, p->workers, w, 0, wr);
+    int64_t lo = align_split64(wr[0], total), hi = align_split64(wr[1], total);
+    if (lo >= hi) return;
+    int64_t j = 0;
+    while (p->bounds[j + 1] <= lo) j++;
+    for (int64_t cursor = lo; cursor < hi; j++) {
+        int64_t seg_end = p->bounds[j + 1] < hi ? p->bounds[j + 1] : hi;
+        int64_t off = cursor - p->bounds[j];
+        memcpy(p->arena + p->jobs[3 * j + 1] + off, p->arena + p->jobs[3 * j + 0] + off,
+               (size_t)(seg_end - cursor));
+        cursor = seg_end;
+    }
+}
+
+static void gather_share(share_pool* p, int64_t w) {
+    int64_t wr[2];
+    ifo_worker_range(p->num_rows, p->workers, w, 0, wr);
+    for (int64_t j = wr[0]; j < wr[1]; j++)
+        memcpy(p->dst + j * p->cols, p->src + (int64_t)p->rows[j] * p->cols,
+               sizeof(uint16_t) * (size_t)p->cols);
+}
+
+static void* copy_share_worker(void* arg) {
+    share_pool* p = (share_pool*)arg;
+    for (long long w; (w = atomic_fetch_add(&p->next, 1)) < p->workers;) copy_share(p, w);
+    return NULL;
+}
+
+static void* gather_share_worker(void* arg) {
+    share_pool* p = (share_pool*)arg;
+    for (long long w; (w = atomic_fetch_add(&p->next, 1)) < p->workers;) gather_share(p, w);
+    return NULL;
+}
+
+static void run_shares(share_pool* p, void* (*fn)(void*), int64_t threads) {
+    atomic_init(&p->next, 0);
+    if (threads > p->workers) threads = p->workers;
+    if (threads <= 1) {
+        fn(p);
+        return;
+    }
+    pthread_t* tids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int64_t t = 1; t < threads; t++) pthread_create(&tids[t], NULL, fn, p);
+    fn(p);
+    for (int64_t t = 1; t < threads; t++) pthread_join(tids[t], NULL);
+    free(tids);
+}
+
+void ifo_copy_jobs_workers(uint8_t* arena, const int64_t* jobs, int64_t num_jobs,
+                           int64_t workers, int64_t threads) {
+    if (num_jobs <= 0 || workers <= 0) return;
+    int64_t* bounds = (int64_t*)malloc(sizeof(int64_t) * (size_t)(num_jobs + 1));
+    bounds[0] = 0;
+    for (int64_t i = 0; i < num_jobs; i++) bounds[i + 1] = bounds[i] + jobs[3 * i + 2];
+    if (bounds[num_jobs] > 0) {
+        share_pool p;
+        memset(&p, 0, sizeof(p));
+        p.arena = arena;
+        p.jobs = jobs;
+        p.bounds = bounds;
+        p.num_jobs = num_jobs;
+        p.workers = workers;
+        run_shares(&p, copy_share_worker, threads);
+    }
+    free(bounds);
+}
+
+void ifo_gather_rows_workers(const uint16_t* src, uint16_t* dst, const int32_t* rows,
+                             int64_t num_rows, int64_t cols, int64_t workers,
+                             int64_t threads) {
+    if (num_rows <= 0 || workers <= 0) return;
+    share_pool p;
+    memset(&p, 0, sizeof(p));
+    p.src = src;
+    p.dst = dst;
+    p.rows = rows;
+    p.num_rows = num_rows;
+    p.cols = cols;
+    p.workers = workers;
+    run_shares(&p, gather_share_worker, threads);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -102,6 +102,11 @@ void ifo_copy_jobs(uint8_t* arena, const int64_t* jobs /* [n][3] */,
                    int64_t num_jobs);
 void ifo_gather_rows(const uint16_t* src, uint16_t* dst, const int32_t* rows,
                      int64_t num_rows, int64_t cols);
+void ifo_copy_jobs_workers(uint8_t* arena, const int64_t* jobs, int64_t num_jobs,
+                           int64_t workers, int64_t threads);
+void ifo_gather_rows_workers(const uint16_t* src, uint16_t* dst, const int32_t* rows,
+                             int64_t num_rows, int64_t cols, int64_t workers,
+                             int64_t threads);
 
 /* ---- MiniMax-M3 block-sparse attention (degree 1) ---------------------- */
 void ifo_index_block_scores(const int32_t* runs, int64_t num_runs,

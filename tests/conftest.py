@@ -18,3 +18,16 @@ def oracle_lib():
 
     oracle.build()
     return oracle
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The bf16-bar comparisons of the session: outputs beyond 1e-2 against
+    each comparison's cap."""
+    from tests.helpers import BAR_LOG
+
+    if not BAR_LOG:
+        return
+    terminalreporter.write_sep("-", "bf16 bar: outputs beyond 1e-2 / cap (of n)")
+    for test, label, over, cap, n, max_abs, fail in BAR_LOG:
+        terminalreporter.write_line(f"{over:>5} / {cap:<5} of {n:>9}  max_abs {max_abs:.4g}"
+                                    f"{'  FAIL ' + str(fail) if fail else ''}  {test} {label}")

@@ -53,11 +53,20 @@ def over_tol_cap(n: int) -> int:
     return OVER_TOL_FIXED + int(OVER_TOL_FRAC * n)
 
 
+# Every assert_bar call of the session, printed as a table at its end (the
+# test run's log then shows each comparison's count beyond 1e-2 and its cap).
+BAR_LOG: list = []
+
+
 def assert_bar(r: dict, label: str = "", strict: bool = False) -> dict:
     """Print the comparison and hold it to the bar: no NaN, every output within
     1e-2 or one bf16 spacing, and at most over_tol_cap(n) outputs beyond 1e-2
     (none when strict)."""
+    import os
+
     cap = 0 if strict else over_tol_cap(r["n"])
+    test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
+    BAR_LOG.append((test, label, r["n_over_tol"], cap, r["n"], r["max_abs"], r["n_fail"]))
     print(f"  {label}: n_over_tol={r['n_over_tol']} (cap {cap}) of {r['n']}, "
           f"max_abs={r['max_abs']:.6g}, n_fail={r['n_fail']}", flush=True)
     assert r["n_nan"] == 0 and r["n_fail"] == 0, (label, r)

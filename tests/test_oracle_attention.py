@@ -171,6 +171,27 @@ def test_copy_jobs_and_gather_closed_form():
     assert np.array_equal(got, src.reshape(50, 64)[rows])
 
 
+@pytest.mark.parametrize("workers,threads", [(1, 1), (3, 2), (16, 8), (200, 8)])
+def test_fanned_out_copy_and_gather_closed_form(workers, threads):
+    """dispatch_copy_jobs' 64-byte aligned worker shares (page_copy.mojo:18-60)
+    and dispatch_gather_rows' row shares write what the jobs and rows say,
+    whatever the worker count: shares that end mid-job, jobs shorter than 64
+    bytes, an empty job and more workers than aligned shares."""
+    rng = np.random.default_rng(40 + workers)
+    arena = rng.integers(0, 255, 1 << 18, dtype=np.uint8)
+    ref = arena.copy()
+    jobs = np.array([[0, 140000, 65536], [70000, 210000, 333], [80001, 220001, 7],
+                     [90000, 230000, 0], [100003, 240007, 5000]])
+    oracle.copy_jobs_workers(arena, jobs, workers, threads)
+    for s, d, n in jobs:
+        ref[d:d + n] = ref[s:s + n]
+    assert np.array_equal(arena, ref)
+    src = seeded_bf16(300 * 96, 6)
+    rows = rng.integers(0, 300, 257).astype(np.int32)
+    got = oracle.gather_rows_workers(src, rows, 96, workers, threads).reshape(-1, 96)
+    assert np.array_equal(got, src.reshape(300, 96)[rows])
+
+
 def test_bq_oracle_against_reference_head_schedule():
     """tests/test_sliding_attention_degree_parity.mojo at degree 1: the oracle's
     prep + bq sliding attention over the reference's 10-step schedule must stay
