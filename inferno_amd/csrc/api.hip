@@ -369,19 +369,12 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   // Query blocks for the MFMA prefill (token plans of full attention).
   hdr[kHdrOffQBlocks] = static_cast<int32_t>(off);
   int64_t n_qblocks = 0;
-  // Only when every run's page table fits the kernel's LDS copy (a sliding
-  // run's table is its ring), and for sliding windows whose span is whole
-  // 16-key tiles (the kernel aligns every row's tiles to 16 up to lo % 16).
-  bool mfma_tables_fit = true;
-  if (sliding) {
-    mfma_tables_fit = g.page_mask + 1 <= kPrefillLdsPages && window % kTile == 0;
-  } else {
-    for (int64_t r = 0; r < num_runs; ++r) {
-      const int64_t b = runs[4 * r], e = r + 1 < num_runs ? runs[4 * (r + 1)] : seq_len;
-      if (e > b && ((runs[4 * r + 1] + (e - 1 - b)) >> g.shift) + 1 > kPrefillLdsPages)
-        mfma_tables_fit = false;
-    }
-  }
+  // The full-attention kernels hold a window of the run's page table in LDS
+  // and take runs of any length; the sliding kernel holds the whole ring, so
+  // the ring must fit, and the window's span must be whole 16-key tiles (the
+  // kernel aligns every row's tiles to 16 up to lo % 16).
+  const bool mfma_tables_fit =
+      !sliding || (g.page_mask + 1 <= kPrefillLdsPages && window % kTile == 0);
   if ((mode == IFR_PLAN_TOKEN_MERGE || mode == IFR_PLAN_TOKEN_DIRECT) && mfma_tables_fit) {
     std::vector<std::array<int64_t, 4>> qbs;
     for (int64_t r = 0; r < num_runs; ++r) {
@@ -703,6 +696,29 @@ int32_t ifr_rms_norm_rope_cache_write(const void* image_dev, const int64_t* info
   return ok();
 }
 
+}  // extern "C"
+
+namespace {
+// Which MFMA prefill kernel, if any, runs a bf16 plan: token plans with
+// query blocks at the shapes the kernels are built for (full attention at
+// head_dim 256 / GQA 2 and 512 / GQA 8, sliding windows at 256 / GQA 2).
+enum class PrefillRoute { kNone, kFull256, kWide512, kSliding256 };
+PrefillRoute bf16_prefill_route(const int64_t* info, int64_t num_q, int64_t num_kv,
+                                int64_t head_dim, int64_t page_mask) {
+  if (info[14] <= 0) return PrefillRoute::kNone;
+  if (info[2] == IFR_PLAN_TOKEN_MERGE && page_mask < 0) {
+    if (head_dim == 256 && num_q == 2 * num_kv) return PrefillRoute::kFull256;
+    if (head_dim == 512 && num_q == 8 * num_kv) return PrefillRoute::kWide512;
+  }
+  if (info[2] == IFR_PLAN_TOKEN_DIRECT && page_mask >= 0 && head_dim == 256 &&
+      num_q == 2 * num_kv)
+    return PrefillRoute::kSliding256;
+  return PrefillRoute::kNone;
+}
+}  // namespace
+
+extern "C" {
+
 int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
                            const void* q, const void* k_base,
                            const void* v_base, void* output, void* partials,
@@ -723,12 +739,13 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
   if (!is_pow2(page_len)) return fail(IFR_EINVAL, "page_len must be a power of two");
   st = check_geometry(info, pow2_shift(page_len), page_len - 1, page_mask);
   if (st) return st;
-  if (partials_bytes < info[3] * partial_stride * 4)
-    return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
   ifr::PagedGeom g{static_cast<int>(pow2_shift(page_len)), static_cast<int>(page_len - 1),
                    static_cast<int>(page_mask)};
-  if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 256 &&
-      num_q == 2 * num_kv && page_mask < 0) {
+  const PrefillRoute route = bf16_prefill_route(info, num_q, num_kv, head_dim, page_mask);
+  // The MFMA prefill routes finalise in-kernel and write no partials.
+  if (route == PrefillRoute::kNone && partials_bytes < info[3] * partial_stride * 4)
+    return fail(IFR_ESPACE, "partials need %lld bytes", (long long)(info[3] * partial_stride * 4));
+  if (route == PrefillRoute::kFull256) {
     // Prefill chunk of full attention: MFMA query blocks, finalised in-kernel.
     IFR_HIP(ifr::launch_prefill_full_mfma(static_cast<const int32_t*>(image_dev),
                                           static_cast<int>(info[14]), q, k_base, v_base,
@@ -738,11 +755,8 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
             "prefill_full_mfma");
     return ok();
   }
-  if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 512 &&
-      num_q == 8 * num_kv && page_mask < 0 &&
-      (info[13] >> g.shift) + 1 <= ifr::prefill_wide_max_pages()) {
-    // The same at Gemma-4's full-attention shape (head_dim 512, GQA 8); its
-    // LDS page table is smaller, so longer runs take the token route.
+  if (route == PrefillRoute::kWide512) {
+    // The same at Gemma-4's full-attention shape (head_dim 512, GQA 8).
     IFR_HIP(ifr::launch_prefill_wide_mfma(static_cast<const int32_t*>(image_dev),
                                           static_cast<int>(info[14]), q, k_base, v_base,
                                           output, static_cast<int>(num_q),
@@ -751,8 +765,7 @@ int32_t ifr_attention_bf16(const void* image_dev, const int64_t* info,
             "prefill_wide_mfma");
     return ok();
   }
-  if (info[2] == IFR_PLAN_TOKEN_DIRECT && info[14] > 0 && head_dim == 256 &&
-      num_q == 2 * num_kv && page_mask >= 0) {
+  if (route == PrefillRoute::kSliding256) {
     // Prefill chunk of a sliding-window layer: MFMA query blocks.
     IFR_HIP(ifr::launch_prefill_sliding_mfma(static_cast<const int32_t*>(image_dev),
                                              static_cast<int>(info[14]), q, k_base, v_base,
@@ -817,7 +830,10 @@ int32_t ifr_attention_bf16_noalloc(const void* image_dev, const int64_t* info, c
   if (num_q <= 0 || head_dim <= 0 || num_q > 64 || head_dim > 4096)
     return fail(IFR_EINVAL, "bad num_q or head_dim");
   const int64_t ps = ifr_flash_partial_stride(num_q, head_dim);
-  const int64_t need = info[3] * ps * 4;
+  // The MFMA prefill routes write no partials, so their chunks need no scratch.
+  const bool mfma = bf16_prefill_route(info, num_q, num_kv, head_dim, page_mask) !=
+                    PrefillRoute::kNone;
+  const int64_t need = mfma ? 0 : info[3] * ps * 4;
   if (need > kStaticScratchBytes)
     return fail(IFR_ESPACE,
                 "the plan's %lld partial stripes need %lld bytes; the static scratch holds %lld",
@@ -1091,8 +1107,7 @@ int32_t bq_attention(const void* image_dev, const int64_t* info, const void* q_i
     return ok();
   }
   if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 512 &&
-      num_q == 8 * num_kv && page_mask < 0 &&
-      (info[13] >> g.shift) + 1 <= ifr::prefill_wide_max_pages()) {
+      num_q == 8 * num_kv && page_mask < 0) {
     // Prefill chunk of a full-attention layer at head_dim 512 / GQA 8.
     IFR_HIP(ifr::launch_prefill_wide_mfma_bq(
                 static_cast<const int32_t*>(image_dev), static_cast<int>(info[14]), q_i8,

@@ -44,8 +44,10 @@ constexpr int kUnitWords = 4;
 // kPrefillTokens consecutive tokens of one run, longest key range first.
 constexpr int kQBlockWords = 4;
 constexpr int kPrefillTokens = 64;
-// The MFMA prefill stages a run's page table in LDS: runs with more pages
-// than this take the token kernels.
+// Page-table entries the MFMA prefill kernels hold in LDS: the full-attention
+// kernels move a window of this many entries along the run; the sliding
+// kernel holds the run's whole ring, so rings of more pages take the token
+// kernels.
 constexpr int kPrefillLdsPages = 4096;
 
 constexpr int kTile = 16;  // reference TILE = f32 SIMD width on AVX-512

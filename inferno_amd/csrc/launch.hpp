@@ -49,9 +49,7 @@ hipError_t launch_prefill_full_mfma(const int32_t* image_dev, int num_qblocks,
                                     const void* v_base, void* output, int num_q,
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream);
-// The same for head_dim 512 / 8 q heads per kv head (prefill_wide.hip), for
-// runs of at most prefill_wide_max_pages() pages.
-int prefill_wide_max_pages();
+// The same for head_dim 512 / 8 q heads per kv head (prefill_wide.hip).
 hipError_t launch_prefill_wide_mfma_bq(const int32_t* image, int num_qblocks, const void* q_i8,
                                        const float* qi_bias, const float* f_q, const void* k,
                                        const float* k_scale, const void* v,

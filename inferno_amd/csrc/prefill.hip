@@ -39,8 +39,8 @@
 // no registers) one iteration ahead.  K rows are stored XOR-swizzled (16-byte
 // chunk c of key k at position c ^ (k & 15)) so the 16 keys a QK operand read
 // touches fall in distinct banks; V rows are stored plainly and read with
-// ds_read_b64_tr_b16 (a 16-lane transposing read).  The run's page table is
-// staged in LDS first.
+// ds_read_b64_tr_b16 (a 16-lane transposing read).  A window of the run's
+// page table is held in LDS.
 // Blocks are numbered kv-head-fastest so every block of a kv head lands on
 // one XCD (block id mod 8) and shares that XCD's L2.
 #include "common.hpp"
@@ -131,11 +131,17 @@ void prefill_full_mfma_kernel(
     for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
   float m = kNegBig, l = 0.0f, S = 1.0f;
 
-  // The run's page table, staged once (the host routes runs with more than
-  // kPrefillLdsPages pages elsewhere): the staging addresses of an iteration
-  // then wait on an LDS read rather than on a global load.
+  // The run's page table in LDS, so that the staging addresses of an
+  // iteration wait on an LDS read rather than on a global load: a window of
+  // kPrefillLdsPages entries (entry i holds page wbase + i), moved forward at
+  // an iteration boundary when the next staged keys pass its end.
   const int n_pages = count_max > 0 ? ((count_max - 1) >> shift) + 1 : 0;
-  for (int i = tid; i < n_pages; i += kPThreads) page_rows[i] = rows[i];
+  int wbase = 0;
+  auto load_window = [&](int first) {
+    const int n = min(kPrefillLdsPages, n_pages - first);
+    for (int i = tid; i < n; i += kPThreads) page_rows[i] = rows[first + i];
+  };
+  load_window(0);
   __syncthreads();
 
   // Staging of one iteration: wave w moves key rows kStageRows*w .. +15 of
@@ -152,7 +158,8 @@ void prefill_full_mfma_kernel(
     for (int i = 0; i < kStageRows / 2; ++i) {
       const int r = stage_row0 + 2 * i;  // key row within the iteration
       const int key = min(it * kKeys + r, count_max - 1);
-      const int64_t slot = static_cast<int64_t>(page_rows[key >> shift]) + (key & row_mask);
+      const int64_t slot =
+          static_cast<int64_t>(page_rows[(key >> shift) - wbase]) + (key & row_mask);
       const int64_t off = slot * kv_stride;
       const int kchunk = row ^ (r & 15);
       const int lds_row = wave * kStageRows + 2 * i;  // wave-uniform
@@ -178,7 +185,7 @@ void prefill_full_mfma_kernel(
       static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(row ^ (4 + 2 * half));
   auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
     const int key0 = it * kKeys + wave * kStageRows;  // wave-uniform
-    const int prow = __builtin_amdgcn_readfirstlane(page_rows[key0 >> shift]);
+    const int prow = __builtin_amdgcn_readfirstlane(page_rows[(key0 >> shift) - wbase]);
     const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
     const char* kb = reinterpret_cast<const char*>(kbase + slot0 * kv_stride);
     const char* vb = reinterpret_cast<const char*>(vbase + slot0 * kv_stride);
@@ -390,8 +397,12 @@ void prefill_full_mfma_kernel(
 
   // End of one iteration: the accumulators and the Q^T fragments stay in
   // AGPRs across iterations (the MFMAs read and write them there; only the
-  // rare rescale moves the accumulators through VGPRs); the next iteration's rows have landed (each wave waits
-  // for its own loads; the barrier publishes them to the block).
+  // rare rescale moves the accumulators through VGPRs); the next iteration's
+  // rows have landed (each wave waits for its own loads; the barrier
+  // publishes them to the block).  If the keys staged during the next
+  // iteration (those of iteration it + 2) reach past the page-table window,
+  // the window moves to their first page (nothing reads it between the
+  // barrier and the refill's barrier).
   auto iteration_end = [&](int it, uint8_t* vnext) {
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
@@ -400,6 +411,15 @@ void prefill_full_mfma_kernel(
     __builtin_amdgcn_s_waitcnt(0);
     if (it + 1 < n_iters) zero_tail(it + 1, vnext);
     __syncthreads();
+    const int j = it + 2;
+    if (j < n_iters) {  // block-uniform
+      const int p_hi = (min((j + 1) * kKeys, count_max) - 1) >> shift;
+      if (p_hi >= wbase + kPrefillLdsPages) {
+        wbase = (j * kKeys) >> shift;
+        load_window(wbase);
+        __syncthreads();
+      }
+    }
   };
   // An iteration whose keys are valid for every row: straight-line code.
   // The next iteration's rows are staged unconditionally (past the last

@@ -8,19 +8,18 @@
 // process_kv_tile (kernels/attention_ops.mojo:165-253), then its one-segment
 // merge (kernels/logsum_merge.mojo:28-122).
 //
-// A row is one (query token, q head).  A pair of waves owns 32 rows = 4
-// tokens x the 8 q heads of one kv head; wave 2p + h of the pair takes dims
-// 256h .. 256h + 255: it holds the Q^T fragments of those dims (64
-// registers) and the O^T accumulator of those output dims (128 registers),
-// the budget of the 256-dim kernel.  Per 32-key iteration each wave forms
-// its half of the scores, S_h^T = K[:, dims of h] . Q_h^T (16 x
-// v_mfma_f32_32x32x16_bf16), the two halves are exchanged through LDS and
-// added in the fixed order S_0 + S_1, so both waves of the pair hold the
-// same score bits, run the same softmax and fold, and each accumulates its
-// own output dims: O_h^T += V^T[dims of h] . P'^T (8 dim blocks x 2 tiles,
-// + lo).  A block of 4 waves (one per SIMD, one block per CU) owns 8 tokens;
-// a plan query block of 64 tokens is 8 such blocks.  Every K and V fragment
-// read from LDS feeds 32 rows, as in the 256-dim kernel.
+// A row is one (query token, q head).  A wave owns 32 rows = 4 tokens x the
+// 8 q heads of one kv head, with all 512 dims: the O^T accumulator of all
+// 512 output dims fills the 256 AGPRs, and the Q^T fragments of the rows
+// (128 VGPRs; 64 for bq codes) leave the other 128 VGPRs to the scores, the
+// softmax and the operand reads (one group of V^T reads and two K reads in
+// flight; the staging addresses are a scalar base plus a 32-bit lane
+// offset).  Each wave therefore computes its rows' whole scores itself,
+// S^T = K . Q^T (32 x v_mfma_f32_32x32x16_bf16 per 32 keys), runs their
+// softmax once, and accumulates O^T += V^T . P'^T over its 16 dim blocks.  A block of 4 waves (one per SIMD, one block per CU)
+// owns 16 tokens = 128 rows sharing each staged K/V tile; a plan query block
+// of 64 tokens is 4 such blocks.  Every K and V fragment read from LDS feeds
+// 32 rows.
 //
 // The C layout, the per-tile softmax (softmax_tile), the folded rescales
 // with the per-row scale S, the hi + lo bf16 parts of P under the kLoShare
@@ -28,19 +27,23 @@
 // into LDS (32 keys of 1 KiB rows, double-buffered) and the transposing
 // V^T reads are those of prefill_full_mfma_kernel (prefill.hip).
 //
+// The run's page table is held in LDS as a window of kWLdsPages entries,
+// moved forward at an iteration boundary when the next staged keys pass its
+// end, so a run of any length stays on this kernel.
+//
 // kBq: the butterquant variant (BqFlashPrefillFullKernel, butterquant_
 // kernels/attention.mojo:267-351, at Gemma-4's bq full layer, modeling/
 // gemma_4_moe_bq.mojo:527-553).  K codes (512-byte rows) are staged straight
-// into LDS; each wave's score half is sum k*q over its dims from
-// v_mfma_i32_32x32x32_i8 plus 128 * sum q over those dims, so the two halves
-// add (as integers, exactly) to the reference's VNNI raw dot, and the score
-// is formed in the reference's order, ((raw - qi_bias) * f_q) * k_scale /
-// 127^2.  V codes pass through registers to LDS as bf16 (exact for int8)
-// and the V scale enters the weight as (w * v_scale) / 127.
+// into LDS; the score's integer part is sum k*q over the 512 dims from
+// v_mfma_i32_32x32x32_i8 plus 128 * sum q, the reference's VNNI raw dot
+// (it reads k ^ 0x80 as unsigned), and the score is formed in the
+// reference's order, ((raw - qi_bias) * f_q) * k_scale / 127^2.  V codes
+// pass through registers to LDS as bf16 (exact for int8) and the V scale
+// enters the weight as (w * v_scale) / 127.
 //
 // Blocks run in an XCD-aware order: launch block b runs work item
 // (b % 8) * per_xcd + b / 8, so the consecutive items of one plan query
-// block (its 8 sub-blocks x kv heads) run on one XCD and share its L2.
+// block (its 4 sub-blocks x kv heads) run on one XCD and share its L2.
 #include <type_traits>
 
 #include "common.hpp"
@@ -53,22 +56,19 @@ namespace {
 using namespace prefill;
 
 constexpr int kWD = 512;                   // head_dim
-constexpr int kWHalf = kWD / 2;            // dims per wave of a pair
 constexpr int kWG = 8;                     // q heads per kv head
-constexpr int kWTokensPerPair = 32 / kWG;  // 4 tokens x 8 heads = 32 rows
-constexpr int kWTokens = (kPWaves / 2) * kWTokensPerPair;  // 8 tokens per block
-constexpr int kWSub = kPrefillTokens / kWTokens;            // blocks per plan query block
+constexpr int kWTokensPerWave = 32 / kWG;  // 4 tokens x 8 heads = 32 rows
+constexpr int kWTokens = kPWaves * kWTokensPerWave;  // 16 tokens per block
+constexpr int kWSub = kPrefillTokens / kWTokens;     // blocks per plan query block
 constexpr int kWKeys = 32;                 // keys per iteration (one S block, two tiles)
 constexpr int kWRowBytes = kWD * 2;        // one key row of K or V in LDS
 constexpr int kWTileBytes = kWKeys * kWRowBytes;  // 32 KiB
-constexpr int kWDimBlocks = kWHalf / 32;   // 32-dim blocks of a wave's O^T
+constexpr int kWDimBlocks = kWD / 32;      // 32-dim blocks of O^T
 constexpr int kWStageRows = kWKeys / kPWaves;  // key rows each wave stages
-constexpr int kWXBytes = 64 * 16 * 4;      // one wave's score half (16 floats per lane)
-constexpr int kWLdsPages = 2048;           // page-table entries held in LDS
+constexpr int kWLdsPages = 2048;           // page-table window held in LDS
 constexpr int kXcds = 8;
 static_assert(kPrefillTokens % kWTokens == 0, "plan query blocks split into kernel blocks");
-static_assert(4 * kWTileBytes + kPWaves * kWXBytes + 4 * kWLdsPages <= 160 * 1024,
-              "LDS budget");
+static_assert(4 * kWTileBytes + 4 * kWLdsPages <= 160 * 1024, "LDS budget");
 
 typedef int wi32x4_t __attribute__((ext_vector_type(4)));
 typedef int wi32x16_t __attribute__((ext_vector_type(16)));
@@ -87,7 +87,6 @@ void prefill_wide_mfma_kernel(
   __shared__ __align__(16) uint8_t kbuf1[kBq ? kWKeys * kWBqRowBytes : kWTileBytes];
   __shared__ __align__(16) uint8_t vbuf0[kWTileBytes];
   __shared__ __align__(16) uint8_t vbuf1[kWTileBytes];
-  __shared__ __align__(16) uint8_t xbuf[kPWaves * kWXBytes];
   __shared__ int32_t page_rows[kWLdsPages];
   // bq: the staged keys' K scales (0 .. 31) and V scales (32 .. 63), per buffer.
   __shared__ __align__(16) float scl[2][kBq ? 2 * kWKeys : 1];
@@ -95,8 +94,6 @@ void prefill_wide_mfma_kernel(
   if (item >= num_items) return;  // block-uniform, before any barrier
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int pair = wave >> 1;
-  const int dh = wave & 1;  // dim half of this wave
   const int lane = tid & 63;
   const int half = lane >> 5;
   const int row = lane & 31;
@@ -117,34 +114,33 @@ void prefill_wide_mfma_kernel(
   // Keys the block needs: [0, count_max).
   const int count_max = base_pos + (t0 + ntok - 1 - buf_start) + 1;
   const int n_iters = (count_max + kWKeys - 1) / kWKeys;
+  const int n_pages = count_max > 0 ? ((count_max - 1) >> shift) + 1 : 0;
 
-  // This lane's row: token 4*pair + (l%32)/8, q head 8g + (l%32)%8.
-  const int tok_local = pair * kWTokensPerPair + (row >> 3);
+  // This lane's row: token 4*wave + (l%32)/8, q head 8g + (l%32)%8.
+  const int tok_local = wave * kWTokensPerWave + (row >> 3);
   const int head = g * kWG + (row & 7);
   const bool row_live = tok_local < ntok;
   const int tok = t0 + tok_local;
   const int count = row_live ? base_pos + (tok - buf_start) + 1 : 0;
-  const int pair_first = pair * kWTokensPerPair;
-  const int pair_last = min(ntok, pair_first + kWTokensPerPair) - 1;
-  const int pair_count = pair_first < ntok ? base_pos + (t0 + pair_last - buf_start) + 1 : 0;
-  // Keys below pair_min are valid for every row of the pair.
-  const int pair_min = pair_first + kWTokensPerPair <= ntok
-                           ? base_pos + (t0 + pair_first - buf_start) + 1
+  const int wave_first = wave * kWTokensPerWave;
+  const int wave_last = min(ntok, wave_first + kWTokensPerWave) - 1;
+  const int wave_count = wave_first < ntok ? base_pos + (t0 + wave_last - buf_start) + 1 : 0;
+  // Keys below wave_min are valid for every row of the wave.
+  const int wave_min = wave_first + kWTokensPerWave <= ntok
+                           ? base_pos + (t0 + wave_first - buf_start) + 1
                            : 0;
 
-  // Q^T fragments of this wave's dims: lane holds
-  // Q[row][256*dh + 16*d + 8*half .. +7] for 16-dim steps d.  In AGPRs, as in
-  // the 256-dim kernel.
-  // bq: the codes Q[row][256*dh + 32*d + 16*half .. +15], 128 * sum of the
-  // wave's 256 codes of the row, and the row's bias and f_q.
-  constexpr int kQFrags = kBq ? kWHalf / 32 : kWHalf / 16;
+  // Q^T fragments: lane holds Q[row][16*d + 8*half .. +7] for the 32 16-dim
+  // steps d.  bq: the codes Q[row][32*d + 16*half .. +15] for the 16 32-dim
+  // steps, 128 * the sum of the row's 512 codes, and its bias and f_q.
+  constexpr int kQFrags = kBq ? kWD / 32 : kWD / 16;
   using QFrag = typename std::conditional<kBq, wi32x4_t, bf16x8_t>::type;
   QFrag qf[kQFrags];
   int qs128 = 0;
   float qb_row = 0.0f, fq_row = 0.0f;
   const int64_t q_row = static_cast<int64_t>(row_live ? tok : t0) * num_q + head;
   if constexpr (kBq) {
-    const int8_t* qr = static_cast<const int8_t*>(qp) + q_row * kWD + kWHalf * dh + 16 * half;
+    const int8_t* qr = static_cast<const int8_t*>(qp) + q_row * kWD + 16 * half;
     int qs = 0;
 #pragma unroll
     for (int d = 0; d < kQFrags; ++d) {
@@ -161,16 +157,14 @@ void prefill_wide_mfma_kernel(
     qb_row = qi_bias[q_row];
     fq_row = f_q[q_row];
   } else {
-    const uint16_t* qr =
-        static_cast<const uint16_t*>(qp) + q_row * kWD + kWHalf * dh + 8 * half;
+    const uint16_t* qr = static_cast<const uint16_t*>(qp) + q_row * kWD + 8 * half;
 #pragma unroll
     for (int d = 0; d < kQFrags; ++d) {
       const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
       qf[d] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
-#pragma unroll
-  for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
+  // The fragments stay in VGPRs: the accumulators fill the 256 AGPRs.
 
   // acc = acc_stored * S (prefill_full_mfma_kernel's scheme).
   f32x16_t acc[kWDimBlocks];
@@ -180,8 +174,13 @@ void prefill_wide_mfma_kernel(
     for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
   float m = kNegBig, l = 0.0f, S = 1.0f;
 
-  const int n_pages = count_max > 0 ? ((count_max - 1) >> shift) + 1 : 0;
-  for (int i = tid; i < n_pages; i += kPThreads) page_rows[i] = rows[i];
+  // Page-table window: LDS entry i holds the run's page wbase + i.
+  int wbase = 0;
+  auto load_window = [&](int first) {
+    const int n = min(kWLdsPages, n_pages - first);
+    for (int i = tid; i < n; i += kPThreads) page_rows[i] = rows[first + i];
+  };
+  load_window(0);
   __syncthreads();
 
   // Staging: wave w moves key rows kWStageRows*w .. +7 of K and of V.  bf16:
@@ -198,14 +197,14 @@ void prefill_wide_mfma_kernel(
   const int8_t* kbase8 = static_cast<const int8_t*>(kcp) + static_cast<int64_t>(g) * kWD;
   const int8_t* vbase8 = static_cast<const int8_t*>(vcp) + static_cast<int64_t>(g) * kWD;
   uint4 vcodes[kBq ? kWStageRows / 2 : 1];
+  auto page_of = [&](int key) { return page_rows[(key >> shift) - wbase]; };
   auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst, int buf) {
     if constexpr (kBq) {
 #pragma unroll
       for (int i = 0; i < kWStageRows / 2; ++i) {
         const int r = wave * kWStageRows + 2 * i + (lane >> 5);
         const int key = min(it * kWKeys + r, count_max - 1);
-        const int64_t off =
-            (static_cast<int64_t>(page_rows[key >> shift]) + (key & row_mask)) * kv_stride;
+        const int64_t off = (static_cast<int64_t>(page_of(key)) + (key & row_mask)) * kv_stride;
         const int c = lane & 31;
         __builtin_amdgcn_global_load_lds(
             kbase8 + off + 16 * (c ^ (r & 15)),
@@ -214,8 +213,7 @@ void prefill_wide_mfma_kernel(
       }
       if (wave == 0) {
         const int key = min(it * kWKeys + (lane & 31), count_max - 1);
-        const int64_t si =
-            (static_cast<int64_t>(page_rows[key >> shift]) + (key & row_mask)) * num_kv + g;
+        const int64_t si = (static_cast<int64_t>(page_of(key)) + (key & row_mask)) * num_kv + g;
         __builtin_amdgcn_global_load_lds((lane < 32 ? k_scale : v_scale) + si,
                                          (lds_void_t*)(&scl[buf][0]), 4, 0, 0);
       }
@@ -224,19 +222,43 @@ void prefill_wide_mfma_kernel(
       for (int i = 0; i < kWStageRows; ++i) {
         const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
         const int key = min(it * kWKeys + r, count_max - 1);
-        const int prow = __builtin_amdgcn_readfirstlane(page_rows[key >> shift]);
+        const int prow = __builtin_amdgcn_readfirstlane(page_of(key));
         const int64_t off = (static_cast<int64_t>(prow) + (key & row_mask)) * kv_stride;
         const uint8_t* krow = reinterpret_cast<const uint8_t*>(kbase + off);  // uniform
         const uint8_t* vrow = reinterpret_cast<const uint8_t*>(vbase + off);
-        const uint32_t lk =
-            static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
-        const uint32_t lv =
-            static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+        uint32_t lk = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
+        uint32_t lv = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+        // Opaque lane offsets: the address stays a uniform base plus a 32-bit
+        // lane offset (the load's scalar-base form) rather than 64-bit lane
+        // addresses hoisted out of the loop.
+        asm volatile("" : "+v"(lk), "+v"(lv));
         __builtin_amdgcn_global_load_lds(krow + lk, (lds_void_t*)(kdst + r * kWRowBytes), 16,
                                          0, 0);
         __builtin_amdgcn_global_load_lds(vrow + lv, (lds_void_t*)(vdst + r * kWRowBytes), 16,
                                          0, 0);
       }
+    }
+  };
+  // bf16, an iteration whose keys all lie below count_max, pages of >= 8
+  // rows: a wave's kWStageRows rows (a multiple of 8 from the iteration's
+  // start) sit in one page, reached by one lookup.
+  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+    const int key0 = it * kWKeys + wave * kWStageRows;  // wave-uniform
+    const int prow = __builtin_amdgcn_readfirstlane(page_of(key0));
+    const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+    const uint8_t* krow0 = reinterpret_cast<const uint8_t*>(kbase + slot0 * kv_stride);
+    const uint8_t* vrow0 = reinterpret_cast<const uint8_t*>(vbase + slot0 * kv_stride);
+    const int64_t row_bytes = 2 * kv_stride;
+#pragma unroll
+    for (int i = 0; i < kWStageRows; ++i) {
+      const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
+      uint32_t lk = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
+      uint32_t lv = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+      asm volatile("" : "+v"(lk), "+v"(lv));
+      __builtin_amdgcn_global_load_lds(krow0 + i * row_bytes + lk,
+                                       (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vrow0 + i * row_bytes + lv,
+                                       (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
     }
   };
   // After the wave's loads have landed: bf16 zeroes the V rows of keys past
@@ -283,107 +305,88 @@ void prefill_wide_mfma_kernel(
   if (n_iters > 0) land_v(0, vbuf0);
   __syncthreads();
 
-  // QK operand reads: chunk 32*dh + 2d + half of key row (row & 31), stored
-  // at chunk (32*dh + 2d + half) ^ (row & 15): byte address k_lane ^ 32d.
-  const int k_lane = row * kWRowBytes + 512 * dh + 16 * ((row & 15) ^ half);
-  // Transposing V^T reads, as in prefill_full_mfma_kernel at 1 KiB rows,
-  // offset to this wave's dims.
+  // QK operand reads: chunk 2d + half of key row (row & 31), stored at chunk
+  // (2d + half) ^ (row & 15): byte address k_lane ^ 32d.
+  const int k_lane = row * kWRowBytes + 16 * ((row & 15) ^ half);
+  // Transposing V^T reads, as in prefill_full_mfma_kernel at 1 KiB rows.
   const int vj = lane & 15;
-  const int v_row = (4 * half + (vj >> 2)) * kWRowBytes + 512 * dh +
+  const int v_row = (4 * half + (vj >> 2)) * kWRowBytes +
                     32 * (((lane >> 4) & 1) ^ ((vj >> 2) & 1)) + 8 * (vj & 3);
   const int v_even = v_row + 64 * (vj >> 3);
   const int v_odd = v_row - 64 * (vj >> 3);
-  // Score halves: chunk c of lane l at byte 1024*c + 16*l of the wave's slot.
-  uint8_t* x_own = xbuf + wave * kWXBytes + 16 * lane;
-  const uint8_t* x_s0 = xbuf + (wave & ~1) * kWXBytes + 16 * lane;
-  const uint8_t* x_s1 = xbuf + (wave | 1) * kWXBytes + 16 * lane;
-
-  // bq K operand reads: chunk 16*dh + 2d + half of key row (row & 31) of
-  // 512 bytes, stored at (16*dh + 2d + half) ^ (row & 15): kq_lane ^ 32d.
-  const int kq_lane = row * kWBqRowBytes + 256 * dh + 16 * ((row & 15) ^ half);
+  // bq K operand reads: chunk 2d + half of key row (row & 31) of 512 bytes,
+  // stored at (2d + half) ^ (row & 15): kq_lane ^ 32d.
+  const int kq_lane = row * kWBqRowBytes + 16 * ((row & 15) ^ half);
   constexpr float kInv127 = 1.0f / 127.0f;
   constexpr float kInv127Sq = kInv127 * kInv127;
 
-  constexpr int kKAhead = 6;
-  // This wave's half of the scores.  bq: the integer dot over its dims plus
-  // 128 * its sum q, carried as bits in the float vector.
-  auto qk = [&](const uint8_t* kl) -> f32x16_t {
+  constexpr int kKAhead = 2;
+  // The rows' scores over the 32 staged keys (value 4j + i holds key
+  // 8j + 4*half + i of the block).  bq: ((raw - qi_bias) * f_q) * k_scale /
+  // 127^2 with raw the integer dot plus 128 * sum q.
+  auto qk = [&](const uint8_t* kl, int buf) -> f32x16_t {
     if constexpr (kBq) {
       wi32x16_t si;
 #pragma unroll
       for (int v = 0; v < 16; ++v) si[v] = 0;
       uint4 kf[kQFrags];
 #pragma unroll
-      for (int d = 0; d < kQFrags; ++d)
+      for (int d = 0; d < kKAhead; ++d)
         kf[d] = *reinterpret_cast<const uint4*>(kl + (kq_lane ^ (32 * d)));
 #pragma unroll
-      for (int d = 0; d < kQFrags; ++d)
+      for (int d = 0; d < kQFrags; ++d) {
+        if (d + kKAhead < kQFrags)
+          kf[d + kKAhead] =
+              *reinterpret_cast<const uint4*>(kl + (kq_lane ^ (32 * (d + kKAhead))));
         si = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(wi32x4_t, kf[d]), qf[d],
                                                    si, 0, 0, 0);
-      f32x16_t bits;
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) bits[v] = __int_as_float(si[v] + qs128);
-      return bits;
-    } else {
-    f32x16_t sblk;
+      for (int d = 0; d < kQFrags - kKAhead; ++d) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
+      f32x16_t sfull;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
-    uint4 kf[kWHalf / 16];
-#pragma unroll
-    for (int d = 0; d < kKAhead; ++d)
-      kf[d] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * d)));
-#pragma unroll
-    for (int d = 0; d < kWHalf / 16; ++d) {
-      if (d + kKAhead < kWHalf / 16)
-        kf[d + kKAhead] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * (d + kKAhead))));
-      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]), qf[d],
-                                                     sblk, 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
-#pragma unroll
-    for (int d = 0; d < kWHalf / 16 - kKAhead; ++d) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
-    return sblk;
-    }
-  };
-  // The pair's full scores: own half out, barrier, the other half in, added
-  // as S_0 + S_1 in both waves.  bq: the integer halves add exactly to the
-  // raw dot; the score is then ((raw - qi_bias) * f_q) * k_scale / 127^2
-  // (value 4j + i holds key 8j + 4*half + i of the block).
-  auto exchange = [&](const f32x16_t& own, int buf) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<float4*>(x_own + 1024 * c) =
-          make_float4(own[4 * c], own[4 * c + 1], own[4 * c + 2], own[4 * c + 3]);
-    __syncthreads();
-    f32x16_t sfull;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float4 a = *reinterpret_cast<const float4*>(x_s0 + 1024 * c);
-      const float4 b = *reinterpret_cast<const float4*>(x_s1 + 1024 * c);
-      if constexpr (kBq) {
+      for (int c = 0; c < 4; ++c) {
         const float4 ks4 = *reinterpret_cast<const float4*>(&scl[buf][8 * c + 4 * half]);
-        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
         const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int raw = __float_as_int(av[i]) + __float_as_int(bv[i]);
-          float sc = static_cast<float>(raw) - qb_row;
+          float sc = static_cast<float>(si[4 * c + i] + qs128) - qb_row;
           sc = sc * fq_row;
           sc = sc * ks[i];
           sfull[4 * c + i] = sc * kInv127Sq;
         }
-      } else {
-        sfull[4 * c] = a.x + b.x;
-        sfull[4 * c + 1] = a.y + b.y;
-        sfull[4 * c + 2] = a.z + b.z;
-        sfull[4 * c + 3] = a.w + b.w;
       }
+      return sfull;
+    } else {
+      f32x16_t sblk;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
+      uint4 kf[kQFrags];
+#pragma unroll
+      for (int d = 0; d < kKAhead; ++d)
+        kf[d] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * d)));
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d) {
+        if (d + kKAhead < kQFrags)
+          kf[d + kKAhead] =
+              *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * (d + kKAhead))));
+        sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]),
+                                                       qf[d], sblk, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+      for (int d = 0; d < kQFrags - kKAhead; ++d) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
+      return sblk;
     }
-    return sfull;
   };
   auto softmax_pair = [&](const f32x16_t& sblk, int tile_key0, bool masked, float (&w)[2][8],
                           float (&corr)[2], bool (&big)[2]) {
@@ -400,8 +403,8 @@ void prefill_wide_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[u][i] = 0.0f;
         const int tk = tile_key0 + 16 * u;
-        if (tk < pair_count) {  // wave-uniform (the same in both waves of the pair)
-          if (tk + 16 <= pair_min) {
+        if (tk < wave_count) {  // wave-uniform
+          if (tk + 16 <= wave_min) {
             softmax_tile<false>(sv, 16, half, m, l, corr[u], w[u], big[u]);
           } else {
             const int valid = min(16, max(0, count - tk));
@@ -412,7 +415,7 @@ void prefill_wide_mfma_kernel(
     }
   };
   // Fold of the two tiles and acc_stored += V^T P''^T (prefill.hip's fold_pv
-  // on one 32-key block).
+  // on one 32-key block, over the 16 dim blocks).
   auto fold_pv = [&](const uint8_t* vl, const float (&w0)[2][8], const float (&corr)[2],
                      const bool (&big)[2], int buf) {
     // bq: the weights as (w * v_scale) / 127; lane value i of tile u is key
@@ -480,23 +483,19 @@ void prefill_wide_mfma_kernel(
       for (int b = 0; b < 4; ++b)
         acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], p, acc[b0 + b], 0, 0, 0);
     };
-    {
-      bf16x8_t ga[4], gb[4];
-      read_group(0, 0, ga);
-      read_group(0, 4, gb);
-      mfma_group(phi[0], 0, ga);
-      read_group(1, 0, ga);
-      mfma_group(phi[0], 4, gb);
-      read_group(1, 4, gb);
-      mfma_group(phi[1], 0, ga);
-      mfma_group(phi[1], 4, gb);
-      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    // Eight groups of four MFMAs (tile u, dim blocks 4q .. 4q+3), each
+    // group's V^T reads issued one group ahead.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        bf16x8_t ga[4];
+        read_group(u, 4 * q, ga);
+        mfma_group(phi[u], 4 * q, ga);
+      }
     }
+    // A tile's lo parts (p - bf16(p)) in a pass of their own when some row
+    // of the wave has its big flag.
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       if (__builtin_amdgcn_ballot_w64(big[u]) != 0) {  // wave-uniform
@@ -504,53 +503,40 @@ void prefill_wide_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
-        bf16x8_t ga[4], gb[4];
-        read_group(u, 0, ga);
-        read_group(u, 4, gb);
-        mfma_group(plo, 0, ga);
-        mfma_group(plo, 4, gb);
-        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bf16x8_t ga[4];
+          read_group(u, 4 * q, ga);
+          mfma_group(plo, 4 * q, ga);
+        }
       }
     }
   };
 
+  // End of iteration it: the next iteration's rows have landed (each wave
+  // waits for its own loads; the barrier publishes them to the block).  If
+  // the keys staged during the next iteration (those of iteration it + 2)
+  // reach past the page-table window, the window moves to their first page
+  // (nothing reads it between the barrier and the refill's barrier).
   auto iteration_end = [&](int it, uint8_t* vnext) {
 #pragma unroll
     for (int b = 0; b < kWDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
-#pragma unroll
-    for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
     __builtin_amdgcn_s_waitcnt(0);
     if (it + 1 < n_iters) land_v(it + 1, vnext);
     __syncthreads();
+    const int j = it + 2;
+    if (j < n_iters) {  // block-uniform
+      const int p_hi = (min((j + 1) * kWKeys, count_max) - 1) >> shift;
+      if (p_hi >= wbase + kWLdsPages) {
+        wbase = (j * kWKeys) >> shift;
+        load_window(wbase);
+        __syncthreads();
+      }
+    }
   };
   // An iteration whose keys are valid for every row of the block.  The
   // next iteration's rows are staged unconditionally (past the last
   // iteration they are clamped, in-bounds rows of an unused buffer).
-  // bf16: the staging of an iteration whose keys all lie below count_max,
-  // with pages of >= 8 rows: a wave's kWStageRows rows (a multiple of 8 from
-  // the iteration's start) sit in one page, reached by one lookup.  (Int8
-  // keeps the per-row lookups: its forms of this spill or measured slower.)
-  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
-    const int key0 = it * kWKeys + wave * kWStageRows;  // wave-uniform
-    const int prow = __builtin_amdgcn_readfirstlane(page_rows[key0 >> shift]);
-    const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
-    const uint8_t* krow0 = reinterpret_cast<const uint8_t*>(kbase + slot0 * kv_stride);
-    const uint8_t* vrow0 = reinterpret_cast<const uint8_t*>(vbase + slot0 * kv_stride);
-    const int64_t row_bytes = 2 * kv_stride;
-#pragma unroll
-    for (int i = 0; i < kWStageRows; ++i) {
-      const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
-      const uint32_t lk =
-          static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
-      const uint32_t lv =
-          static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
-      __builtin_amdgcn_global_load_lds(krow0 + i * row_bytes + lk,
-                                       (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vrow0 + i * row_bytes + lv,
-                                       (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
-    }
-  };
   auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                             uint8_t* vnext) {
     if (!kBq && shift >= 3 && (it + 2) * kWKeys <= count_max)  // block-uniform
@@ -559,12 +545,12 @@ void prefill_wide_mfma_kernel(
       stage(it + 1, knext, vnext, (it + 1) & 1);
     float w[2][8], corr[2];
     bool big[2];
-    const f32x16_t s = exchange(qk(kl), it & 1);
+    const f32x16_t s = qk(kl, it & 1);
     softmax_pair(s, 0, false, w, corr, big);
     fold_pv(vl, w, corr, big, it & 1);
     iteration_end(it, vnext);
   };
-  // An iteration on the causal diagonal: per-tile masks (a pair whose rows
+  // An iteration on the causal diagonal: per-tile masks (a wave whose rows
   // all end before a tile gets corr 1 and zero weights for it).  One call
   // site with the buffers chosen at run time keeps the register allocation
   // of the whole kernel within the register file.
@@ -574,7 +560,7 @@ void prefill_wide_mfma_kernel(
     if (it + 1 < n_iters) stage(it + 1, knext, vnext, (it + 1) & 1);
     float w[2][8], corr[2];
     bool big[2];
-    const f32x16_t s = exchange(qk(kl), it & 1);
+    const f32x16_t s = qk(kl, it & 1);
     softmax_pair(s, key_base, true, w, corr, big);
     fold_pv(vl, w, corr, big, it & 1);
     iteration_end(it, vnext);
@@ -598,15 +584,13 @@ void prefill_wide_mfma_kernel(
   }
 
   // ---- one-segment merge and bf16 store (PrefillMergeKernel) ----
-  // Lane l holds dims 256*dh + 32*b + 8*j + 4*half + i (value 4*j + i of
-  // block b).
+  // Lane l holds dims 32*b + 8*j + 4*half + i (value 4*j + i of block b).
   if (row_live) {
     const float c0 = l > 0.0f ? fexp(max_ref(-87.0f, m - m)) : 0.0f;
     const float gl = l * c0;
     const bool live = gl > 0.0f;
     const float inv_l = live ? 1.0f / gl : 0.0f;
-    uint16_t* dst =
-        out + (static_cast<int64_t>(tok) * num_q + head) * kWD + kWHalf * dh + 4 * half;
+    uint16_t* dst = out + (static_cast<int64_t>(tok) * num_q + head) * kWD + 4 * half;
 #pragma unroll
     for (int b = 0; b < kWDimBlocks; ++b) {
 #pragma unroll
@@ -625,8 +609,6 @@ void prefill_wide_mfma_kernel(
 }
 
 }  // namespace
-
-int prefill_wide_max_pages() { return kWLdsPages; }
 
 hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const void* q,
                                     const void* k, const void* v, void* output, int num_q,

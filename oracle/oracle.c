@@ -59,7 +59,8 @@
  *
  * Parity left unpinned (no way to run Mojo here): the lane order of Mojo's
  * SIMD.reduce_add (taken as the halving tree of SIMD.reduce), FMA contraction
- * of `a*b - c*d` in RoPE and of `l*corr + sum` (taken as not contracted), the
+ * of `a*b - c*d` in RoPE, of `l*corr + sum` and of fexp's `a_magic*x + bias_f`
+ * (all taken as not contracted; the fexp tests build the same choice in), the
  * f32->bf16 cast (taken as RNE, butterquant/convert.mojo:14-17), the order of
  * the sum of squares in the head RMS norm (VDPBF16PS pairs into port_unroll
  * accumulators, below float64 agreement) and fptosi in

@@ -97,6 +97,26 @@ def test_prefill_page_sizes(page_len):
     assert_bar(r, f"prefill page_len={page_len}")
 
 
+@pytest.mark.parametrize("page_len", [4, 8])
+def test_prefill_long_run_moves_the_page_window(page_len):
+    """Runs whose page table outgrows the kernel's LDS window of 4,096
+    entries (40,000 cached positions: 5,000 pages of 8 rows, 10,000 of 4)
+    stay on the MFMA route; the window moves along the run once or twice."""
+    announce(f"prefill beyond the LDS page window, page_len={page_len}")
+    prefix, new = [40000, 100], [70, 64]
+    case = make_prefill_case(31 + page_len, prefix, new, page_len=page_len)
+    n = sum(new)
+    q = seeded_bf16(n * NUM_Q * HEAD_DIM, 41)
+    k = seeded_bf16(case.cache_rows * KV_STRIDE, 42)
+    v = seeded_bf16(case.cache_rows * KV_STRIDE, 43)
+    got = _prefill(case, n, to_dev(q), to_dev(k), to_dev(v), page_len=page_len)
+    ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=NUM_Q,
+                           num_kv=NUM_KV, head_dim=HEAD_DIM, kv_stride=KV_STRIDE, window=0,
+                           cache_size=page_len, page_len=page_len, seq_len=n, cap=16,
+                           threads=16)
+    assert_bar(compare_bf16(got, ref), f"prefill long run page_len={page_len}")
+
+
 def test_prefill_config4_shape_append_then_attend():
     """Config 4: 8 sequences append 2048 tokens each onto prefixes ~ U[0,16384]
     (RoPE + cache write for the whole chunk, then causal prefill).  The cache

@@ -92,16 +92,19 @@ def test_wide_prefill_page_sizes(page_len):
     assert_bar(r, f"wide prefill page_len {page_len}")
 
 
-def test_wide_prefill_long_run_takes_token_route():
-    """A run whose page table outgrows the kernel's LDS copy (2,200 pages of
-    8 rows) runs the token-partitioned route with the same results."""
-    announce("wide prefill beyond the LDS page table")
-    prefix, new = [17500, 40], [20, 30]
-    case = make_prefill_case(15, prefix, new, page_len=8)
+@pytest.mark.parametrize("page_len", [4, 8])
+def test_wide_prefill_long_run_moves_the_page_window(page_len):
+    """Runs whose page table outgrows the kernel's LDS window of 2,048
+    entries (40,000 cached positions: 5,000 pages of 8 rows, 10,000 of 4)
+    stay on the MFMA route; the window moves along the run two to four
+    times."""
+    announce(f"wide prefill beyond the LDS page window, page_len={page_len}")
+    prefix, new = [40000, 40], [20, 30]
+    case = make_prefill_case(15 + page_len, prefix, new, page_len=page_len)
     n = sum(new)
     r = _prefill(case, n, seeded_bf16(n * NQ * D, 16), seeded_bf16(case.cache_rows * KVS, 17),
-                 seeded_bf16(case.cache_rows * KVS, 18), page_len=8)
-    assert_bar(r, "wide prefill long run")
+                 seeded_bf16(case.cache_rows * KVS, 18), page_len=page_len)
+    assert_bar(r, f"wide prefill long run page_len={page_len}")
 
 
 def test_wide_prefill_8x2048_append_then_attend():
