@@ -371,10 +371,8 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   int64_t n_qblocks = 0;
   // The full-attention kernels hold a window of the run's page table in LDS
   // and take runs of any length; the sliding kernel holds the whole ring, so
-  // the ring must fit, and the window's span must be whole 16-key tiles (the
-  // kernel aligns every row's tiles to 16 up to lo % 16).
-  const bool mfma_tables_fit =
-      !sliding || (g.page_mask + 1 <= kPrefillLdsPages && window % kTile == 0);
+  // the ring must fit.
+  const bool mfma_tables_fit = !sliding || g.page_mask + 1 <= kPrefillLdsPages;
   if ((mode == IFR_PLAN_TOKEN_MERGE || mode == IFR_PLAN_TOKEN_DIRECT) && mfma_tables_fit) {
     std::vector<std::array<int64_t, 4>> qbs;
     for (int64_t r = 0; r < num_runs; ++r) {
@@ -1099,6 +1097,22 @@ int32_t bq_attention(const void* image_dev, const int64_t* info, const void* q_i
                 static_cast<int>(num_q), static_cast<int>(num_kv), kv_stride, g,
                 static_cast<int>(info[12]), as_stream(stream)),
             "prefill_sliding_mfma_bq");
+    if (o_i8)
+      IFR_HIP(ifr::launch_bq_block_quant(output, o_i8, o_sa, num_q * head_dim,
+                                         static_cast<int>(head_dim), info[5],
+                                         as_stream(stream)),
+              "bq_block_quant");
+    return ok();
+  }
+  if (info[2] == IFR_PLAN_TOKEN_MERGE && info[14] > 0 && head_dim == 256 &&
+      num_q == 2 * num_kv && page_mask < 0) {
+    // Prefill chunk of a full-attention layer at head_dim 256 / GQA 2.
+    IFR_HIP(ifr::launch_prefill_full_mfma_bq(
+                static_cast<const int32_t*>(image_dev), static_cast<int>(info[14]), q_i8,
+                qi_bias, f_q, k_base, k_scale, v_base, v_scale, output,
+                static_cast<int>(num_q), static_cast<int>(num_kv), kv_stride, g,
+                as_stream(stream)),
+            "prefill_full_mfma_bq");
     if (o_i8)
       IFR_HIP(ifr::launch_bq_block_quant(output, o_i8, o_sa, num_q * head_dim,
                                          static_cast<int>(head_dim), info[5],

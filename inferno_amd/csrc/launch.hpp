@@ -49,6 +49,13 @@ hipError_t launch_prefill_full_mfma(const int32_t* image_dev, int num_qblocks,
                                     const void* v_base, void* output, int num_q,
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream);
+// The same over butterquant int8 KV (f32 scales per row and kv head).
+hipError_t launch_prefill_full_mfma_bq(const int32_t* image, int num_qblocks, const void* q_i8,
+                                       const float* qi_bias, const float* f_q, const void* k,
+                                       const float* k_scale, const void* v,
+                                       const float* v_scale, void* output, int num_q,
+                                       int num_kv, int64_t kv_stride, PagedGeom geom,
+                                       hipStream_t stream);
 // The same for head_dim 512 / 8 q heads per kv head (prefill_wide.hip).
 hipError_t launch_prefill_wide_mfma_bq(const int32_t* image, int num_qblocks, const void* q_i8,
                                        const float* qi_bias, const float* f_q, const void* k,
@@ -61,8 +68,8 @@ hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream);
 
-// MFMA chunked prefill, sliding window (head_dim 256, gqa 2, window a
-// multiple of 16): the finalised output of every query block.
+// MFMA chunked prefill, sliding window (head_dim 256, gqa 2): the finalised
+// output of every query block.
 hipError_t launch_prefill_sliding_mfma(const int32_t* image_dev, int num_qblocks,
                                        const void* q, const void* k_base, const void* v_base,
                                        void* output, int num_q, int num_kv, int64_t kv_stride,

@@ -43,6 +43,17 @@
 // page table is held in LDS.
 // Blocks are numbered kv-head-fastest so every block of a kv head lands on
 // one XCD (block id mod 8) and shares that XCD's L2.
+//
+// kBq: the butterquant variant (BqFlashPrefillFullKernel, butterquant_
+// kernels/attention.mojo:267-351) at 16 q / 8 kv x 256, with the sliding
+// kernel's int8 pieces: K codes (256-byte rows) staged straight into LDS,
+// scores from v_mfma_i32_32x32x32_i8 plus 128 * sum q (the reference's VNNI
+// raw dot, which reads k ^ 0x80 as unsigned) formed in the reference's order
+// ((raw - qi_bias) * f_q) * k_scale / 127^2, V codes through registers into
+// the bf16 V tile (exact for int8), and the V scale entering each weight as
+// (w * v_scale) / 127.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "prefill_common.hpp"
@@ -52,21 +63,31 @@ namespace {
 
 using namespace prefill;
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kBqRowBytes = kPD;  // one kv head's row of int8 codes
+
 // One wave per SIMD (up to 512 VGPR + AGPR per lane); one block per CU.
+template <bool kBq>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_full_mfma_kernel(
-    const int32_t* __restrict__ image, const uint16_t* __restrict__ q,
-    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int32_t* __restrict__ image, const void* __restrict__ qp,
+    const float* __restrict__ qi_bias, const float* __restrict__ f_q,
+    const void* __restrict__ kcp, const float* __restrict__ k_scale,
+    const void* __restrict__ vcp, const float* __restrict__ v_scale,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride,
     int shift, int row_mask) {
   // Two K and two V buffers as separate LDS objects: the LDS reads of one
   // buffer then provably do not alias the loads landing in the other, and
   // no wait for those loads is inserted before the reads.
-  __shared__ __align__(16) uint8_t kbuf0[kTileBytes];
-  __shared__ __align__(16) uint8_t kbuf1[kTileBytes];
+  __shared__ __align__(16) uint8_t kbuf0[kBq ? kKeys * kBqRowBytes : kTileBytes];
+  __shared__ __align__(16) uint8_t kbuf1[kBq ? kKeys * kBqRowBytes : kTileBytes];
   __shared__ __align__(16) uint8_t vbuf0[kTileBytes];
   __shared__ __align__(16) uint8_t vbuf1[kTileBytes];
   __shared__ int32_t page_rows[kPrefillLdsPages];
+  // bq: the staged keys' K and V scales, per buffer.
+  __shared__ __align__(16) float kscl[2][kBq ? kKeys : 1];
+  __shared__ __align__(16) float vscl[2][kBq ? kKeys : 1];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -103,13 +124,37 @@ void prefill_full_mfma_kernel(
                            ? base_pos + (t0 + wave_first - buf_start) + 1
                            : 0;
 
-  // Q^T fragments: lane holds Q[row][16*d + 8*half .. +7] for 16-dim steps d.
-  bf16x8_t qf[kPD / 16];
-  {
-    const uint16_t* qr =
-        q + (static_cast<int64_t>(row_live ? tok : t0) * num_q + head) * kPD + 8 * half;
+  // Q^T fragments.  bf16: lane holds Q[row][16*d + 8*half .. +7] for 16-dim
+  // steps d; bq: the codes Q[row][32*d + 16*half .. +15], with the row's
+  // 128 * sum q, bias and f_q.
+  constexpr int kQFrags = kBq ? kPD / 32 : kPD / 16;
+  using QFrag = typename std::conditional<kBq, i32x4_t, bf16x8_t>::type;
+  QFrag qf[kQFrags];
+  int qs128 = 0;
+  float qb_row = 0.0f, fq_row = 0.0f;
+  const int64_t q_row = static_cast<int64_t>(row_live ? tok : t0) * num_q + head;
+  if constexpr (kBq) {
+    const int8_t* qr = static_cast<const int8_t*>(qp) + q_row * kPD + 16 * half;
+    int qs = 0;
 #pragma unroll
-    for (int d = 0; d < kPD / 16; ++d) {
+    for (int d = 0; d < kQFrags; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * d);
+      qf[d] = __builtin_bit_cast(i32x4_t, v);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.x), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, qs, false);
+      qs = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, qs, false);
+    }
+    // The row's other 128 codes are in lane ^ 32.
+    const auto sw = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(qs),
+                                                    static_cast<uint32_t>(qs), false, false);
+    qs128 = 128 * (static_cast<int>(sw[0]) + static_cast<int>(sw[1]));
+    qb_row = qi_bias[q_row];
+    fq_row = f_q[q_row];
+  } else {
+    const uint16_t* qr = static_cast<const uint16_t*>(qp) + q_row * kPD + 8 * half;
+#pragma unroll
+    for (int d = 0; d < kQFrags; ++d) {
       const uint4 v = *reinterpret_cast<const uint4*>(qr + 16 * d);
       qf[d] = __builtin_bit_cast(bf16x8_t, v);
     }
@@ -117,7 +162,7 @@ void prefill_full_mfma_kernel(
   // The Q^T fragments live in AGPRs (MFMA operands may come from there),
   // which leaves the VGPRs to the softmax and the operand reads.
 #pragma unroll
-  for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
+  for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
 
   // The O^T accumulator is kept as acc_stored with acc = acc_stored * S: a
   // tile's rescale multiplies S, and the weights entering the MFMA are
@@ -150,10 +195,43 @@ void prefill_full_mfma_kernel(
   // holds global chunk p ^ (key & 15), for V chunk p ^ 2*(key & 3).  Keys past count_max read the last
   // key (in bounds); their V rows are zeroed once the last iteration's
   // loads have landed.
-  const uint16_t* kbase = kc + static_cast<int64_t>(g) * kPD;
-  const uint16_t* vbase = vc + static_cast<int64_t>(g) * kPD;
+  // bq: K code rows of 256 bytes, four per load (lane p: row p / 16, LDS
+  // chunk p % 16 holding global chunk (p % 16) ^ (key & 15)); V codes to
+  // registers (the same rows, 16 codes from 16 * (p % 16)), written to LDS as
+  // bf16 rows once landed; wave 0 moves the 64 keys' K and V scales.
+  const uint16_t* kbase = static_cast<const uint16_t*>(kcp) + static_cast<int64_t>(g) * kPD;
+  const uint16_t* vbase = static_cast<const uint16_t*>(vcp) + static_cast<int64_t>(g) * kPD;
+  const int8_t* kbase8 = static_cast<const int8_t*>(kcp) + static_cast<int64_t>(g) * kPD;
+  const int8_t* vbase8 = static_cast<const int8_t*>(vcp) + static_cast<int64_t>(g) * kPD;
   const int stage_row0 = wave * kStageRows + half;
-  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+  auto slot_of = [&](int key) -> int64_t {
+    return static_cast<int64_t>(page_rows[(key >> shift) - wbase]) + (key & row_mask);
+  };
+  uint4 vcodes[kBq ? kStageRows / 4 : 1];
+  auto stage_scales = [&](int it, int buf) {
+    if (wave == 0) {
+      const int key = min(it * kKeys + lane, count_max - 1);
+      const int64_t si = slot_of(key) * num_kv + g;
+      __builtin_amdgcn_global_load_lds(k_scale + si, (lds_void_t*)(&kscl[buf][0]), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds(v_scale + si, (lds_void_t*)(&vscl[buf][0]), 4, 0, 0);
+    }
+  };
+  auto stage = [&](int it, uint8_t* kdst, uint8_t* vdst, int buf) {
+    if constexpr (kBq) {
+#pragma unroll
+      for (int i = 0; i < kStageRows / 4; ++i) {
+        const int rr = wave * kStageRows + 4 * i + (lane >> 4);
+        const int key = min(it * kKeys + rr, count_max - 1);
+        const int64_t off = slot_of(key) * kv_stride;
+        const int c = lane & 15;
+        __builtin_amdgcn_global_load_lds(
+            kbase8 + off + 16 * (c ^ (rr & 15)),
+            (lds_void_t*)(kdst + (wave * kStageRows + 4 * i) * kBqRowBytes), 16, 0, 0);
+        vcodes[i] = *reinterpret_cast<const uint4*>(vbase8 + off + 16 * c);
+      }
+      stage_scales(it, buf);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < kStageRows / 2; ++i) {
       const int r = stage_row0 + 2 * i;  // key row within the iteration
@@ -178,15 +256,35 @@ void prefill_full_mfma_kernel(
   // the base, i.e. i * 4 * kv_stride (uniform) + hk (lane); its K chunk
   // row ^ rr = (row ^ half) ^ 2i gives the byte offset x16 ^ 32i, its V
   // chunk row ^ 2*(rr & 3) one of two lane constants (i even or odd).
-  const int hk = half * static_cast<int>(kv_stride) * 2;
-  const uint32_t x16 = 16u * static_cast<uint32_t>(row ^ half);
-  const uint32_t hv0 = static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(row ^ (2 * half));
+  // bq: row rr = 4i + lr (lr = lane / 16) at i * 4 * kv_stride + lr *
+  // kv_stride bytes, K chunk (c ^ lr) ^ 4i.
+  const int lr = lane >> 4;
+  const int cq = lane & 15;
+  const int hk = kBq ? lr * static_cast<int>(kv_stride) : half * static_cast<int>(kv_stride) * 2;
+  const uint32_t x16 = kBq ? 16u * static_cast<uint32_t>(cq ^ lr)
+                           : 16u * static_cast<uint32_t>(row ^ half);
+  const uint32_t hv0 = kBq ? static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(cq)
+                           : static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(row ^ (2 * half));
   const uint32_t hv1 =
       static_cast<uint32_t>(hk) + 16u * static_cast<uint32_t>(row ^ (4 + 2 * half));
-  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
+  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst, int buf) {
     const int key0 = it * kKeys + wave * kStageRows;  // wave-uniform
     const int prow = __builtin_amdgcn_readfirstlane(page_rows[(key0 >> shift) - wbase]);
     const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+    if constexpr (kBq) {
+      const char* kb = reinterpret_cast<const char*>(kbase8 + slot0 * kv_stride);
+      const char* vb = reinterpret_cast<const char*>(vbase8 + slot0 * kv_stride);
+      const int64_t step = 4 * kv_stride;
+#pragma unroll
+      for (int i = 0; i < kStageRows / 4; ++i) {
+        __builtin_amdgcn_global_load_lds(
+            kb + i * step + (static_cast<uint32_t>(hk) + (x16 ^ (64u * i))),
+            (lds_void_t*)(kdst + (wave * kStageRows + 4 * i) * kBqRowBytes), 16, 0, 0);
+        vcodes[i] = *reinterpret_cast<const uint4*>(vb + i * step + hv0);
+      }
+      stage_scales(it, buf);
+      return;
+    }
     const char* kb = reinterpret_cast<const char*>(kbase + slot0 * kv_stride);
     const char* vb = reinterpret_cast<const char*>(vbase + slot0 * kv_stride);
     const int64_t step = 4 * kv_stride;  // bytes from row pair i to i + 1
@@ -200,9 +298,36 @@ void prefill_full_mfma_kernel(
                                        (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
     }
   };
-  // V rows of keys >= count_max in this wave's staged rows become zeros
-  // (after the wave's own loads into them have landed).
+  // After the wave's loads have landed: bf16 zeroes the V rows of keys past
+  // count_max; bq writes its V codes as bf16 rows (the bf16 swizzle: chunk c
+  // of row rr at c ^ 2*(rr & 3)), zeros past count_max.
   auto zero_tail = [&](int it, uint8_t* vdst) {
+    if constexpr (kBq) {
+#pragma unroll
+      for (int i = 0; i < kStageRows / 4; ++i) {
+        const int rr = wave * kStageRows + 4 * i + (lane >> 4);
+        const bool in = it * kKeys + rr < count_max;
+        const uint32_t w[4] = {vcodes[i].x, vcodes[i].y, vcodes[i].z, vcodes[i].w};
+        uint32_t bf[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int b = 0; b < 4; b += 2) {
+            const float f0 = static_cast<float>(static_cast<int8_t>(w[j] >> (8 * b)));
+            const float f1 = static_cast<float>(static_cast<int8_t>(w[j] >> (8 * b + 8)));
+            bf[2 * j + b / 2] =
+                in ? ((__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u)) : 0u;
+          }
+        }
+        const int c0 = 2 * (lane & 15);
+        uint8_t* vr = vdst + rr * kRowBytes;
+        *reinterpret_cast<uint4*>(vr + 16 * (c0 ^ (2 * (rr & 3)))) =
+            make_uint4(bf[0], bf[1], bf[2], bf[3]);
+        *reinterpret_cast<uint4*>(vr + 16 * ((c0 + 1) ^ (2 * (rr & 3)))) =
+            make_uint4(bf[4], bf[5], bf[6], bf[7]);
+      }
+      return;
+    }
     if ((it + 1) * kKeys <= count_max) return;  // block-uniform
 #pragma unroll
     for (int i = 0; i < kStageRows / 2; ++i) {
@@ -213,7 +338,7 @@ void prefill_full_mfma_kernel(
     }
   };
 
-  if (n_iters > 0) stage(0, kbuf0, vbuf0);
+  if (n_iters > 0) stage(0, kbuf0, vbuf0, 0);
   __builtin_amdgcn_s_waitcnt(0);  // the Q fragments and iteration 0's rows
   if (n_iters > 0) zero_tail(0, vbuf0);
   __syncthreads();
@@ -239,10 +364,47 @@ void prefill_full_mfma_kernel(
   const int v_even = v_row + 64 * (vj >> 3);
   const int v_odd = v_row - 64 * (vj >> 3);
 
-  // S^T of tile pair h (32 keys) of the staged iteration.
-  // The K operand reads run kKAhead steps ahead of their MFMAs.
+  // bq K operand reads: chunk 2d + half of key row (row & 31) of 256 bytes,
+  // stored at (2d + half) ^ (row & 15): byte address kq_lane ^ 32d.
+  const int kq_lane = row * kBqRowBytes + 16 * ((row & 15) ^ half);
+  constexpr float kInv127 = 1.0f / 127.0f;
+  constexpr float kInv127Sq = kInv127 * kInv127;
+
+  // S^T of tile pair h (32 keys) of the staged iteration (buffer buf).
+  // The K operand reads run kKAhead steps ahead of their MFMAs.  bq:
+  // ((raw - qi_bias) * f_q) * k_scale / 127^2 per (row, key), raw the
+  // integer dot plus 128 * sum q; value 4j + i holds key 8j + 4*half + i.
   constexpr int kKAhead = 6;
-  auto qk = [&](const uint8_t* kl, int h) {
+  auto qk = [&](const uint8_t* kl, int h, int buf) {
+    if constexpr (kBq) {
+      i32x16_t si;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) si[v] = 0;
+      const uint8_t* kh = kl + 32 * h * kBqRowBytes;
+      uint4 kf[kQFrags];
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d)
+        kf[d] = *reinterpret_cast<const uint4*>(kh + (kq_lane ^ (32 * d)));
+#pragma unroll
+      for (int d = 0; d < kQFrags; ++d)
+        si = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, kf[d]), qf[d],
+                                                   si, 0, 0, 0);
+      f32x16_t sblk;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 ks4 =
+            *reinterpret_cast<const float4*>(&kscl[buf][32 * h + 8 * j + 4 * half]);
+        const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float sc = static_cast<float>(si[4 * j + i] + qs128) - qb_row;
+          sc = sc * fq_row;
+          sc = sc * ks[i];
+          sblk[4 * j + i] = sc * kInv127Sq;
+        }
+      }
+      return sblk;
+    }
     f32x16_t sblk;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
@@ -300,8 +462,29 @@ void prefill_full_mfma_kernel(
   // Fold of the pair and acc_stored += V^T P''^T:
   // acc*c_a*c_b + w_a*c_b V_a + w_b V_b = S' (acc_stored + (w_a*c_b V_a +
   // w_b V_b) / S'),  S' = S*c_a*c_b.
-  auto fold_pv = [&](const uint8_t* vl, int h, const float (&w)[2][8], const float (&corr)[2],
-                     const bool (&big)[2]) {
+  auto fold_pv = [&](const uint8_t* vl, int h, const float (&w0)[2][8], const float (&corr)[2],
+                     const bool (&big)[2], int buf) {
+    // bq: the weights as (w * v_scale) / 127; lane value i of tile u is key
+    // 32h + 16u + 8*(i/4) + 4*half + i%4.
+    float w[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float vs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (kBq) {
+          const float4 v4 = *reinterpret_cast<const float4*>(
+              &vscl[buf][32 * h + 16 * u + 8 * j + 4 * half]);
+          vs[0] = v4.x;
+          vs[1] = v4.y;
+          vs[2] = v4.z;
+          vs[3] = v4.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[u][4 * j + i] = kBq ? (w0[u][4 * j + i] * vs[i]) * kInv127 : w0[u][4 * j + i];
+      }
+    }
     float S_new = S * (corr[0] * corr[1]);
     if (__builtin_amdgcn_ballot_w64(S_new < 0x1p-64f) != 0) {  // wave-uniform
       // The accumulators are copied to VGPRs here, inside the rare branch
@@ -407,7 +590,7 @@ void prefill_full_mfma_kernel(
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
 #pragma unroll
-    for (int d = 0; d < kPD / 16; ++d) asm volatile("" : "+a"(qf[d]));
+    for (int d = 0; d < kQFrags; ++d) asm volatile("" : "+a"(qf[d]));
     __builtin_amdgcn_s_waitcnt(0);
     if (it + 1 < n_iters) zero_tail(it + 1, vnext);
     __syncthreads();
@@ -427,36 +610,38 @@ void prefill_full_mfma_kernel(
   // staging shares a block with the score MFMAs.
   auto full_iteration = [&](bool page_stage, int it, const uint8_t* kl, const uint8_t* vl,
                             uint8_t* knext, uint8_t* vnext) {
+    const int buf = it & 1;
     if (page_stage)  // block-uniform
-      stage_page(it + 1, knext, vnext);
+      stage_page(it + 1, knext, vnext, buf ^ 1);
     else
-      stage(it + 1, knext, vnext);
+      stage(it + 1, knext, vnext, buf ^ 1);
     // Straight-line order that lets the pair-1 scores (MFMA) run under the
     // pair-0 softmax (VALU), and the pair-0 PV (MFMA) under the pair-1
     // softmax.
     float w0[2][8], c0[2], w1[2][8], c1[2];
     bool g0[2], g1[2];
-    const f32x16_t s0 = qk(kl, 0);
-    const f32x16_t s1 = qk(kl, 1);
+    const f32x16_t s0 = qk(kl, 0, buf);
+    const f32x16_t s1 = qk(kl, 1, buf);
     softmax_pair(s0, 0, false, w0, c0, g0);
-    fold_pv(vl, 0, w0, c0, g0);
+    fold_pv(vl, 0, w0, c0, g0, buf);
     softmax_pair(s1, 0, false, w1, c1, g1);
-    fold_pv(vl, 1, w1, c1, g1);
+    fold_pv(vl, 1, w1, c1, g1, buf);
     iteration_end(it, vnext);
   };
   // An iteration on the causal diagonal: per-tile masks.
   auto masked_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                               uint8_t* vnext) {
     const int key_base = it * kKeys;
-    if (it + 1 < n_iters) stage(it + 1, knext, vnext);
+    const int buf = it & 1;
+    if (it + 1 < n_iters) stage(it + 1, knext, vnext, buf ^ 1);
 #pragma unroll 1
     for (int h = 0; h < kBlocks; ++h) {
       if (key_base + 32 * h >= wave_count) break;  // wave-uniform
       float w[2][8], corr[2];
       bool big[2];
-      const f32x16_t sb = qk(kl, h);
+      const f32x16_t sb = qk(kl, h, buf);
       softmax_pair(sb, key_base + 32 * h, true, w, corr, big);
-      fold_pv(vl, h, w, corr, big);
+      fold_pv(vl, h, w, corr, big, buf);
     }
     iteration_end(it, vnext);
   };
@@ -516,11 +701,24 @@ hipError_t launch_prefill_full_mfma(const int32_t* image, int num_qblocks, const
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(prefill_full_mfma_kernel, dim3(num_qblocks * num_kv), dim3(kPThreads),
-                     0, stream, image, static_cast<const uint16_t*>(q),
-                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                     static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
-                     geom.row_mask);
+  hipLaunchKernelGGL(prefill_full_mfma_kernel<false>, dim3(num_qblocks * num_kv),
+                     dim3(kPThreads), 0, stream, image, q, nullptr, nullptr, k, nullptr, v,
+                     nullptr, static_cast<uint16_t*>(output), num_q, num_kv, kv_stride,
+                     geom.shift, geom.row_mask);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_full_mfma_bq(const int32_t* image, int num_qblocks, const void* q_i8,
+                                       const float* qi_bias, const float* f_q, const void* k,
+                                       const float* k_scale, const void* v,
+                                       const float* v_scale, void* output, int num_q,
+                                       int num_kv, int64_t kv_stride, PagedGeom geom,
+                                       hipStream_t stream) {
+  if (num_qblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(prefill_full_mfma_kernel<true>, dim3(num_qblocks * num_kv),
+                     dim3(kPThreads), 0, stream, image, q_i8, qi_bias, f_q, k, k_scale, v,
+                     v_scale, static_cast<uint16_t*>(output), num_q, num_kv, kv_stride,
+                     geom.shift, geom.row_mask);
   return hipGetLastError();
 }
 

@@ -20,10 +20,12 @@
 // exactly the reference's per-tile steps.  The weights of aligned tile t - 1
 // are then complete (its low part belonged to tile J - 1, its high part to J)
 // and its P.V MFMA runs; tile t's low-part weights wait one step.  Rows whose
-// window lies before the tile, or that ended earlier, add nothing.  A final
-// step past the last staged tile completes the last reference tile of rows
-// with r = 0.  Pads (keys past p in the last tile of a row with lo = 0) score
-// -1e30: their fexp(-87) enters l, a zero weight P.V.
+// window lies before the tile, or that ended earlier, add nothing.  A row's
+// last tile J_K (K = (p - lo) / 16) completes at aligned step
+// lo / 16 + K + 1, which a final step past the last staged tile covers.
+// Pads (keys past p in a row's last tile: with lo = 0, or when the window is
+// not a multiple of 16, in its high or its low part) score -1e30: their
+// fexp(-87) enters l, a zero weight P.V.
 //
 // As in the full kernel the accumulator is kept as acc_stored with acc =
 // acc_stored * S; a weight enters the MFMA divided by S right after its own
@@ -110,9 +112,10 @@ void prefill_sliding_mfma_kernel(
   const int p = p_first + tok_local;
   const int lo = max(0, p - window + 1);
   const int r = lo & 15;
-  // Aligned tiles at which the row completes a reference tile: (t_first, t_end].
+  // Aligned tiles at which the row completes a reference tile: (t_first,
+  // t_end], t_end the step of its last tile J_K, K = (p - lo) / 16.
   const int t_first = row_live ? (lo >> 4) : (1 << 30);
-  const int t_end = row_live ? (p >> 4) + (r == 0 ? 1 : 0) : -1;
+  const int t_end = row_live ? (lo >> 4) + ((p - lo) >> 4) + 1 : -1;
 
   // Q^T fragments.  bf16: lane holds Q[row][16*d + 8*half .. +7]; bq: the
   // codes Q[row][32*d + 16*half .. +15], with the row's 128 * sum q, bias
@@ -466,7 +469,7 @@ void prefill_sliding_mfma_kernel(
     for (int i = 0; i < 8; ++i) {
       const int kk = key_of(i);
       low[i] = kk < r;
-      const bool pad = !low[i] && (16 * (t - 1) + kk > p);
+      const bool pad = (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
       sel[i] = (fin && !pad) ? (low[i] ? st[i] : s_prev[i]) : kNegBig;
     }
     float mx = fmaxf(fmaxf(fmaxf(sel[0], sel[1]), fmaxf(sel[2], sel[3])),
@@ -507,7 +510,7 @@ void prefill_sliding_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kk = key_of(i);
-      const bool pad = !low[i] && (16 * (t - 1) + kk > p);
+      const bool pad = (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
       const float w = (fin && !pad) ? e[i] * inv_s : 0.0f;
       pw[i] = low[i] ? pend[i] : w;
       pend[i] = low[i] ? w : 0.0f;

@@ -320,7 +320,9 @@ void prefill_wide_mfma_kernel(
   constexpr float kInv127 = 1.0f / 127.0f;
   constexpr float kInv127Sq = kInv127 * kInv127;
 
-  constexpr int kKAhead = 2;
+  // K operand reads in flight ahead of their MFMAs (measured best: 6 for
+  // bf16, 4 for the int8 codes).
+  constexpr int kKAhead = kBq ? 4 : 6;
   // The rows' scores over the 32 staged keys (value 4j + i holds key
   // 8j + 4*half + i of the block).  bq: ((raw - qi_bias) * f_q) * k_scale /
   // 127^2 with raw the integer dot plus 128 * sum q.
@@ -483,8 +485,8 @@ void prefill_wide_mfma_kernel(
       for (int b = 0; b < 4; ++b)
         acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], p, acc[b0 + b], 0, 0, 0);
     };
-    // Eight groups of four MFMAs (tile u, dim blocks 4q .. 4q+3), each
-    // group's V^T reads issued one group ahead.
+    // Eight groups of four MFMAs (tile u, dim blocks 4q .. 4q+3), one group
+    // of V^T reads in flight (a second one does not fit the VGPRs left).
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll

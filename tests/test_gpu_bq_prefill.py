@@ -1,7 +1,8 @@
 """GPU parity of the butterquant MFMA prefill -- sliding windows at head_dim
 256 / GQA 2 (BqFlashPrefillSlidingKernel, butterquant_kernels/attention.mojo:
-170-264) and full attention at Gemma-4's full-layer shape, head_dim 512 /
-GQA 8 (BqFlashPrefillFullKernel, :267-351) -- against the oracle's bq token
+170-264) and full attention (BqFlashPrefillFullKernel, :267-351) at head_dim
+256 / GQA 2 and at Gemma-4's full-layer shape, head_dim 512 / GQA 8 --
+against the oracle's bq token
 route: int8 K/V codes with f32 scales per row
 and kv head, int8 queries with their bias (128 * sum q) and f_q.  The scores
 come from an int8 MFMA and are formed in the reference's order, so they
@@ -96,7 +97,7 @@ def _run(window, prefix, new, ring, page_len, seed, q_scale=1.0, quant=False):
     return compare_bf16(got, ref)
 
 
-@pytest.mark.parametrize("window", [16, 48, 64, 1024])
+@pytest.mark.parametrize("window", [16, 48, 64, 1024, 1, 17, 100, 1023])
 def test_bq_sliding_prefill_windows(window):
     """Chunks from position 0, inside the first window and far past it; full
     and partial query blocks."""
@@ -122,8 +123,10 @@ def test_bq_sliding_prefill_page_sizes(page_len, ring):
     assert_bar(r, f"page_len {page_len}")
 
 
-def _run_full(prefix, new, page_len, seed, quant=False):
-    """Full attention at head_dim 512 / GQA 8 over page lists (no ring)."""
+def _run_full(prefix, new, page_len, seed, quant=False, shape=(WNQ, WNKV, WD)):
+    """Full attention over page lists (no ring): by default at head_dim 512 /
+    GQA 8, or at the shape given (head_dim 256 / GQA 2)."""
+    WNQ, WNKV, WD = shape
     case = make_prefill_case(seed, prefix, new, page_len=page_len)
     runs, rows, cache_rows = case.runs, case.base_rows, case.cache_rows
     kvs = WNKV * WD
@@ -132,7 +135,7 @@ def _run_full(prefix, new, page_len, seed, quant=False):
     q = _codes(n * WNQ * WD, seed + 2)
     qb = (128.0 * q.reshape(n * WNQ, WD).astype(np.int64).sum(axis=1)).astype(np.float32)
     # A 512-dim dot has sqrt(2) times the spread of a 256-dim one.
-    fq = rng.uniform(0.35, 1.05, n * WNQ).astype(np.float32)
+    fq = (rng.uniform(0.35, 1.05, n * WNQ) * np.sqrt(512 / WD)).astype(np.float32)
     k = _codes(cache_rows * kvs, seed + 3, outliers=True)
     v = _codes(cache_rows * kvs, seed + 4)
     ks = rng.uniform(0.5, 1.5, cache_rows * WNKV).astype(np.float32)
@@ -178,3 +181,29 @@ def test_bq_full_layer_prefill_page_sizes(page_len):
     announce(f"bq mfma full-layer prefill page_len={page_len}")
     r = _run_full([0, 900, 2500], [96, 129, 64], page_len, 23)
     assert_bar(r, f"full layer page_len {page_len}")
+
+
+def test_bq_full_attention_prefill_hd256():
+    """Full attention at 16 q / 8 kv x 256 on the int8 MFMA route: chunks from
+    position 0, short and long prefixes, partial query blocks, a one-token
+    chunk; the o_proj block quant on top."""
+    announce("bq mfma full-attention prefill hd256")
+    r = _run_full([0, 100, 1000, 3000, 63, 5], [40, 33, 100, 64, 1, 7], 64, 31, quant=True,
+                  shape=(NQ, NKV, D))
+    assert_bar(r, "full attention hd256")
+
+
+@pytest.mark.parametrize("page_len", [8, 1024])
+def test_bq_full_attention_prefill_hd256_page_sizes(page_len):
+    """Pages of 8 rows (the per-row staging) and of 1,024."""
+    announce(f"bq mfma full-attention prefill hd256 page_len={page_len}")
+    r = _run_full([0, 900, 2500], [96, 129, 64], page_len, 33, shape=(NQ, NKV, D))
+    assert_bar(r, f"full attention hd256 page_len {page_len}")
+
+
+def test_bq_full_attention_prefill_hd256_long_run():
+    """A run of 40,000 cached positions in pages of 8 rows (5,000 pages) moves
+    the kernel's 4,096-entry page-table window once."""
+    announce("bq mfma full-attention prefill hd256 long run")
+    r = _run_full([40000, 50], [70, 30], 8, 35, shape=(NQ, NKV, D))
+    assert_bar(r, "full attention hd256 long run")

@@ -17,7 +17,7 @@ GPU and every output of every query token is compared with the oracle.
 - config 11 (sliding window 1024 on 64-page rings): append + sliding MFMA
   prefill (FlashPrefillSlidingKernel, kernels/flash_attention_prefill.mojo:
   18-114), checked the same way.
-- --kv bq forms of configs 11 and 12: the append is bq prep
+- --kv bq forms of configs 4, 11 and 12: the append is bq prep
   (butterquant_kernels/attention.mojo:494-632), whose codes, scales, q codes,
   q biases and f_q are compared whole and bit for bit; the attention
   (BqFlashPrefill{Sliding,Full}Kernel, :170-351) is held to the same bar.
@@ -214,3 +214,15 @@ def test_fullsize_config11_bq_sliding_prefill():
     w.setup(torch.device("cuda:0"), _args(11))
     assert int(w.plan.info[14]) > 0, "config 11 bq must take the MFMA prefill route"
     _check_bq(w, 0, w.window, w.RING * bench.PAGE_LEN, False, "config 11 bq")
+
+
+def test_fullsize_config4_bq_prefill():
+    """bench --config 4 --kv bq: COW of codes and scales, bq prep, and the
+    int8 MFMA prefill at 16 q / 8 kv x 256."""
+    import torch
+
+    announce("fullsize prefill config 4 bq: setup")
+    w = bench.PrefillBf16(SEED, 4, kv="bq")
+    w.setup(torch.device("cuda:0"), _args(4))
+    assert int(w.plan.info[14]) > 0, "config 4 bq must take the MFMA prefill route"
+    _check_bq(w, 1, 0, bench.PAGE_LEN, False, "config 4 bq")

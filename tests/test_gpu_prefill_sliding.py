@@ -59,13 +59,15 @@ def _ref(runs, rows, n, window, ring_pages, q, k, v, page_len=PAGE_LEN):
                             cap=16, threads=16)
 
 
-@pytest.mark.parametrize("window", [16, 48, 64, 304, 1024])
+@pytest.mark.parametrize("window", [16, 48, 64, 304, 1024, 1, 5, 17, 100, 1000, 1023])
 def test_sliding_prefill_windows(window):
     """Chunks that start at position 0, inside the first window, and far past
     it (the window start moves with every token), full and partial query
-    blocks, windows of one tile, of three, and not a power of two."""
+    blocks, windows of one tile, of three, not a power of two, and windows
+    that are not a multiple of 16 (a row's last tile then ends past its
+    position, with pads in the low or the high part of an aligned tile)."""
     announce(f"sliding mfma prefill window={window}")
-    prefix = [0, 5, window - 3, 700, 3000]
+    prefix = [0, 5, max(0, window - 3), 700, 3000]
     new = [100, 64, 129, 77, 200]
     ring = 1 << int(np.ceil(np.log2((window + max(new) + 2 * PAGE_LEN) / PAGE_LEN)))
     runs, rows, cache_rows = _ring_case(window, prefix, new, ring)
