@@ -65,9 +65,26 @@ constexpr double kExpQa = 1.6501418352127075, kExpQb = -0.37554836273193359,
 // 2^-9 * kLoShare * max|v|.
 constexpr float kLoShare = 0x1p-7f;
 
+// F = 1.0 with the mantissa bits of i: (i & 0x7FFFFF) | 0x3F800000 as one
+// v_and_or_b32 (the mask from a scalar register, 1.0 as an inline constant)
+// instead of an AND and an OR that each carry a literal.  The mask's s_mov
+// has no side effects, so the compiler hoists it out of the loops.
+__device__ __forceinline__ float mantissa_one(int32_t i) {
+  uint32_t m, r;
+  asm("s_mov_b32 %0, 0x7fffff" : "=s"(m));
+  asm("v_and_or_b32 %0, %1, %2, 1.0" : "=v"(r) : "v"(i), "s"(m));
+  return __uint_as_float(r);
+}
+// The maximum of 8 values as three v_max3_f32 and one v_max_f32 (the
+// maximum of finite values is the same in any order).
+__device__ __forceinline__ float max8(const float (&v)[8]) {
+  return fmaxf(fmaxf(fmaxf(v[0], v[1]), v[2]),
+               fmaxf(fmaxf(fmaxf(v[3], v[4]), v[5]), fmaxf(v[6], v[7])));
+}
+
 __device__ __forceinline__ float fexp_fused_t(float t) {
   const int32_t i = static_cast<int32_t>(t);
-  const float F = __uint_as_float((static_cast<uint32_t>(i) & 0x7FFFFFu) | 0x3F800000u);
+  const float F = mantissa_one(i);
   float p = __builtin_fmaf(F, static_cast<float>(kExpQc), static_cast<float>(kExpQb - 2 * kExpQc));
   p = __builtin_fmaf(F, p, static_cast<float>(kExpQa - kExpQb + kExpQc));
   return __int_as_float(i) * p;
@@ -96,8 +113,7 @@ __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, in
     const int key = 8 * (i >> 2) + 4 * half + (i & 3);
     sc[i] = (!kMasked || key < valid) ? sv[i] : kNegBig;
   }
-  float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
-                   fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+  float mx = max8(sc);
   mx = max_xor32(mx);
   const float m_new = fmaxf(mx, m);
   const float c = fexp_fused(m - m_new);

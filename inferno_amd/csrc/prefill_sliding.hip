@@ -472,8 +472,7 @@ void prefill_sliding_mfma_kernel(
       const bool pad = (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
       sel[i] = (fin && !pad) ? (low[i] ? st[i] : s_prev[i]) : kNegBig;
     }
-    float mx = fmaxf(fmaxf(fmaxf(sel[0], sel[1]), fmaxf(sel[2], sel[3])),
-                     fmaxf(fmaxf(sel[4], sel[5]), fmaxf(sel[6], sel[7])));
+    float mx = max8(sel);
     mx = max_xor32(mx);
     const float m_new = fmaxf(mx, m);
     const float c = fexp_fused(m - m_new);
