@@ -41,9 +41,15 @@
 // pass through registers to LDS as bf16 (exact for int8) and the V scale
 // enters the weight as (w * v_scale) / 127.
 //
-// Blocks run in an XCD-aware order: launch block b runs work item
-// (b % 8) * per_xcd + b / 8, so the consecutive items of one plan query
-// block (its 4 sub-blocks x kv heads) run on one XCD and share its L2.
+// Blocks run in an XCD-aware order.  Workgroups go to the 8 XCDs round
+// robin (block b to XCD b % 8, in order of b on each), and the plan lists
+// its query blocks run-major, longest first.  XCD x takes the plan query
+// blocks x, x + 8, x + 16, ...: every XCD gets an even share of every run
+// (a run-per-XCD split left the XCD holding the longest run working long
+// after the others), the blocks running together on one XCD still belong
+// to one run and walk its keys in step through that XCD's L2, and the
+// items of one query block (4 sub-blocks x kv heads) are consecutive on
+// their XCD.
 #include <type_traits>
 
 #include "common.hpp"
@@ -82,7 +88,7 @@ void prefill_wide_mfma_kernel(
     const void* __restrict__ kcp, const float* __restrict__ k_scale,
     const void* __restrict__ vcp, const float* __restrict__ v_scale,
     uint16_t* __restrict__ out, int num_q, int num_kv, int64_t kv_stride, int shift,
-    int row_mask, int num_items, int per_xcd) {
+    int row_mask, int num_qblocks) {
   __shared__ __align__(16) uint8_t kbuf0[kBq ? kWKeys * kWBqRowBytes : kWTileBytes];
   __shared__ __align__(16) uint8_t kbuf1[kBq ? kWKeys * kWBqRowBytes : kWTileBytes];
   __shared__ __align__(16) uint8_t vbuf0[kWTileBytes];
@@ -90,16 +96,18 @@ void prefill_wide_mfma_kernel(
   __shared__ int32_t page_rows[kWLdsPages];
   // bq: the staged keys' K scales (0 .. 31) and V scales (32 .. 63), per buffer.
   __shared__ __align__(16) float scl[2][kBq ? 2 * kWKeys : 1];
-  const int item = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (item >= num_items) return;  // block-uniform, before any barrier
+  const int items_per_qb = num_kv * kWSub;
+  const int slot = blockIdx.x / kXcds;
+  const int qb = (slot / items_per_qb) * kXcds + blockIdx.x % kXcds;
+  if (qb >= num_qblocks) return;  // block-uniform, before any barrier
+  const int item = slot % items_per_qb;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int half = lane >> 5;
   const int row = lane & 31;
   const int g = item % num_kv;
-  const int sub = (item / num_kv) % kWSub;
-  const int qb = item / (num_kv * kWSub);
+  const int sub = item / num_kv;
 
   const int32_t* blk = image + image[kHdrOffQBlocks] + qb * kQBlockWords;
   const int run = blk[0];
@@ -617,12 +625,11 @@ hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  const int items = num_qblocks * kWSub * num_kv;
-  const int per_xcd = (items + kXcds - 1) / kXcds;
-  hipLaunchKernelGGL(prefill_wide_mfma_kernel<false>, dim3(per_xcd * kXcds), dim3(kPThreads), 0,
+  const int blocks = (num_qblocks + kXcds - 1) / kXcds * kXcds * kWSub * num_kv;
+  hipLaunchKernelGGL(prefill_wide_mfma_kernel<false>, dim3(blocks), dim3(kPThreads), 0,
                      stream, image, q, nullptr, nullptr, k, nullptr, v, nullptr,
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
-                     geom.row_mask, items, per_xcd);
+                     geom.row_mask, num_qblocks);
   return hipGetLastError();
 }
 
@@ -633,12 +640,11 @@ hipError_t launch_prefill_wide_mfma_bq(const int32_t* image, int num_qblocks, co
                                        int num_kv, int64_t kv_stride, PagedGeom geom,
                                        hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  const int items = num_qblocks * kWSub * num_kv;
-  const int per_xcd = (items + kXcds - 1) / kXcds;
-  hipLaunchKernelGGL(prefill_wide_mfma_kernel<true>, dim3(per_xcd * kXcds), dim3(kPThreads), 0,
+  const int blocks = (num_qblocks + kXcds - 1) / kXcds * kXcds * kWSub * num_kv;
+  hipLaunchKernelGGL(prefill_wide_mfma_kernel<true>, dim3(blocks), dim3(kPThreads), 0,
                      stream, image, q_i8, qi_bias, f_q, k, k_scale, v, v_scale,
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
-                     geom.row_mask, items, per_xcd);
+                     geom.row_mask, num_qblocks);
   return hipGetLastError();
 }
 
