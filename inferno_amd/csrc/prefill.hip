@@ -375,6 +375,19 @@ void prefill_full_mfma_kernel(
   // ((raw - qi_bias) * f_q) * k_scale / 127^2 per (row, key), raw the
   // integer dot plus 128 * sum q; value 4j + i holds key 8j + 4*half + i.
   constexpr int kKAhead = 6;
+  // bf16 page staging split into 16 single loads (K then V of row pair i
+  // for load j = 2i, 2i + 1), so they can be issued between MFMAs.
+  auto page_load = [&](int j, const char* kb, const char* vb, uint8_t* kdst, uint8_t* vdst) {
+    const int i = j >> 1;
+    const int64_t step = 4 * kv_stride;  // bytes from row pair i to i + 1
+    const int lds_row = wave * kStageRows + 2 * i;  // wave-uniform
+    if ((j & 1) == 0)
+      __builtin_amdgcn_global_load_lds(kb + i * step + (static_cast<uint32_t>(hk) + (x16 ^ (32u * i))),
+                                       (lds_void_t*)(kdst + lds_row * kRowBytes), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds(vb + i * step + ((i & 1) ? hv1 : hv0),
+                                       (lds_void_t*)(vdst + lds_row * kRowBytes), 16, 0, 0);
+  };
   auto qk = [&](const uint8_t* kl, int h, int buf) {
     if constexpr (kBq) {
       i32x16_t si;
@@ -429,6 +442,38 @@ void prefill_full_mfma_kernel(
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
+    return sblk;
+  };
+  // bf16 S^T of tile pair h with the next iteration's page-staged loads
+  // 8h .. 8h + 7 issued after the odd MFMAs: a load's issue then overlaps
+  // the MFMA pipe instead of holding up the wave ahead of the scores (the
+  // 64 staging loads of a block take about a thousand cycles to pass the
+  // texture unit).
+  auto qk_staging = [&](const uint8_t* kl, int h, const char* kb, const char* vb,
+                        uint8_t* kdst, uint8_t* vdst) {
+    f32x16_t sblk;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
+    const uint8_t* kh = kl + 32 * h * kRowBytes;
+    uint4 kf[kPD / 16];
+#pragma unroll
+    for (int d = 0; d < kKAhead; ++d)
+      kf[d] = *reinterpret_cast<const uint4*>(kh + (k_lane ^ (32 * d)));
+#pragma unroll
+    for (int d = 0; d < kPD / 16; ++d) {
+      if (d + kKAhead < kPD / 16)
+        kf[d + kKAhead] = *reinterpret_cast<const uint4*>(kh + (k_lane ^ (32 * (d + kKAhead))));
+      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]), qf[d],
+                                                     sblk, 0, 0, 0);
+      if (d & 1) page_load(8 * h + (d >> 1), kb, vb, kdst, vdst);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+    for (int d = 0; d < kPD / 16; ++d) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (d + kKAhead < kPD / 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (d & 1) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    }
     return sblk;
   };
   // Online softmax of the pair's two tiles; tile_key0 is the first key of
@@ -611,17 +656,30 @@ void prefill_full_mfma_kernel(
   auto full_iteration = [&](bool page_stage, int it, const uint8_t* kl, const uint8_t* vl,
                             uint8_t* knext, uint8_t* vnext) {
     const int buf = it & 1;
-    if (page_stage)  // block-uniform
-      stage_page(it + 1, knext, vnext, buf ^ 1);
-    else
-      stage(it + 1, knext, vnext, buf ^ 1);
+    f32x16_t s0, s1;
+    if (!kBq && page_stage) {  // block-uniform
+      // One page lookup for the wave's rows of the next iteration; the
+      // loads go out between the score MFMAs.
+      const int key0 = (it + 1) * kKeys + wave * kStageRows;  // wave-uniform
+      const int prow = __builtin_amdgcn_readfirstlane(page_rows[(key0 >> shift) - wbase]);
+      const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+      const char* kb = reinterpret_cast<const char*>(kbase + slot0 * kv_stride);
+      const char* vb = reinterpret_cast<const char*>(vbase + slot0 * kv_stride);
+      s0 = qk_staging(kl, 0, kb, vb, knext, vnext);
+      s1 = qk_staging(kl, 1, kb, vb, knext, vnext);
+    } else {
+      if (page_stage)  // block-uniform
+        stage_page(it + 1, knext, vnext, buf ^ 1);
+      else
+        stage(it + 1, knext, vnext, buf ^ 1);
+      s0 = qk(kl, 0, buf);
+      s1 = qk(kl, 1, buf);
+    }
     // Straight-line order that lets the pair-1 scores (MFMA) run under the
     // pair-0 softmax (VALU), and the pair-0 PV (MFMA) under the pair-1
     // softmax.
     float w0[2][8], c0[2], w1[2][8], c1[2];
     bool g0[2], g1[2];
-    const f32x16_t s0 = qk(kl, 0, buf);
-    const f32x16_t s1 = qk(kl, 1, buf);
     softmax_pair(s0, 0, false, w0, c0, g0);
     fold_pv(vl, 0, w0, c0, g0, buf);
     softmax_pair(s1, 0, false, w1, c1, g1);

@@ -247,28 +247,6 @@ void prefill_wide_mfma_kernel(
       }
     }
   };
-  // bf16, an iteration whose keys all lie below count_max, pages of >= 8
-  // rows: a wave's kWStageRows rows (a multiple of 8 from the iteration's
-  // start) sit in one page, reached by one lookup.
-  auto stage_page = [&](int it, uint8_t* kdst, uint8_t* vdst) {
-    const int key0 = it * kWKeys + wave * kWStageRows;  // wave-uniform
-    const int prow = __builtin_amdgcn_readfirstlane(page_of(key0));
-    const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
-    const uint8_t* krow0 = reinterpret_cast<const uint8_t*>(kbase + slot0 * kv_stride);
-    const uint8_t* vrow0 = reinterpret_cast<const uint8_t*>(vbase + slot0 * kv_stride);
-    const int64_t row_bytes = 2 * kv_stride;
-#pragma unroll
-    for (int i = 0; i < kWStageRows; ++i) {
-      const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
-      uint32_t lk = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
-      uint32_t lv = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
-      asm volatile("" : "+v"(lk), "+v"(lv));
-      __builtin_amdgcn_global_load_lds(krow0 + i * row_bytes + lk,
-                                       (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vrow0 + i * row_bytes + lv,
-                                       (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
-    }
-  };
   // After the wave's loads have landed: bf16 zeroes the V rows of keys past
   // count_max; bq writes its V codes as bf16 rows (zeros past count_max).
   auto land_v = [&](int it, uint8_t* vdst) {
@@ -397,6 +375,52 @@ void prefill_wide_mfma_kernel(
       __builtin_amdgcn_sched_group_barrier(0x008, kKAhead, 0);
       return sblk;
     }
+  };
+  // bf16 scores with the next iteration's page-staged rows loaded between
+  // the MFMAs (K and V of row i after MFMAs 4i + 1 and 4i + 3): a load's
+  // issue then overlaps the MFMA pipe instead of holding up the wave ahead
+  // of the scores.  kb / vb: the wave's first staged row; kdst / vdst: the
+  // next buffers.
+  auto qk_staging = [&](const uint8_t* kl, const uint8_t* kb, const uint8_t* vb, uint8_t* kdst,
+                        uint8_t* vdst) -> f32x16_t {
+    const int64_t row_bytes = 2 * kv_stride;
+    f32x16_t sblk;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sblk[v] = 0.0f;
+    uint4 kf[kQFrags];
+#pragma unroll
+    for (int d = 0; d < kKAhead; ++d)
+      kf[d] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * d)));
+#pragma unroll
+    for (int d = 0; d < kQFrags; ++d) {
+      if (d + kKAhead < kQFrags)
+        kf[d + kKAhead] = *reinterpret_cast<const uint4*>(kl + (k_lane ^ (32 * (d + kKAhead))));
+      sblk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[d]), qf[d],
+                                                     sblk, 0, 0, 0);
+      if (d & 1) {
+        const int i = d >> 2;
+        const int r = wave * kWStageRows + i;  // wave-uniform key row of the iteration
+        if ((d & 2) == 0) {
+          uint32_t lk = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(16 * (r & 15));
+          asm volatile("" : "+v"(lk));
+          __builtin_amdgcn_global_load_lds(kb + i * row_bytes + lk,
+                                           (lds_void_t*)(kdst + r * kWRowBytes), 16, 0, 0);
+        } else {
+          uint32_t lv = static_cast<uint32_t>(16 * lane) ^ static_cast<uint32_t>(32 * (r & 3));
+          asm volatile("" : "+v"(lv));
+          __builtin_amdgcn_global_load_lds(vb + i * row_bytes + lv,
+                                           (lds_void_t*)(vdst + r * kWRowBytes), 16, 0, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+    for (int d = 0; d < kQFrags; ++d) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (d + kKAhead < kQFrags) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (d & 1) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    }
+    return sblk;
   };
   auto softmax_pair = [&](const f32x16_t& sblk, int tile_key0, bool masked, float (&w)[2][8],
                           float (&corr)[2], bool (&big)[2]) {
@@ -549,13 +573,20 @@ void prefill_wide_mfma_kernel(
   // iteration they are clamped, in-bounds rows of an unused buffer).
   auto full_iteration = [&](int it, const uint8_t* kl, const uint8_t* vl, uint8_t* knext,
                             uint8_t* vnext) {
-    if (!kBq && shift >= 3 && (it + 2) * kWKeys <= count_max)  // block-uniform
-      stage_page(it + 1, knext, vnext);
-    else
+    f32x16_t s;
+    if (!kBq && shift >= 3 && (it + 2) * kWKeys <= count_max) {  // block-uniform
+      // The wave's kWStageRows rows of the next iteration lie in one page.
+      const int key0 = (it + 1) * kWKeys + wave * kWStageRows;  // wave-uniform
+      const int prow = __builtin_amdgcn_readfirstlane(page_of(key0));
+      const int64_t slot0 = static_cast<int64_t>(prow) + (key0 & row_mask);
+      s = qk_staging(kl, reinterpret_cast<const uint8_t*>(kbase + slot0 * kv_stride),
+                     reinterpret_cast<const uint8_t*>(vbase + slot0 * kv_stride), knext, vnext);
+    } else {
       stage(it + 1, knext, vnext, (it + 1) & 1);
+      s = qk(kl, it & 1);
+    }
     float w[2][8], corr[2];
     bool big[2];
-    const f32x16_t s = qk(kl, it & 1);
     softmax_pair(s, 0, false, w, corr, big);
     fold_pv(vl, w, corr, big, it & 1);
     iteration_end(it, vnext);
