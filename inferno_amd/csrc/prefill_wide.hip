@@ -43,13 +43,14 @@
 //
 // Blocks run in an XCD-aware order.  Workgroups go to the 8 XCDs round
 // robin (block b to XCD b % 8, in order of b on each), and the plan lists
-// its query blocks run-major, longest first.  XCD x takes the plan query
-// blocks x, x + 8, x + 16, ...: every XCD gets an even share of every run
-// (a run-per-XCD split left the XCD holding the longest run working long
-// after the others), the blocks running together on one XCD still belong
-// to one run and walk its keys in step through that XCD's L2, and the
-// items of one query block (4 sub-blocks x kv heads) are consecutive on
-// their XCD.
+// its query blocks run-major, longest first.  When num_kv divides 8, XCD x
+// serves kv head x % num_kv and the query blocks x / num_kv, x / num_kv +
+// 8 / num_kv, ...: every XCD gets an even share of every run (a run-per-XCD
+// split left the XCD holding the longest run working long after the
+// others), each key tile is fetched by 8 / num_kv XCDs rather than all 8,
+// and the blocks running together on one XCD belong to one run and kv head
+// and walk its keys in step through that XCD's L2.  Otherwise XCD x takes
+// query blocks x, x + 8, ... with all their kv heads.
 #include <type_traits>
 
 #include "common.hpp"
@@ -96,18 +97,27 @@ void prefill_wide_mfma_kernel(
   __shared__ int32_t page_rows[kWLdsPages];
   // bq: the staged keys' K scales (0 .. 31) and V scales (32 .. 63), per buffer.
   __shared__ __align__(16) float scl[2][kBq ? 2 * kWKeys : 1];
-  const int items_per_qb = num_kv * kWSub;
+  const int x = blockIdx.x % kXcds;
   const int slot = blockIdx.x / kXcds;
-  const int qb = (slot / items_per_qb) * kXcds + blockIdx.x % kXcds;
+  int qb, g, sub;
+  if (kXcds % num_kv == 0) {
+    // XCD x serves kv head x % num_kv and every (8 / num_kv)-th query block.
+    const int lanes = kXcds / num_kv;
+    qb = (slot / kWSub) * lanes + x / num_kv;
+    g = x % num_kv;
+    sub = slot % kWSub;
+  } else {
+    const int items_per_qb = num_kv * kWSub;
+    qb = (slot / items_per_qb) * kXcds + x;
+    g = (slot % items_per_qb) % num_kv;
+    sub = (slot % items_per_qb) / num_kv;
+  }
   if (qb >= num_qblocks) return;  // block-uniform, before any barrier
-  const int item = slot % items_per_qb;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int half = lane >> 5;
   const int row = lane & 31;
-  const int g = item % num_kv;
-  const int sub = item / num_kv;
 
   const int32_t* blk = image + image[kHdrOffQBlocks] + qb * kQBlockWords;
   const int run = blk[0];
@@ -649,6 +659,13 @@ void prefill_wide_mfma_kernel(
   }
 }
 
+// Grid of the XCD-aware order above (blocks past the last query block exit).
+int wide_blocks(int num_qblocks, int num_kv) {
+  const int lanes = kXcds % num_kv == 0 ? kXcds / num_kv : kXcds;
+  const int per_lane = kXcds % num_kv == 0 ? kWSub : kWSub * num_kv;
+  return (num_qblocks + lanes - 1) / lanes * per_lane * kXcds;
+}
+
 }  // namespace
 
 hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const void* q,
@@ -656,7 +673,7 @@ hipError_t launch_prefill_wide_mfma(const int32_t* image, int num_qblocks, const
                                     int num_kv, int64_t kv_stride, PagedGeom geom,
                                     hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  const int blocks = (num_qblocks + kXcds - 1) / kXcds * kXcds * kWSub * num_kv;
+  const int blocks = wide_blocks(num_qblocks, num_kv);
   hipLaunchKernelGGL(prefill_wide_mfma_kernel<false>, dim3(blocks), dim3(kPThreads), 0,
                      stream, image, q, nullptr, nullptr, k, nullptr, v, nullptr,
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
@@ -671,7 +688,7 @@ hipError_t launch_prefill_wide_mfma_bq(const int32_t* image, int num_qblocks, co
                                        int num_kv, int64_t kv_stride, PagedGeom geom,
                                        hipStream_t stream) {
   if (num_qblocks <= 0) return hipSuccess;
-  const int blocks = (num_qblocks + kXcds - 1) / kXcds * kXcds * kWSub * num_kv;
+  const int blocks = wide_blocks(num_qblocks, num_kv);
   hipLaunchKernelGGL(prefill_wide_mfma_kernel<true>, dim3(blocks), dim3(kPThreads), 0,
                      stream, image, q_i8, qi_bias, f_q, k, k_scale, v, v_scale,
                      static_cast<uint16_t*>(output), num_q, num_kv, kv_stride, geom.shift,
