@@ -183,6 +183,15 @@ def test_bq_full_layer_prefill_page_sizes(page_len):
     assert_bar(r, f"full layer page_len {page_len}")
 
 
+@pytest.mark.parametrize("nkv", [1, 3])
+def test_bq_full_layer_prefill_kv_head_counts(nkv):
+    """8 and 24 q heads at head_dim 512 / GQA 8: both of the kernel's block
+    placements over the XCDs (the kv head count divides 8, or not)."""
+    announce(f"bq mfma full-layer prefill num_kv={nkv}")
+    r = _run_full([0, 300, 1500, 70], [70, 129, 64, 9], 64, 41 + nkv, shape=(8 * nkv, nkv, WD))
+    assert_bar(r, f"full layer num_kv {nkv}")
+
+
 def test_bq_full_attention_prefill_hd256():
     """Full attention at 16 q / 8 kv x 256 on the int8 MFMA route: chunks from
     position 0, short and long prefixes, partial query blocks, a one-token

@@ -3,9 +3,11 @@
 FlashPrefillFullKernel + PrefillMergeKernel, kernels/
 flash_attention_prefill.mojo:117-248): the chunk's tokens against the
 oracle's token-partitioned route, within 1e-2 (one bf16 spacing where
-|x| >= 2).  Each pair of waves splits the score dims and exchanges the
-halves, so partial blocks, pairs without live rows and the causal diagonal
-all cross that exchange."""
+|x| >= 2).  A wave owns 4 tokens x 8 q heads over all 512 dims and a block
+16 tokens, so the cases cover partial blocks, waves without live rows, the
+causal diagonal, page-table windows that move, and both of the kernel's
+block placements (kv head counts that divide the 8 XCDs and one that does
+not)."""
 import numpy as np
 import pytest
 
@@ -31,22 +33,23 @@ def _table(runs, rows) -> KVRunTable:
     return t
 
 
-def _plan(case, n, page_len):
+def _plan(case, n, page_len, kvs=KVS):
     return AttentionPlan(_table(case.runs, case.base_rows), n, kind=FULL, window=0,
                          cache_size=page_len, page_len=page_len, cache_rows=case.cache_rows,
-                         cap=16, kv_row_bytes=KVS * 2)
+                         cap=16, kv_row_bytes=kvs * 2)
 
 
-def _prefill(case, n, q, k, v, page_len=64):
-    plan = _plan(case, n, page_len)
+def _prefill(case, n, q, k, v, page_len=64, nq=NQ, nkv=NKV):
+    kvs = nkv * D
+    plan = _plan(case, n, page_len, kvs)
     assert plan.summary.mode == 2 and int(plan.info[14]) > 0, "no query blocks"
-    out = empty_dev(n * NQ * D, np.uint16)
-    partials, ps = A.partials_buffer(plan, NQ, D)
-    A.attention_bf16(plan, to_dev(q), to_dev(k), to_dev(v), out, partials, ps, num_q=NQ,
-                     num_kv=NKV, head_dim=D, kv_stride=KVS)
+    out = empty_dev(n * nq * D, np.uint16)
+    partials, ps = A.partials_buffer(plan, nq, D)
+    A.attention_bf16(plan, to_dev(q), to_dev(k), to_dev(v), out, partials, ps, num_q=nq,
+                     num_kv=nkv, head_dim=D, kv_stride=kvs)
     got = from_dev(out, np.uint16)
-    ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=NQ, num_kv=NKV,
-                           head_dim=D, kv_stride=KVS, window=0, cache_size=page_len,
+    ref = oracle.attention(FULL, case.runs, case.base_rows, q, k, v, num_q=nq, num_kv=nkv,
+                           head_dim=D, kv_stride=kvs, window=0, cache_size=page_len,
                            page_len=page_len, seq_len=n, cap=16, threads=16)
     return compare_bf16(got, ref)
 
@@ -77,6 +80,21 @@ def test_wide_prefill_diffuse_scores():
     r = _prefill(case, n, q, seeded_bf16(case.cache_rows * KVS, 9),
                  seeded_bf16(case.cache_rows * KVS, 10))
     assert_bar(r, "wide prefill diffuse")
+
+
+@pytest.mark.parametrize("nkv", [1, 3])
+def test_wide_prefill_kv_head_counts(nkv):
+    """8 and 24 q heads (1 and 3 kv heads at GQA 8): one kv head for every
+    XCD, and a count that does not divide the 8 XCDs (the kernel then
+    spreads each query block's kv heads over one XCD)."""
+    announce(f"wide mfma prefill num_kv={nkv}")
+    nq = 8 * nkv
+    prefix, new = [0, 300, 1500, 70], [70, 129, 64, 9]
+    case = make_prefill_case(21 + nkv, prefix, new)
+    n = sum(new)
+    r = _prefill(case, n, seeded_bf16(n * nq * D, 22), seeded_bf16(case.cache_rows * nkv * D, 23),
+                 seeded_bf16(case.cache_rows * nkv * D, 24), nq=nq, nkv=nkv)
+    assert_bar(r, f"wide prefill num_kv {nkv}")
 
 
 @pytest.mark.parametrize("page_len", [8, 1024])
