@@ -22,9 +22,10 @@
 // costliest LDS operation on gfx950).
 // The reference's per-tile steps are kept in tile order: a row skips tiles
 // past its position (the reference never visits them), pads of its last
-// tile score -1e30 (their fexp(-87) enters l, not PV), and m, corr, w use
-// the biased exp; l is updated tile by tile.  The accumulator rescales of
-// a pair of tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 equals the
+// tile score -1e30 (the reference adds their fexp(-87) ~ 1.6e-38 to l;
+// here they weigh 0, the same l in f32), and m, corr, w use the biased
+// exp; l is updated tile by tile.  The accumulator rescales of a pair of
+// tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 equals the
 // reference's nested (acc*c0 + w0 V0)*c1 + w1 V1 up to f32 rounding, and
 // the product of the rescales is carried as a per-row scale S (acc =
 // acc_stored * S) that divides the weights instead of multiplying the 128
@@ -536,6 +537,7 @@ void prefill_full_mfma_kernel(
       // (the asm keeps the copy from being hoisted to the loop).
 #pragma unroll
       for (int b = 0; b < kDimBlocks; ++b) {
+        asm volatile("" : "+a"(acc[b]));  // no copy out of AGPRs ahead of the branch
         f32x16_t t = acc[b];
         asm volatile("" : "+v"(t));
         acc[b] = t * S_new;

@@ -76,10 +76,21 @@ __device__ __forceinline__ float mantissa_one(int32_t i) {
   return __uint_as_float(r);
 }
 // The maximum of 8 values as three v_max3_f32 and one v_max_f32 (the
-// maximum of finite values is the same in any order).
+// maximum of finite values is the same in any order).  Written as
+// instructions: fmaxf on values the compiler cannot prove canonical (MFMA
+// results copied out of AGPRs) gets a v_max_f32 x, x canonicalisation per
+// input, 8 extra VALU instructions per tile.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 __device__ __forceinline__ float max8(const float (&v)[8]) {
-  return fmaxf(fmaxf(fmaxf(v[0], v[1]), v[2]),
-               fmaxf(fmaxf(fmaxf(v[3], v[4]), v[5]), fmaxf(v[6], v[7])));
+  float r;
+  asm("v_max_f32 %0, %1, %2"
+      : "=v"(r)
+      : "v"(max3_raw(v[0], v[1], v[2])), "v"(max3_raw(max3_raw(v[3], v[4], v[5]), v[6], v[7])));
+  return r;
 }
 
 __device__ __forceinline__ float fexp_fused_t(float t) {
@@ -92,13 +103,31 @@ __device__ __forceinline__ float fexp_fused_t(float t) {
 __device__ __forceinline__ float fexp_fused(float x) {
   return fexp_fused_t(__builtin_fmaf(kExpA, fmaxf(x, -87.0f), kExpBias));
 }
+// The same for a score's weight, without the clamp at x = -87: the
+// conversion to unsigned (v_cvt_u32_f32) takes t < 0, i.e. x below about
+// -87.5, to 0 and so to a weight of 0 instead of fexp(-87) ~ 1.6e-38, and t
+// between 0 and the clamp's t gives weights below 1.2e-38.  A row's running
+// l holds its largest weight (fexp(0) = 0.99963 when it entered, then
+// rescaled by fexp(0) per tile without a new maximum: above 0.2 over 4,096
+// tiles), so weights this small change neither l nor any weighted sum in
+// f32: the results are those of the clamped form, one VALU instruction
+// less per score.
+__device__ __forceinline__ float fexp_fused_u(float t) {
+  uint32_t i;
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(i) : "v"(t));
+  const float F = mantissa_one(static_cast<int32_t>(i));
+  float p = __builtin_fmaf(F, static_cast<float>(kExpQc), static_cast<float>(kExpQb - 2 * kExpQc));
+  p = __builtin_fmaf(F, p, static_cast<float>(kExpQa - kExpQb + kExpQc));
+  return __uint_as_float(i) * p;
+}
 
 // One tile's online-softmax step for this lane's row (process_kv_tile's
 // m / corr / w / l updates, attention_ops.mojo:165-180).  sv[0..7] are the
 // lane's 8 keys of the tile, key 8*(i/4) + 4*half + i%4 for value i.
 // Masked: the tile reaches past some row's last key (or the row is empty);
 // a row with no key in the tile is left untouched (corr 1, weights 0), pads
-// score -1e30 and enter l only.  The in-lane sum of the 8 weights comes
+// score -1e30 (the reference's fexp(-87) of a pad enters l; here its weight
+// is 0, which leaves l as it is, see fexp_fused_u).  The in-lane sum of the 8 weights comes
 // first, then lane ^32's (the same 16 weights as the reference's halving
 // tree, added in another order).  Maxima use v_max_f32 (the scores are
 // finite for finite inputs).  big: the tile's weight sum exceeds kLoShare of
@@ -117,12 +146,12 @@ __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, in
   mx = max_xor32(mx);
   const float m_new = fmaxf(mx, m);
   const float c = fexp_fused(m - m_new);
-  // a*(s - m_new) + bias as one fma per key, clamped at s - m_new = -87.
+  // a*(s - m_new) + bias as one fma per key (weights below fexp(-87) go to
+  // 0 or below it, as fexp_fused_u states).
   const float t0 = __builtin_fmaf(-kExpA, m_new, kExpBias);
-  const float t_min = __builtin_fmaf(kExpA, -87.0f, kExpBias);
   float e[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) e[i] = fexp_fused_t(fmaxf(__builtin_fmaf(kExpA, sc[i], t0), t_min));
+  for (int i = 0; i < 8; ++i) e[i] = fexp_fused_u(__builtin_fmaf(kExpA, sc[i], t0));
   float ts = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
   ts = sum_xor32(ts);
   if (kMasked) {

@@ -24,8 +24,9 @@
 // last tile J_K (K = (p - lo) / 16) completes at aligned step
 // lo / 16 + K + 1, which a final step past the last staged tile covers.
 // Pads (keys past p in a row's last tile: with lo = 0, or when the window is
-// not a multiple of 16, in its high or its low part) score -1e30: their
-// fexp(-87) enters l, a zero weight P.V.
+// not a multiple of 16, in its high or its low part) score -1e30 and get
+// weight 0 (the reference's fexp(-87) ~ 1.6e-38 of a pad enters l, which
+// cannot change l in f32; see fexp_fused_u).
 //
 // As in the full kernel the accumulator is kept as acc_stored with acc =
 // acc_stored * S; a weight enters the MFMA divided by S right after its own
@@ -477,10 +478,9 @@ void prefill_sliding_mfma_kernel(
     const float m_new = fmaxf(mx, m);
     const float c = fexp_fused(m - m_new);
     const float te = __builtin_fmaf(-kExpA, m_new, kExpBias);
-    const float t_min = __builtin_fmaf(kExpA, -87.0f, kExpBias);
     float e[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = fexp_fused_t(fmaxf(__builtin_fmaf(kExpA, sel[i], te), t_min));
+    for (int i = 0; i < 8; ++i) e[i] = fexp_fused_u(__builtin_fmaf(kExpA, sel[i], te));
     float ts = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
     ts = sum_xor32(ts);
     const float corr = fin ? c : 1.0f;
