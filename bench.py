@@ -1547,6 +1547,49 @@ class GatherBench:
                           f"{'all' if n == self.ROWS else 'the first'} {n} of the {self.ROWS} "
                           f"rows, {threads} worker shares on {threads} threads")
 
+class PhaseEvents:
+    """HIP timing events created with hipEventDisableSystemFence, recorded on
+    the launch stream.  A default event (torch.cuda.Event) ends with a
+    system-scope fence whose cache writeback and invalidation slow the kernel
+    that follows it (config 11's sliding prefill: about 800 instead of 700 us
+    after an event, 700 us when launched right after the append, as rocprofv3
+    shows for both); these events time the phases as they run back to back.
+    The runtime is the HIP library torch has loaded (one per process)."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, stream):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.stream = ctypes.c_void_p(int(stream.cuda_stream))
+        self.events = []
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
+
+    def record(self):
+        ev = self.ct.c_void_p()
+        self._check(self.hip.hipEventCreateWithFlags(self.ct.byref(ev),
+                                                     self.ct.c_uint(self.DISABLE_SYSTEM_FENCE)),
+                    "hipEventCreateWithFlags")
+        self._check(self.hip.hipEventRecord(ev, self.stream), "hipEventRecord")
+        self.events.append(ev)
+        return ev
+
+    def elapsed_us(self, a, b) -> float:
+        ms = self.ct.c_float()
+        self._check(self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value * 1e3
+
+    def close(self):
+        for ev in self.events:
+            self.hip.hipEventDestroy(ev)
+        self.events = []
+
+
 def measure(w, steps: int, warmup: int, graph: bool):
     """Returns the wall time of K eager steps, of K steps replayed from a HIP
     graph (None unless graph), and per-phase HIP-event times."""
@@ -1595,19 +1638,23 @@ def measure(w, steps: int, warmup: int, graph: bool):
         torch.cuda.synchronize()
         wall_graph = time.perf_counter() - t0
         del g
-    # Timed region 3: K steps phase by phase with HIP events between them.
+    # Timed region 3: K steps phase by phase with HIP events between them
+    # (events without the system-scope fence; see PhaseEvents).
     n = len(w.phases)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
+    pe = PhaseEvents(stream)
     torch.cuda.synchronize()
+    evs = []
     for i in range(steps):
-        evs[i][0].record(stream)
-        for j, ph in enumerate(w.phases):
+        row = [pe.record()]
+        for ph in w.phases:
             w.launch(ph)
-            evs[i][j + 1].record(stream)
+            row.append(pe.record())
+        evs.append(row)
     torch.cuda.synchronize()
-    per = {ph: statistics.mean(e[j].elapsed_time(e[j + 1]) * 1e3 for e in evs)
+    per = {ph: statistics.mean(pe.elapsed_us(e[j], e[j + 1]) for e in evs)
            for j, ph in enumerate(w.phases)}
-    per["step"] = statistics.mean(e[0].elapsed_time(e[n]) * 1e3 for e in evs)
+    per["step"] = statistics.mean(pe.elapsed_us(e[0], e[n]) for e in evs)
+    pe.close()
     return wall, wall_graph, per
 
 

@@ -326,8 +326,12 @@ void prefill_sliding_mfma_kernel(
   const int vj = lane & 15;
   const int v_row = (4 * half + (vj >> 2)) * kRowBytes +
                     32 * (((lane >> 4) & 1) ^ ((vj >> 2) & 1)) + 8 * (vj & 3);
-  const int v_even = v_row + 64 * (vj >> 3);
-  const int v_odd = v_row - 64 * (vj >> 3);
+  int v_even = v_row + 64 * (vj >> 3);
+  int v_odd1 = v_row - 64 * (vj >> 3) + 64;  // odd block b at v_odd1 + 64 * (b - 1)
+  // Opaque to the compiler: from the known low bits of these offsets it
+  // would combine them with the buffer address by OR, one VALU instruction
+  // per read, instead of a base register and immediate offsets.
+  asm("" : "+v"(v_even), "+v"(v_odd1));
 
   // bq K operand reads: chunk 2d + half of key row (row & 31) of 256 bytes,
   // stored at (2d + half) ^ (row & 15): byte address kq_lane ^ 32d.
@@ -429,7 +433,7 @@ void prefill_sliding_mfma_kernel(
     bf16x8_t av[kDimBlocks];
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) {
-      const uint8_t* vb = vt + ((b & 1) ? v_odd : v_even) + 64 * b;
+      const uint8_t* vb = (b & 1) ? vt + v_odd1 + 64 * (b - 1) : vt + v_even + 64 * b;
       const s16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)vb);
       const s16x4_t v1 =
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + 8 * kRowBytes));
