@@ -465,16 +465,19 @@ void prefill_sliding_mfma_kernel(
   // Step of aligned tile t with scores st: completes the row's reference
   // tile (high part of t - 1, low part of t) when t_first < t <= t_end, then
   // P.V of tile t - 1 (vprev, rows prev_row ..) unless do_pv is false.
-  auto step = [&](int t, const float (&st)[8], const uint8_t* vprev, int prev_row,
-                  bool do_pv, int prev_buf) {
-    const bool fin = t > t_first && t <= t_end;
+  // kInner: every row of the wave completes a reference tile at t and none
+  // of its keys lies past the row's position (no fin or pad tests).
+  auto step_impl = [&](auto inner_c, int t, const float (&st)[8], const uint8_t* vprev,
+                       int prev_row, bool do_pv, int prev_buf) {
+    constexpr bool kInner = decltype(inner_c)::value;
+    const bool fin = kInner || (t > t_first && t <= t_end);
     float sel[8];
     bool low[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kk = key_of(i);
       low[i] = kk < r;
-      const bool pad = (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
+      const bool pad = !kInner && (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
       sel[i] = (fin && !pad) ? (low[i] ? st[i] : s_prev[i]) : kNegBig;
     }
     float mx = max8(sel);
@@ -513,7 +516,7 @@ void prefill_sliding_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kk = key_of(i);
-      const bool pad = (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
+      const bool pad = !kInner && (low[i] ? 16 * t : 16 * (t - 1)) + kk > p;
       const float w = (fin && !pad) ? e[i] * inv_s : 0.0f;
       pw[i] = low[i] ? pend[i] : w;
       pend[i] = low[i] ? w : 0.0f;
@@ -523,8 +526,25 @@ void prefill_sliding_mfma_kernel(
     pend_big = big && r != 0;
     if (do_pv) pv(vprev, prev_row, pw, need_lo, prev_buf);
   };
-
-  for (int it = 0; it < n_iters; ++it) {
+  // The steps at which every row of the wave is inside: t_first < t <=
+  // t_end, and the row's last key at step t (16t + r - 1 for its low part,
+  // 16t - 1 for its high part) at most p.  Wave-uniform bounds [in_lo,
+  // in_hi] (a wave with rows past the block's last token has none).
+  int in_lo = t_first + 1;
+  int in_hi = min(t_end, r > 0 ? (p - r + 1) >> 4 : (p + 1) >> 4);
+  if (!row_live) in_hi = -1;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    in_lo = max(in_lo, __shfl_xor(in_lo, o));
+    in_hi = min(in_hi, __shfl_xor(in_hi, o));
+  }
+  in_lo = __builtin_amdgcn_readfirstlane(in_lo);
+  in_hi = __builtin_amdgcn_readfirstlane(in_hi);
+  const std::true_type inner_yes{};
+  const std::false_type inner_no{};
+  // One iteration: the scores of its two 32-key blocks and its four steps,
+  // all of them kInner or none.
+  auto iteration = [&](auto inner_c, int it) {
     uint8_t* kl = (it & 1) ? kbuf1 : kbuf0;
     uint8_t* vl = (it & 1) ? vbuf1 : vbuf0;
     uint8_t* kn = (it & 1) ? kbuf0 : kbuf1;
@@ -537,7 +557,7 @@ void prefill_sliding_mfma_kernel(
     for (int i = 0; i < 8; ++i) st[i] = s0[i];
     // Tile tb - 1 lies in the other buffer (the previous iteration's last
     // tile); it is read before that buffer is restaged.
-    step(tb, st, vn, 48, it > 0, nb);
+    step_impl(inner_c, tb, st, vn, 48, it > 0, nb);
     __syncthreads();
     if (it + 1 < n_iters) {
       if (interior(it + 1))
@@ -547,14 +567,14 @@ void prefill_sliding_mfma_kernel(
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s0[8 + i];
-    step(tb + 1, st, vl, 0, true, cb);
+    step_impl(inner_c, tb + 1, st, vl, 0, true, cb);
     const f32x16_t s1 = qk(kl, 1, cb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s1[i];
-    step(tb + 2, st, vl, 16, true, cb);
+    step_impl(inner_c, tb + 2, st, vl, 16, true, cb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = s1[8 + i];
-    step(tb + 3, st, vl, 32, true, cb);
+    step_impl(inner_c, tb + 3, st, vl, 32, true, cb);
 #pragma unroll
     for (int b = 0; b < kDimBlocks; ++b) asm volatile("" : "+a"(acc[b]));
 #pragma unroll
@@ -562,7 +582,16 @@ void prefill_sliding_mfma_kernel(
     __builtin_amdgcn_s_waitcnt(0);
     if (it + 1 < n_iters) land_v(it + 1, vn);
     __syncthreads();
-  }
+  };
+  // Iterations whose four steps tile0 + 4it .. +3 all lie in [in_lo, in_hi]
+  // run the kInner form, in a loop of their own (one form per loop keeps
+  // the register allocation of each loop to one iteration body).
+  const int it_in0 = min(n_iters, max(0, (in_lo - tile0 + 3) >> 2));
+  const int it_in1 = max(it_in0, min(n_iters, (in_hi - 3 - tile0 >= 0) ? ((in_hi - 3 - tile0) >> 2) + 1 : 0));
+  int it = 0;
+  for (; it < it_in0; ++it) iteration(inner_no, it);
+  for (; it < it_in1; ++it) iteration(inner_yes, it);
+  for (; it < n_iters; ++it) iteration(inner_no, it);
   // The step past the last staged tile: completes the last reference tile of
   // rows with r = 0 and runs the last tile's P.V.
   if (n_iters > 0) {
@@ -570,7 +599,7 @@ void prefill_sliding_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = kNegBig;
     const int lb = (n_iters - 1) & 1;
-    step(tile0 + 4 * n_iters, st, lb ? vbuf1 : vbuf0, 48, true, lb);
+    step_impl(inner_no, tile0 + 4 * n_iters, st, lb ? vbuf1 : vbuf0, 48, true, lb);
   }
 
   // Finalisation of the sliding prefill: acc * (1/l).
