@@ -397,7 +397,7 @@ void prefill_full_mfma_kernel(
     if constexpr (kBq) {
       i32x16_t si;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) si[v] = 0;
+      for (int v = 0; v < 16; ++v) si[v] = qs128;  // the raw dot's 128 * sum q, exact in int32
       const uint8_t* kh = kl + 32 * h * kBqRowBytes;
       uint4 kf[kQFrags];
 #pragma unroll
@@ -415,7 +415,7 @@ void prefill_full_mfma_kernel(
         const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float sc = static_cast<float>(si[4 * j + i] + qs128) - qb_row;
+          float sc = static_cast<float>(si[4 * j + i]) - qb_row;
           sc = sc * fq_row;
           sc = sc * ks[i];
           sblk[4 * j + i] = sc * kInv127Sq;

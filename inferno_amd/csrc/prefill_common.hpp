@@ -145,7 +145,10 @@ __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, in
   float mx = max8(sc);
   mx = max_xor32(mx);
   const float m_new = fmaxf(mx, m);
-  const float c = fexp_fused(m - m_new);
+  // corr without the clamp as well: below -87.5 it is 0 instead of about
+  // 1e-39, which scales an l of at least 0.2 (or 0) and acc alike to
+  // nothing next to the tile's own weights.
+  const float c = fexp_fused_u(__builtin_fmaf(kExpA, m - m_new, kExpBias));
   // a*(s - m_new) + bias as one fma per key (weights below fexp(-87) go to
   // 0 or below it, as fexp_fused_u states).
   const float t0 = __builtin_fmaf(-kExpA, m_new, kExpBias);

@@ -345,7 +345,7 @@ void prefill_sliding_mfma_kernel(
     if constexpr (kBq) {
       i32x16_t si;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) si[v] = 0;
+      for (int v = 0; v < 16; ++v) si[v] = qs128;  // the raw dot's 128 * sum q, exact in int32
       const uint8_t* kh = kl + 32 * h * kBqRowBytes;
       uint4 kf[kQFrags];
 #pragma unroll
@@ -365,7 +365,7 @@ void prefill_sliding_mfma_kernel(
         const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float sc = static_cast<float>(si[4 * j + i] + qs128) - qb_row;
+          float sc = static_cast<float>(si[4 * j + i]) - qb_row;
           sc = sc * fq_row;
           sc = sc * ks[i];
           sblk[4 * j + i] = sc * kInv127Sq;
@@ -483,7 +483,7 @@ void prefill_sliding_mfma_kernel(
     float mx = max8(sel);
     mx = max_xor32(mx);
     const float m_new = fmaxf(mx, m);
-    const float c = fexp_fused(m - m_new);
+    const float c = fexp_fused_u(__builtin_fmaf(kExpA, m - m_new, kExpBias));
     const float te = __builtin_fmaf(-kExpA, m_new, kExpBias);
     float e[8];
 #pragma unroll
