@@ -22,7 +22,7 @@
 // costliest LDS operation on gfx950).
 // The reference's per-tile steps are kept in tile order: a row skips tiles
 // past its position (the reference never visits them), pads of its last
-// tile score -1e30 (the reference adds their fexp(-87) ~ 1.6e-38 to l;
+// tile score -1e30 (the reference adds their fexp(-87) = 1.4e-38 to l;
 // here they weigh 0, the same l in f32), and m, corr, w use the biased
 // exp; l is updated tile by tile.  The accumulator rescales of a pair of
 // tiles are folded: acc*c0*c1 + (w0*c1) V0 + w1 V1 equals the
@@ -31,7 +31,7 @@
 // acc_stored * S) that divides the weights instead of multiplying the 128
 // accumulators.  P' enters the bf16 MFMA as hi + lo bf16 parts (~16
 // significant bits per weight); QK^T products are exact in f32.  The biased
-// exp is evaluated with fused multiply-adds (fexp_fused): its value differs
+// exp is evaluated with fused multiply-adds (fexp_fused_u): its value differs
 // from the reference's separately rounded steps by about 2e-5 relative,
 // far inside the bf16 output tolerance, and it saves a third of the
 // softmax's VALU work, which bounds this kernel together with the MFMAs.

@@ -47,9 +47,8 @@ __device__ __forceinline__ float max_xor32(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// The reference's biased exp (the steps of fexp) with fused multiply-adds.
-// The argument arrives pre-scaled: t = a_magic * x + bias_f, clamped below
-// at x = -87 by the caller.
+// The reference's biased exp (the steps of fexp) with fused multiply-adds
+// (fexp_fused_u below).
 constexpr float kExpA = 12102203.16156148f;
 constexpr float kExpBias = 1059208216.0f;
 // The quadratic a + f*(b + c*f) in the mantissa fraction f = F - 1 is
@@ -93,25 +92,16 @@ __device__ __forceinline__ float max8(const float (&v)[8]) {
   return r;
 }
 
-__device__ __forceinline__ float fexp_fused_t(float t) {
-  const int32_t i = static_cast<int32_t>(t);
-  const float F = mantissa_one(i);
-  float p = __builtin_fmaf(F, static_cast<float>(kExpQc), static_cast<float>(kExpQb - 2 * kExpQc));
-  p = __builtin_fmaf(F, p, static_cast<float>(kExpQa - kExpQb + kExpQc));
-  return __int_as_float(i) * p;
-}
-__device__ __forceinline__ float fexp_fused(float x) {
-  return fexp_fused_t(__builtin_fmaf(kExpA, fmaxf(x, -87.0f), kExpBias));
-}
-// The same for a score's weight, without the clamp at x = -87: the
-// conversion to unsigned (v_cvt_u32_f32) takes t < 0, i.e. x below about
-// -87.5, to 0 and so to a weight of 0 instead of fexp(-87) ~ 1.6e-38, and t
-// between 0 and the clamp's t gives weights below 1.2e-38.  A row's running
-// l holds its largest weight (fexp(0) = 0.99963 when it entered, then
-// rescaled by fexp(0) per tile without a new maximum: above 0.2 over 4,096
-// tiles), so weights this small change neither l nor any weighted sum in
-// f32: the results are those of the clamped form, one VALU instruction
-// less per score.
+// The biased exp of a pre-scaled argument t = a_magic * x + bias_f, without
+// the reference's clamp at x = -87: the conversion to unsigned
+// (v_cvt_u32_f32) takes t < 0, i.e. x below about -87.5, to 0 and so to a
+// weight of 0 instead of fexp(-87) = 1.4e-38, and t between 0 and the
+// clamp's t gives weights below 1.4e-38.  A row's running l holds its
+// largest weight (fexp(0) = 0.99963 when it entered, then rescaled by
+// fexp(0) per tile without a new maximum: above 0.2 over 4,096 tiles), so
+// weights this small change neither l nor any weighted sum in f32: the
+// results are those of the clamped form, one VALU instruction less per
+// score.
 __device__ __forceinline__ float fexp_fused_u(float t) {
   uint32_t i;
   asm("v_cvt_u32_f32 %0, %1" : "=v"(i) : "v"(t));
@@ -145,9 +135,9 @@ __device__ __forceinline__ void softmax_tile(const float (&sv)[8], int valid, in
   float mx = max8(sc);
   mx = max_xor32(mx);
   const float m_new = fmaxf(mx, m);
-  // corr without the clamp as well: below -87.5 it is 0 instead of about
-  // 1e-39, which scales an l of at least 0.2 (or 0) and acc alike to
-  // nothing next to the tile's own weights.
+  // corr without the clamp as well: below -87.5 it is 0 instead of
+  // fexp(-87) = 1.4e-38, which scales an l of at least 0.2 (or 0) and acc
+  // alike to nothing next to the tile's own weights.
   const float c = fexp_fused_u(__builtin_fmaf(kExpA, m - m_new, kExpBias));
   // a*(s - m_new) + bias as one fma per key (weights below fexp(-87) go to
   // 0 or below it, as fexp_fused_u states).

@@ -25,7 +25,7 @@
 // lo / 16 + K + 1, which a final step past the last staged tile covers.
 // Pads (keys past p in a row's last tile: with lo = 0, or when the window is
 // not a multiple of 16, in its high or its low part) score -1e30 and get
-// weight 0 (the reference's fexp(-87) ~ 1.6e-38 of a pad enters l, which
+// weight 0 (the reference's fexp(-87) = 1.4e-38 of a pad enters l, which
 // cannot change l in f32; see fexp_fused_u).
 //
 // As in the full kernel the accumulator is kept as acc_stored with acc =
