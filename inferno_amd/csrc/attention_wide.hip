@@ -73,7 +73,7 @@ struct WideTile {
   using VT = typename std::conditional<kBq, uint2, uint4>::type;
   uint4 k[kSteps];
   VT v[kTile];
-  float ks[4], vs[4];  // bq: scales of positions 4*(l/16) + j
+  float ks, vs;  // bq: the scales of position l % 16 (the lane's K row)
 };
 
 __device__ __forceinline__ void unpack8(const uint4& w, float* f) {
@@ -112,6 +112,11 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   // every lane as two broadcast LDS reads (LDS instructions, where 8
   // v_readlanes per position were VALU work in a VALU-bound loop).
   __shared__ __align__(16) float wl[kTile * kWG];
+  // bq: the tile's K and V scales, lane l's at [l] (position l % 16, four
+  // copies), so a lane reads positions 4*(l/16) .. +3 as one float4: one
+  // scale load per lane and tile instead of four, each with its own row
+  // lookup.
+  __shared__ __align__(16) float scl[2][kBq ? 64 : 1];
 
   const int lane = threadIdx.x;
   const int g = blockIdx.x;
@@ -217,10 +222,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     const uint8_t* kr = kh + slot_of(r, r16) * row_bytes;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) d.k[s] = wide_load16(kr + 64 * s);
-    if constexpr (kBq) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) d.ks[j] = k_scale[slot_of(r, 4 * qd + j) * num_kv + g];
-    }
+    if constexpr (kBq) d.ks = k_scale[slot_of(r, r16) * num_kv + g];
   };
   auto load_v = [&](Tile& d, const TileRows& r) {
 #pragma unroll
@@ -232,10 +234,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
         d.v[t] = wide_load16(vr);
       }
     }
-    if constexpr (kBq) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) d.vs[j] = v_scale[slot_of(r, 4 * qd + j) * num_kv + g];
-    }
+    if constexpr (kBq) d.vs = v_scale[slot_of(r, r16) * num_kv + g];
   };
 
   Tile d;
@@ -263,11 +262,16 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
                                                     __builtin_bit_cast(wi32x4_t, qf), si,
                                                     0, 0, 0);
       }
+      // The K scales of the lane's positions 4*qd + j from the lanes that
+      // loaded them (the wave's own LDS: its write lands before its read).
+      scl[0][lane] = d.ks;
+      const float4 ks4 = *reinterpret_cast<const float4*>(&scl[0][4 * qd]);
+      const float ksj[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float sc = static_cast<float>(si[j] + qsum128) - qbias;
         sc = sc * fq;
-        sc = sc * d.ks[j];
+        sc = sc * ksj[j];
         sc = sc * inv127sq;
         sj[j] = 4 * qd + j < tile_len ? sc : kNegBig;
       }
@@ -306,9 +310,12 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     m = m_new;
     if constexpr (kBq) {
       // bq_process_kv_tile's value weights: (w * v_scale) / 127.
+      scl[1][lane] = d.vs;
+      const float4 vs4 = *reinterpret_cast<const float4*>(&scl[1][4 * qd]);
+      const float vsj[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float a = w[j] * d.vs[j];
+        const float a = w[j] * vsj[j];
         w[j] = a * inv127;
       }
     }
