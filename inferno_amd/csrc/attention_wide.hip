@@ -66,6 +66,8 @@ __device__ __forceinline__ uint2 wide_load8(const uint8_t* p) {
   return make_uint2(v.x, v.y);
 }
 
+typedef __attribute__((address_space(1))) const uint8_t gu8_t;  // global memory
+
 template <bool kBq>
 struct WideTile {
   static constexpr int kRow = kBq ? kWD : 2 * kWD;  // bytes of one head's row
@@ -117,6 +119,9 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   // scale load per lane and tile instead of four, each with its own row
   // lookup.
   __shared__ __align__(16) float scl[2][kBq ? 64 : 1];
+  // The tile's corrections of the 8 heads (lane h writes head h's), read
+  // back by every lane as two broadcast LDS reads instead of 8 v_readlanes.
+  __shared__ __align__(16) float cl[kWG];
 
   const int lane = threadIdx.x;
   const int g = blockIdx.x;
@@ -178,8 +183,22 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   const float inv127 = 1.0f / 127.0f;
   const float inv127sq = inv127 * inv127;
 
+  // Row addresses: slots are page-table rows (int32) and row_bytes is
+  // below 2^31 (checked at launch), so slot * row_bytes is one 32 x 32 ->
+  // 64-bit multiply (v_mad_u64_u32) instead of a 64-bit product.  A V row's
+  // address is wave-uniform: its base stays in SGPRs and the load adds the
+  // lane's 32-bit offset (global_load's saddr form, no VALU address work).
+  const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
+  auto row_off = [&](int64_t slot) -> uint64_t {
+    return static_cast<uint64_t>(static_cast<uint32_t>(slot)) * rb32;
+  };
+  auto scale_idx = [&](int64_t slot) -> uint64_t {
+    return static_cast<uint64_t>(static_cast<uint32_t>(slot)) * static_cast<uint32_t>(num_kv) +
+           static_cast<uint32_t>(g);
+  };
   const uint8_t* kh = kc + static_cast<int64_t>(g) * kRow + 16 * qd;
-  const uint8_t* vh = vc + static_cast<int64_t>(g) * kRow + kVB * lane;
+  const uint8_t* vg = vc + static_cast<int64_t>(g) * kRow;
+  const uint32_t v_lane = kVB * lane;
 
   float m = kNegBig;  // state of head hq (the same in the lanes of a column)
   float lsum = 0.0f;
@@ -219,22 +238,26 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     }
   };
   auto load_k = [&](Tile& d, const TileRows& r) {
-    const uint8_t* kr = kh + slot_of(r, r16) * row_bytes;
+    const uint8_t* kr = kh + row_off(slot_of(r, r16));
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) d.k[s] = wide_load16(kr + 64 * s);
-    if constexpr (kBq) d.ks = k_scale[slot_of(r, r16) * num_kv + g];
+    if constexpr (kBq) d.ks = k_scale[scale_idx(slot_of(r, r16))];
   };
+  // The V scale first: the softmax then waits for it alone, not for the
+  // tile's V rows, which only the P.V needs.
   auto load_v = [&](Tile& d, const TileRows& r) {
+    if constexpr (kBq) d.vs = v_scale[scale_idx(slot_of(r, r16))];
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      const uint8_t* vr = vh + slot_of(r, t) * row_bytes;
+      const gu8_t* vrow = (const gu8_t*)(vg + row_off(slot_of(r, t)));
+      asm("" : "+s"(vrow));
+      const uint8_t* vr = (const uint8_t*)(vrow + v_lane);
       if constexpr (kBq) {
         d.v[t] = wide_load8(vr);
       } else {
         d.v[t] = wide_load16(vr);
       }
     }
-    if constexpr (kBq) d.vs = v_scale[slot_of(r, r16) * num_kv + g];
   };
 
   Tile d;
@@ -333,11 +356,14 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     }
 
     // ---- scale_unrolled, then P.V in position order ----
+    if (lane < kWG) cl[lane] = corr;  // lane h: column h, head h
+    const float4 ca = *reinterpret_cast<const float4*>(&cl[0]);
+    const float4 cb = *reinterpret_cast<const float4*>(&cl[4]);
+    const float chs[kWG] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
 #pragma unroll
     for (int h = 0; h < kWG; ++h) {
-      const float ch = readlane_f32(corr, h);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] * ch;
+      for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] * chs[h];
     }
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
@@ -416,6 +442,7 @@ hipError_t launch_wide(const int32_t* image, int num_items, const void* q,
                        int64_t kv_stride, PagedGeom geom, hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   const int64_t row_bytes = kv_stride * (kBq ? 1 : 2);
+  if (row_bytes <= 0 || row_bytes > INT32_MAX) return hipErrorInvalidValue;  // 32-bit row math
   dim3 grid(num_kv, num_items);  // an item's kv heads side by side
   const auto* qp = static_cast<const uint8_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k);
