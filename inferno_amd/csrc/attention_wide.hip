@@ -267,11 +267,15 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
   // it is: the accumulators start at +0 and never become -0 by addition).
   // Otherwise positions past the tile are skipped.  kNext: the loads of
   // tile rn are issued into the tile's registers as soon as this tile is
-  // done with them (K after the score MFMAs, V after the P.V).
-  auto step = [&](auto flat_c, auto next_c, const TileRows& r, const TileRows& rn) {
+  // done with them (K after the score MFMAs, V after the P.V).  kFull: the
+  // tile holds kTile positions, so no score is masked and no position
+  // skipped (the same operations as the general form on such a tile).
+  auto step = [&](auto flat_c, auto next_c, auto full_c, const TileRows& r,
+                  const TileRows& rn) {
     constexpr bool kFlat = decltype(flat_c)::value;
     constexpr bool kNext = decltype(next_c)::value;
-    const int tile_len = r.len;
+    constexpr bool kFull = decltype(full_c)::value;
+    const int tile_len = kFull ? kTile : r.len;
 
     // ---- scores: lane holds positions 4*qd + j of head hq ----
     float sj[4];
@@ -296,7 +300,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
         sc = sc * fq;
         sc = sc * ksj[j];
         sc = sc * inv127sq;
-        sj[j] = 4 * qd + j < tile_len ? sc : kNegBig;
+        sj[j] = (kFull || 4 * qd + j < tile_len) ? sc : kNegBig;
       }
     } else {
       wf32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -308,7 +312,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
                                                      0, 0);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sj[j] = 4 * qd + j < tile_len ? sc[j] : kNegBig;
+      for (int j = 0; j < 4; ++j) sj[j] = (kFull || 4 * qd + j < tile_len) ? sc[j] : kNegBig;
     }
     if constexpr (kNext) {
       __builtin_amdgcn_sched_barrier(0);
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
       }
     }
 
-    if constexpr (kFlat) {
+    if constexpr (kFlat && !kFull) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) w[j] = 4 * qd + j < tile_len ? w[j] : 0.0f;
     }
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     }
 #pragma unroll
     for (int t = 0; t < kTile; ++t) {
-      if (kFlat || t < tile_len) {  // wave-uniform
+      if (kFlat || kFull || t < tile_len) {  // wave-uniform
         float vf[8];
         unpack8(d.v[t], vf);
         const float4 wa = *reinterpret_cast<const float4*>(&wl[t * kWG]);
@@ -403,7 +407,10 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
     __builtin_amdgcn_sched_barrier(0);  // K before V, as in the loop
     load_v(d, r);
     __builtin_amdgcn_sched_barrier(0);
-    for (int pos0 = start; pos0 < end; pos0 += kTile) {
+    // The item's full tiles run without masks, in a loop of their own; a
+    // last partial tile takes the general form.
+    int pos0 = start;
+    auto tile = [&](auto full_c) {
       const int nxt = pos0 + kTile;
       TileRows rn = r;
       if (nxt < end)
@@ -413,11 +420,15 @@ __global__ __launch_bounds__(64) void flash_partial_wide_kernel(
       // bf16 with flat P.V; int8 skips positions past the tile (its
       // outputs are compared bit for bit).
       if constexpr (kBq)
-        step(no, yes, r, rn);
+        step(no, yes, full_c, r, rn);
       else
-        step(yes, yes, r, rn);
+        step(yes, yes, full_c, r, rn);
       r = rn;
-    }
+      pos0 = nxt;
+    };
+    const int n_full = (end - start) / kTile;
+    for (int i = 0; i < n_full; ++i) tile(yes);
+    if (pos0 < end) tile(no);
   }
 
   float* part = partials + static_cast<int64_t>(stripe) * partial_stride;

@@ -77,7 +77,6 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 __device__ __forceinline__ float fexp(float x) {
   const float a_magic = 12102203.16156148f;
   const float bias_f = 1059208216.0f;
-  const float inv_two23 = 1.0f / 8388608.0f;
   const float qc_a = 1.6501418352127075f;
   const float qc_b = -0.37554836273193359f;
   const float qc_c = 0.38696467876434326f;
@@ -86,7 +85,12 @@ __device__ __forceinline__ float fexp(float x) {
   int32_t i = static_cast<int32_t>(t);
   uint32_t u = static_cast<uint32_t>(i);
   float k = __uint_as_float(u);
-  float f = static_cast<float>(u & 0x7FFFFFu) * inv_two23;
+  // f = (float)(u & 0x7FFFFF) / 2^23, formed as F - 1 with F = 1.f (the
+  // mantissa bits under a biased exponent of 0): both are m / 2^23 exactly
+  // (F - 1 is exact by Sterbenz' lemma, and m / 2^23 needs no rounding), so
+  // the bits are the reference's, in one and-or and one subtract instead of
+  // an and, an int-to-float conversion and a multiply.
+  float f = __uint_as_float((u & 0x7FFFFFu) | 0x3F800000u) - 1.0f;
   float p = f * qc_c;
   p = qc_b + p;
   p = f * p;
