@@ -554,9 +554,9 @@ void prefill_full_mfma_kernel(
     const float inv_s = __builtin_amdgcn_rcpf(S_new);
     const float fs[2] = {corr[1] * inv_s, inv_s};
     // P''^T of both tiles in bf16 (hi): k index 8*half + i holds the lane's
-    // value i.  A tile's lo parts (p - bf16(p), about 8 more bits) follow in
-    // a pass of their own when some row of the wave has the tile's big flag
-    // (more than kLoShare of its running l).
+    // value i.  A tile's lo parts (p - bf16(p), about 8 more bits) join the
+    // pass when some row of the wave has the tile's big flag (more than
+    // kLoShare of its running l).
     bf16x8_t phi[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -584,50 +584,37 @@ void prefill_full_mfma_kernel(
                                    __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     };
-    auto pass = [&](const bf16x8_t (&pp)[2]) {
-      auto mfma_group = [&](int u, int b0, const bf16x8_t (&av)[4]) {
+    // One pass over the pair's V^T fragments.  A tile's lo parts (kLo0 /
+    // kLo1) take the MFMAs right after its hi parts on the same fragments,
+    // so they cost MFMA issue only, no LDS reads of their own; per
+    // accumulator the order is hi 0, lo 0, hi 1, lo 1.
+    auto mfma_group = [&](const bf16x8_t& p, int b0, const bf16x8_t (&av)[4]) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[b0 + b] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], pp[u], acc[b0 + b], 0, 0, 0);
-      };
-      bf16x8_t ga[4], gb[4];
-      read_group(0, 0, ga);
-      read_group(0, 4, gb);
-      mfma_group(0, 0, ga);
-      read_group(1, 0, ga);
-      mfma_group(0, 4, gb);
-      read_group(1, 4, gb);
-      mfma_group(1, 0, ga);
-      mfma_group(1, 4, gb);
-      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      for (int b = 0; b < 4; ++b)
+        acc[b0 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b], p, acc[b0 + b], 0, 0, 0);
     };
-    pass(phi);
+    auto lo_part = [&](int u) {
+      bf16x8_t plo;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (__builtin_amdgcn_ballot_w64(big[u]) != 0) {  // wave-uniform
-        bf16x8_t plo;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
-        bf16x8_t ga[4], gb[4];
-        read_group(u, 0, ga);
-        read_group(u, 4, gb);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[b], plo, acc[b], 0, 0, 0);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[4 + b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gb[b], plo, acc[4 + b], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      }
-    }
+      for (int i = 0; i < 8; ++i)
+        plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
+      return plo;
+    };
+    const bool lo0 = __builtin_amdgcn_ballot_w64(big[0]) != 0;  // wave-uniform
+    const bool lo1 = __builtin_amdgcn_ballot_w64(big[1]) != 0;
+    bf16x8_t ga[4], gb[4];
+    read_group(0, 0, ga);
+    read_group(0, 4, gb);
+    mfma_group(phi[0], 0, ga);
+    if (lo0) mfma_group(lo_part(0), 0, ga);
+    read_group(1, 0, ga);
+    mfma_group(phi[0], 4, gb);
+    if (lo0) mfma_group(lo_part(0), 4, gb);
+    read_group(1, 4, gb);
+    mfma_group(phi[1], 0, ga);
+    if (lo1) mfma_group(lo_part(1), 0, ga);
+    mfma_group(phi[1], 4, gb);
+    if (lo1) mfma_group(lo_part(1), 4, gb);
   };
 
   // End of one iteration: the accumulators and the Q^T fragments stay in

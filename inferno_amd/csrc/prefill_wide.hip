@@ -534,28 +534,22 @@ void prefill_wide_mfma_kernel(
     };
     // Eight groups of four MFMAs (tile u, dim blocks 4q .. 4q+3), one group
     // of V^T reads in flight (a second one does not fit the VGPRs left).
+    // A tile's lo parts (p - bf16(p)) take the MFMAs right after its hi
+    // parts on the same fragments when some row of the wave has its big
+    // flag (per accumulator: hi 0, lo 0, hi 1, lo 1).
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
+      const bool lo = __builtin_amdgcn_ballot_w64(big[u]) != 0;  // wave-uniform
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         bf16x8_t ga[4];
         read_group(u, 4 * q, ga);
         mfma_group(phi[u], 4 * q, ga);
-      }
-    }
-    // A tile's lo parts (p - bf16(p)) in a pass of their own when some row
-    // of the wave has its big flag.
+        if (lo) {
+          bf16x8_t plo;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (__builtin_amdgcn_ballot_w64(big[u]) != 0) {  // wave-uniform
-        bf16x8_t plo;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          bf16x8_t ga[4];
-          read_group(u, 4 * q, ga);
+          for (int i = 0; i < 8; ++i)
+            plo[i] = static_cast<__bf16>(w[u][i] * fs[u] - static_cast<float>(phi[u][i]));
           mfma_group(plo, 4 * q, ga);
         }
       }
