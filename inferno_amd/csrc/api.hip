@@ -260,6 +260,12 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
   int32_t* hdr = img;
   memset(hdr, 0, sizeof(int32_t) * kHdrWords);
   int64_t off = kHdrWords;
+  // Items first, at the fixed offset the decode kernels read them from;
+  // the region is sized for the most items a plan of this shape can have.
+  static_assert(kItemsOff == kHdrWords, "items follow the header");
+  int32_t* items = img + off;
+  hdr[kHdrOffItems] = static_cast<int32_t>(off);
+  off += kItemWords * std::max<int64_t>({cap, seq_len, 1});
   hdr[kHdrOffRuns] = static_cast<int32_t>(off);
   memcpy(img + off, runs, sizeof(int32_t) * 4 * num_runs);
   off += 4 * num_runs;
@@ -275,8 +281,6 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
     }
   }
   off += seq_len;
-  int32_t* items = img + off;
-  hdr[kHdrOffItems] = static_cast<int32_t>(off);
   int64_t n_items = 0, n_units = 0, n_stripes = 0;
   int32_t mode = IFR_PLAN_SPLIT_MERGE;
   auto put_item = [&](int64_t q_row, int64_t run, int64_t start_pos,
@@ -355,7 +359,6 @@ int32_t plan_impl(int32_t* img, int64_t img_words, const int32_t* runs,
     }
     n_stripes = seq_len;
   }
-  off += n_items * kItemWords;
   hdr[kHdrOffUnits] = static_cast<int32_t>(off);
   n_units = static_cast<int64_t>(unit_buf.size() / 3);
   for (int64_t u = 0; u < n_units; ++u) {

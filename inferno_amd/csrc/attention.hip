@@ -97,7 +97,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void flash_partial_bf16_kernel(
   const int g = blockIdx.x * kDecodeWaves + wave;
   if (g >= num_kv) return;
 
-  const int32_t* item = image + image[kHdrOffItems] + blockIdx.y * kItemWords;
+  const int32_t* item = image + kItemsOff + blockIdx.y * kItemWords;
   const int q_row = item[0];
   const int start_pos = item[2];
   const int start = item[3];

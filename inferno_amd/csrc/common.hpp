@@ -35,6 +35,10 @@ enum PlanHeader : int {
 // image word offset of the run's row table.
 constexpr int kItemRowsOff = 6;
 constexpr int kItemWords = 8;
+// The items start right after the header (the planner reserves room for
+// its largest item count there), so a decode wave reaches its item in one
+// load instead of a header load followed by the item load.
+constexpr int kItemsOff = kHdrWords;
 // A merge unit: one output token row, for every q head.
 // {out_row, stripe_base, n_stripes, 0}
 constexpr int kUnitWords = 4;
